@@ -1,0 +1,251 @@
+"""Benchmark of the paged KV-cache decode path on one MI355X.
+
+A step is one decode step of the whole model's KV path: for every layer,
+append each sequence's new K/V row (f32 source rounded to f16) into its
+slot, then paged GQA decode attention over the full context. Inputs are
+resident in HBM before the timed region. Prints one JSON line.
+
+Default workload: BASELINE configs[1], Llama-3.2-1B shape (16 layers, 32 q
+heads / 8 KV heads, head_dim 64, block_size 16, 64 sequences x 2048 tokens,
+block tables a random permutation of a pool sized for exactly the live
+tokens). Other configs: --config qwen3-0.6b | gemma-3-270m | qwen2.5-0.5b.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "paged-decode attn HBM GB/s (% of peak) + decode tok/s, 1 MI355X"
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--config", default="llama-3.2-1b")
+    p.add_argument("--no-cpu", action="store_true",
+                   help="skip the CPU baseline leg")
+    p.add_argument("--cpu-seconds", type=float, default=12.0,
+                   help="wall-clock budget of the CPU baseline sample")
+    return p.parse_args()
+
+
+def build_workload(W, name):
+    c = W.CONFIGS[name]
+    if name == "llama-3.2-1b":
+        return W.uniform_batch(c, 2048)
+    if name == "qwen3-0.6b":
+        return W.uniform_batch(c, 4096)
+    if name == "gemma-3-270m":
+        return W.uniform_batch(c, 1024)
+    if name == "qwen2.5-0.5b":
+        return W.qwen25_batch()
+    if name == "smollm2-360m":
+        return W.smollm2_batch()
+    raise SystemExit(f"unknown config {name}")
+
+
+def fill_pool(torch, st, seed, scale):
+    """Writes N(0,1)*scale f16 rows into every slot of every layer through
+    the append kernel (f16 source), drawn on the device."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    bs, nkv, hd = st.block_size, st.n_kv_heads, st.head_dim
+    total = st.num_blocks * bs
+    chunk = max(1, (1 << 28) // (nkv * hd * 2))  # 256 MiB of f16 per tensor
+    for layer in range(st.n_layers):
+        for t0 in range(0, total, chunk):
+            n = min(chunk, total - t0)
+            s = torch.arange(t0, t0 + n, device="cuda", dtype=torch.int64)
+            blk = (s // bs).to(torch.int32)
+            off = (s % bs).to(torch.int32)
+            k = torch.randn((n, nkv, hd), generator=g, device="cuda",
+                            dtype=torch.float16)
+            v = torch.randn((n, nkv, hd), generator=g, device="cuda",
+                            dtype=torch.float16)
+            if scale != 1.0:
+                k.mul_(scale)
+                v.mul_(scale)
+            st.write_tokens(layer, blk, off, k, v)
+        torch.cuda.synchronize()
+
+
+def cpu_baseline(orc, W, st, db, budget_s):
+    """The oracle's restatement of rvllm's CPU decode path (append + padded
+    gather + batch_mask + gqa_attention, f32 math over the f16 cache) on the
+    host cores, one layer of the same workload, repeated within budget_s.
+    Returns the cpu_baseline dict."""
+    import torch
+    c = db.cfg
+    threads = max(1, min(16, os.cpu_count() or 1))
+    ids = torch.from_numpy(np.arange(db.num_blocks, dtype=np.int32)).cuda()
+    cache = orc.KvCache(db.num_blocks, c.block_size, c.n_kv_heads,
+                        c.head_dim, orc.F16)
+    cache.k[:] = st.read_blocks(0, 0, ids).cpu().view(torch.int16).numpy() \
+        .view(np.uint16)
+    cache.v[:] = st.read_blocks(0, 1, ids).cpu().view(torch.int16).numpy() \
+        .view(np.uint16)
+    rng = W.Rng(c.seed + 99)
+    nk = rng.normal((db.batch, c.n_kv_heads, c.head_dim))
+    nv = rng.normal((db.batch, c.n_kv_heads, c.head_dim))
+    q = rng.normal((db.batch, c.n_heads, c.head_dim))
+    idx = db.padded_tables().reshape(-1)
+    reps, t_total = 0, 0.0
+    while reps < 1 or (t_total < budget_s and reps < 50):
+        t0 = time.perf_counter()
+        orc.decode_step(cache, db.slot_block, db.slot_off, nk, nv, idx,
+                        db.max_blocks, db.ctx_lens, q, n_threads=threads)
+        t_total += time.perf_counter() - t0
+        reps += 1
+    per_layer = t_total / reps
+    layer_bytes = W.decode_bytes(db) + W.append_bytes(db.batch, c)
+    return {
+        "value": round(layer_bytes / per_layer / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"oracle decode_step (rvllm CPU path restated in C: "
+                   f"write_tokens + padded gather + batch_mask + "
+                   f"gqa_attention, f32) on layer 0 of the same workload, "
+                   f"{reps} repetitions, {per_layer * 1e3:.1f} ms/layer; "
+                   f"tok/s extrapolated to {c.n_layers} layers"),
+        "tok_per_s": round(db.batch / (per_layer * c.n_layers), 2),
+        "ms_per_layer": round(per_layer * 1e3, 3),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for {args.gpus}); the "
+              "paged KV path shards by sequence or KV head with no exchange "
+              "inside it, so run one process per GPU.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from rvllm_amd import workloads as W
+    from rvllm_amd.kv_storage import HipKvStorage
+
+    torch.cuda.set_device(0)
+    db = build_workload(W, args.config)
+    c = db.cfg
+    st = HipKvStorage(c.n_layers, db.num_blocks, c.block_size, c.n_kv_heads,
+                      c.head_dim)
+    fill_pool(torch, st, c.seed, c.value_scale)
+
+    def u32(a):
+        return torch.from_numpy(np.ascontiguousarray(a, np.uint32)
+                                .view(np.int32).copy()).cuda()
+
+    if len(db.cow_src):  # prefix sharers move onto private copies first
+        st.copy_blocks(u32(db.cow_src), u32(db.cow_dst))
+    tables = u32(db.padded_tables())
+    ctx = u32(db.ctx_lens)
+    sb, so = u32(db.slot_block), u32(db.slot_off)
+    max_ctx = int(db.ctx_lens.max())
+    g = torch.Generator(device="cuda")
+    g.manual_seed(c.seed + 7)
+    L, B = c.n_layers, db.batch
+    q = [torch.randn((B, c.n_heads, c.head_dim), generator=g, device="cuda")
+         for _ in range(L)]
+    nk = [torch.randn((B, c.n_kv_heads, c.head_dim), generator=g,
+                      device="cuda") for _ in range(L)]
+    nv = [torch.randn((B, c.n_kv_heads, c.head_dim), generator=g,
+                      device="cuda") for _ in range(L)]
+    out = [torch.empty_like(q[0]) for _ in range(L)]
+    ws = st.alloc_workspace(B, c.n_heads, max_ctx)
+    part = st.decode_partition_tokens(B, c.n_heads, max_ctx)
+
+    ev = None
+
+    def step(record=False):
+        for layer in range(L):
+            st.write_tokens(layer, sb, so, nk[layer], nv[layer])
+            if record:
+                ev[layer][0].record()
+            st.paged_decode(layer, q[layer], tables, ctx, max_ctx,
+                            out=out[layer], ws=ws)
+            if record:
+                ev[layer][1].record()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+
+    # Per-launch decode duration with HIP events on the pool's stream
+    # (torch's current stream), over a second pass of the same steps.
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)]
+          for _ in range(L)]
+    durs = []
+    for _ in range(args.steps):
+        step(record=True)
+        torch.cuda.synchronize()
+        durs.extend(ev[l][0].elapsed_time(ev[l][1]) for l in range(L))
+    dec_ms = float(np.mean(durs))
+
+    dec_bytes = W.decode_bytes(db)
+    app_bytes = W.append_bytes(B, c)
+    step_bytes = L * (dec_bytes + app_bytes)
+    achieved = dec_bytes / (dec_ms * 1e-3) / 1e9
+    res = {
+        "metric": METRIC,
+        "value": round(step_bytes / dt / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 KV, f32 accumulate",
+        "data": "synthetic: K/V ~ N(0,1)*scale f16, q ~ N(0,1) f32, seeded "
+                "random-permutation block tables",
+        "config": {
+            "workload": f"{c.name}: {c.description}; {L} layers, "
+                        f"{c.n_heads} q / {c.n_kv_heads} kv heads, head_dim "
+                        f"{c.head_dim}, block_size {c.block_size}, "
+                        f"{B} seqs, max ctx {max_ctx}",
+            "global_batch": B,
+            "seq_len": max_ctx,
+            "parallelism": "single GPU",
+            "partition_tokens": part,
+        },
+        "pct_of_peak": round(100 * step_bytes / dt / 1e9 / HBM_PEAK_GBS, 2),
+        "tok_per_s": round(B / dt, 1),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "paged_decode (partition + reduction launches)",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "algorithmic_bytes_per_launch": dec_bytes,
+            "avg_launch_ms": round(dec_ms, 5),
+        },
+    }
+    if not args.no_cpu:
+        from oracle import oracle as orc
+        res["cpu_baseline"] = cpu_baseline(orc, W, st, db, args.cpu_seconds)
+    print(json.dumps(res), flush=True)
+    st.close()
+
+
+if __name__ == "__main__":
+    main()

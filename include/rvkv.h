@@ -1,0 +1,214 @@
+/*
+ * rvkv.h - C ABI of the MI355X (gfx950) paged KV-cache hot path.
+ *
+ * Drop-in boundary for rvllm's KV storage + attention read path. Every entry
+ * point takes plain pointers and sizes; device pointers are caller-owned
+ * (hipMalloc'd, torch-allocated, anything addressable by the pool's device).
+ * A Rust `-sys` crate binds this header 1:1 (see the binding stubs shipped
+ * with the integration notes).
+ *
+ * Conventions (mirroring rvllm's CUDA backend, src/cuda/ops.rs:325-352 and
+ * src/cuda/kv_storage.rs:65-164):
+ *  - every call validates its scalar arguments BEFORE launching anything and
+ *    returns 0 or a negative RVKV_E* code; the reason is then readable from
+ *    rvkv_last_error() as "<op>: <reason>" (thread-local string);
+ *  - every call enqueues on the pool's stream and never synchronises; the
+ *    caller synchronises (rvllm: stream.synchronize() in
+ *    src/cuda/engine.rs:374);
+ *  - a pool is driven from one thread at a time (rvllm's single engine
+ *    thread, src/server/worker.rs:1-5);
+ *  - block ids and slot offsets found in device arrays are bounds-checked by
+ *    the kernels: an out-of-range id makes the kernel skip that row (append,
+ *    copy) or read zeros (gather, decode) instead of faulting.
+ *
+ * Cache layout (physical, per layer, per K/V tensor): f16
+ *   [num_blocks][n_kv_heads][block_size][head_dim]
+ * i.e. head-major inside a block, so one (block, head) tile is one contiguous
+ * block_size*head_dim*2-byte run. The LOGICAL contents are rvllm's
+ * [num_blocks, block_size, n_kv_heads, head_dim] (src/kv_storage.rs:7-13);
+ * rvkv_read_blocks / rvkv_gather expose the logical view.
+ */
+#ifndef RVKV_H
+#define RVKV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct rvkv_pool rvkv_pool;
+
+/* A hipStream_t, passed as an opaque pointer so this header needs no HIP
+ * include. NULL is the device's null stream. */
+typedef void *rvkv_stream;
+
+typedef enum {
+  RVKV_F16 = 1, /* IEEE binary16 */
+  RVKV_F32 = 2  /* IEEE binary32 */
+} rvkv_dtype;
+
+enum {
+  RVKV_OK = 0,
+  RVKV_EINVAL = -1,      /* bad argument (message says which) */
+  RVKV_EHIP = -2,        /* a HIP runtime call failed */
+  RVKV_ENOMEM = -3,      /* device allocation failed */
+  RVKV_EUNSUPPORTED = -4 /* valid but not implemented shape */
+};
+
+/* Thread-local "<op>: <reason>" of the last failing call on this thread
+ * ("" if none). Replaces the Box<dyn Error> strings of src/cuda/ops.rs. */
+const char *rvkv_last_error(void);
+
+/* ---- a1: pool ------------------------------------------------------------
+ * Replaces CudaKvStorage::new (src/cuda/kv_storage.rs:77-100) /
+ * KvStorage::new (src/kv_storage.rs:84-104): zeroed K and V storage for
+ * n_layers attention layers. One device allocation for all layers; 64-bit
+ * offsets throughout. cache_dtype must be RVKV_F16. The pool binds to the
+ * current HIP device and to `stream`. */
+int rvkv_pool_create(uint32_t n_layers, uint32_t num_blocks,
+                     uint32_t block_size, uint32_t n_kv_heads,
+                     uint32_t head_dim, rvkv_dtype cache_dtype,
+                     rvkv_stream stream, rvkv_pool **out);
+void rvkv_pool_destroy(rvkv_pool *pool);
+/* Bytes of device memory the pool holds (K+V, all layers). */
+size_t rvkv_pool_bytes(const rvkv_pool *pool);
+/* Rebinds the pool to another stream on the same device. */
+int rvkv_pool_set_stream(rvkv_pool *pool, rvkv_stream stream);
+
+/* ---- a2: KV append -------------------------------------------------------
+ * Replaces CudaKvStorage::write_tokens (src/cuda/kv_storage.rs:105-126) ->
+ * kv_write_wrapper (src/cuda/ops.rs:313-373) -> kv_write.cu, and the CPU
+ * KvStorage::write_tokens (src/kv_storage.rs:116-150).
+ * k, v: device [n_tokens, n_kv_heads, head_dim], src_dtype F32 (rounded to
+ * f16 round-to-nearest-even) or F16 (copied bit for bit).
+ * slot_block, slot_off: device u32[n_tokens], token i -> (block, offset).
+ * Slots must be distinct within one call (the reference's precondition,
+ * src/cuda/kernels/kv_write.cu:33). n_tokens == 0 is an error, as in
+ * kv_write_wrapper. */
+int rvkv_append(rvkv_pool *pool, uint32_t layer, const void *k, const void *v,
+                rvkv_dtype src_dtype, const uint32_t *slot_block,
+                const uint32_t *slot_off, uint32_t n_tokens);
+
+/* ---- a4: block-table gather ---------------------------------------------
+ * Replaces CudaKvStorage::gather (src/cuda/kv_storage.rs:132-164) ->
+ * kv_gather_wrapper (src/cuda/ops.rs:381-445) -> kv_gather.cu, and
+ * KvStorage::gather (src/kv_storage.rs:157-173).
+ * block_idx: device u32[batch*max_blocks], each sequence's block table padded
+ * to max_blocks (rvllm's GatherPlan convention, src/kv_storage.rs:59-67).
+ * out_k, out_v: device [batch, n_kv_heads, ctx_len, head_dim] of out_dtype
+ * (F32 = the reference's output type; F16 = raw cache bits).
+ * ctx_len must not exceed max_blocks*block_size. */
+int rvkv_gather(const rvkv_pool *pool, uint32_t layer,
+                const uint32_t *block_idx, uint32_t batch, uint32_t max_blocks,
+                uint32_t ctx_len, void *out_k, void *out_v,
+                rvkv_dtype out_dtype);
+
+/* ---- a5 + a6: paged GQA decode attention ---------------------------------
+ * Replaces, for q_len == 1, the chain kv_gather x2 -> attention_scores ->
+ * mask_add_broadcast -> softmax -> attention_apply
+ * (src/cuda/model.rs:528-569) and the CPU gather + batch_mask +
+ * gqa_attention (src/model.rs:346-415, 628-644).
+ * q: device f32 [batch, n_heads, head_dim]; out: device f32, same shape.
+ * block_tables: device u32 [batch, max_blocks]; ctx_lens: device u32[batch],
+ * the real context length of each sequence INCLUDING the token appended this
+ * step (rvllm's read_num_tokens). Each ctx_len must be <= max_ctx_len and
+ * <= max_blocks*block_size (larger values are clamped).
+ * Query head h reads KV head h / (n_heads / n_kv_heads).
+ * scale multiplies q.k (rvllm: 1/sqrt(head_dim)).
+ * window > 0 keeps only the last `window` keys (rvllm's sliding-window mask
+ * j + window <= offset, src/model.rs:361, with offset = ctx_len - 1);
+ * window <= 0 means no window.
+ * ws: device scratch of at least rvkv_decode_workspace_bytes(...) bytes,
+ * 256-byte aligned; contents need no initialisation.
+ * A sequence with ctx_len 0 gets an all-zero output row.
+ * Supported: head_dim in {32, 64, 128, 256}, block_size a power of two
+ * >= 512/head_dim, n_heads a multiple of n_kv_heads. */
+int rvkv_paged_decode(const rvkv_pool *pool, uint32_t layer, const float *q,
+                      const uint32_t *block_tables, const uint32_t *ctx_lens,
+                      uint32_t batch, uint32_t max_blocks, uint32_t n_heads,
+                      uint32_t max_ctx_len, float scale, int32_t window,
+                      float *out, void *ws, size_t ws_bytes);
+
+/* Workspace bytes rvkv_paged_decode needs for this batch shape. */
+size_t rvkv_decode_workspace_bytes(const rvkv_pool *pool, uint32_t batch,
+                                   uint32_t n_heads, uint32_t max_ctx_len);
+
+/* Tokens per context partition rvkv_paged_decode will use for this shape
+ * (each partition is one wavefront per (sequence, KV head)). */
+uint32_t rvkv_decode_partition_tokens(const rvkv_pool *pool, uint32_t batch,
+                                      uint32_t n_heads, uint32_t max_ctx_len);
+
+/* ---- a10: prefix-cache copy-on-write -------------------------------------
+ * No counterpart in the reference (rvllm never mutates a shared block; its
+ * only copy is the whole-cache KvStorage::clone, src/kv_storage.rs:15-33).
+ * Copies block src[i] -> dst[i] for every layer, K and V, bit for bit.
+ * src, dst: device u32[n]. dst blocks must be distinct and not among src. */
+int rvkv_copy_blocks(rvkv_pool *pool, const uint32_t *src,
+                     const uint32_t *dst, uint32_t n);
+
+/* ---- inspection (test and integration support) --------------------------
+ * Logical view of whole blocks: out is device [n, block_size, n_kv_heads,
+ * head_dim] f16 for blocks block_ids[0..n) of (layer, which: 0 = K, 1 = V).
+ * The raw-cache view rvllm's tests read (src/cuda/ops.rs:1104-1114). */
+int rvkv_read_blocks(const rvkv_pool *pool, uint32_t layer, uint32_t which,
+                     const uint32_t *block_ids, uint32_t n, void *out);
+
+/* 64-bit FNV-1a over the logical little-endian f16 bytes of each listed
+ * block of (layer, which): out device u64[n]. Lets a host compare full-size
+ * caches against a CPU model block by block. */
+int rvkv_block_checksums(const rvkv_pool *pool, uint32_t layer,
+                         uint32_t which, const uint32_t *block_ids, uint32_t n,
+                         uint64_t *out);
+
+/* ---- a8/a9/a10 host side: block manager -----------------------------------
+ * Host-only (no device memory). Stands in for the external
+ * kv-cache-scheduler 0.2.0 crate as rvllm's engine uses it
+ * (src/engine.rs:351-539): a block pool with a free list, per-sequence block
+ * tables, logical_to_physical slot mapping, refcounted prefix sharing and the
+ * copy-on-write decision before an append. */
+typedef struct rvkv_bm rvkv_bm;
+
+rvkv_bm *rvkv_bm_create(uint32_t num_blocks, uint32_t block_size);
+void rvkv_bm_destroy(rvkv_bm *bm);
+/* Free blocks (kv-cache-scheduler's pool.available()). */
+uint32_t rvkv_bm_available(const rvkv_bm *bm);
+/* Shuffles the free list with a seeded Fisher-Yates (fragmented pools). */
+void rvkv_bm_shuffle_free(rvkv_bm *bm, uint64_t seed);
+/* Adds a sequence holding n_tokens, allocating ceil(n_tokens/bs) blocks.
+ * Returns the new sequence id (>= 0) or a negative code (pool full). */
+int64_t rvkv_bm_add_seq(rvkv_bm *bm, uint32_t n_tokens);
+/* Adds a sequence whose first n_shared tokens reuse `parent`'s blocks
+ * (refcount + 1 each; a partially filled shared last block is shared too),
+ * then allocates private blocks up to n_tokens. */
+int64_t rvkv_bm_fork_seq(rvkv_bm *bm, int64_t parent, uint32_t n_shared,
+                         uint32_t n_tokens);
+/* Drops a sequence; blocks whose refcount reaches 0 return to the free list.
+ */
+int rvkv_bm_free_seq(rvkv_bm *bm, int64_t seq);
+/* Reserves the slot for the sequence's next token (position num_tokens):
+ * allocates a block at a block boundary; if the target block is shared
+ * (refcount > 1) it is replaced by a fresh private block and the pair
+ * (old, new) is reported in *cow_src / *cow_dst (else both UINT32_MAX) so
+ * the caller can enqueue rvkv_copy_blocks before the append. Writes the
+ * slot to *block, *offset. */
+int rvkv_bm_append_slot(rvkv_bm *bm, int64_t seq, uint32_t *block,
+                        uint32_t *offset, uint32_t *cow_src,
+                        uint32_t *cow_dst);
+/* logical_to_physical(pos) of rvllm's BlockTable. */
+int rvkv_bm_slot(const rvkv_bm *bm, int64_t seq, uint32_t pos,
+                 uint32_t *block, uint32_t *offset);
+uint32_t rvkv_bm_num_tokens(const rvkv_bm *bm, int64_t seq);
+uint32_t rvkv_bm_num_blocks(const rvkv_bm *bm, int64_t seq);
+uint32_t rvkv_bm_refcount(const rvkv_bm *bm, uint32_t block);
+/* Copies the sequence's block table into table[0..cap); returns its length
+ * or a negative code. */
+int rvkv_bm_table(const rvkv_bm *bm, int64_t seq, uint32_t *table,
+                  uint32_t cap);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RVKV_H */

@@ -1,0 +1,968 @@
+// rvkv.hip - MI355X (gfx950) paged KV cache: append, gather, copy-on-write
+// block copy and paged GQA decode attention, behind the C ABI of
+// include/rvkv.h. Hand-written HIP for CDNA4 (wave64, DPP, fdot2).
+//
+// Physical cache layout, per layer and per K/V tensor, f16:
+//   [num_blocks][n_kv_heads][block_size][head_dim]
+// One (block, head) tile is a contiguous block_size*head_dim run, so a
+// wavefront reading one KV head of a sequence streams whole 2 KiB+ runs
+// (bs 16, hd 64) with 128-bit lane loads. rvllm's logical layout
+// [num_blocks, block_size, n_kv_heads, head_dim] (src/kv_storage.rs:7) is
+// what gather/read_blocks expose.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/rvkv.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char *op, const char *reason) {
+  g_last_error = std::string(op) + ": " + reason;
+  return code;
+}
+
+int hip_fail(const char *op, hipError_t e) {
+  g_last_error = std::string(op) + ": " + hipGetErrorString(e);
+  return RVKV_EHIP;
+}
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ h2 as_h2(uint32_t x) {
+  return __builtin_bit_cast(h2, x);
+}
+__device__ __forceinline__ uint32_t as_u32(h2 x) {
+  return __builtin_bit_cast(uint32_t, x);
+}
+
+}  // namespace
+
+struct rvkv_pool {
+  uint32_t n_layers, num_blocks, block_size, n_kv, head_dim;
+  hipStream_t stream;
+  int device;
+  uint16_t *base;        // 2 * n_layers tensors
+  size_t tensor_elems;   // num_blocks * n_kv * block_size * head_dim
+  size_t block_elems;    // n_kv * block_size * head_dim
+
+  uint16_t *tensor(uint32_t layer, uint32_t which) const {
+    return base + ((size_t)layer * 2 + which) * tensor_elems;
+  }
+};
+
+// ---------------------------------------------------------------------------
+// a2: KV append. One thread per VW contiguous elements of one (token, head)
+// row; VW = 8 (16-byte f16 store) when head_dim % 8 == 0.
+// Replaces kv_write.cu (one thread per f32 scalar, 32-bit indices).
+// ---------------------------------------------------------------------------
+template <int VW, bool SRC_F32>
+__global__ void __launch_bounds__(256)
+    append_kernel(const void *__restrict__ k, const void *__restrict__ v,
+                  const uint32_t *__restrict__ slot_block,
+                  const uint32_t *__restrict__ slot_off,
+                  uint16_t *__restrict__ kc, uint16_t *__restrict__ vc,
+                  uint32_t n_tokens, uint32_t n_kv, uint32_t hd, uint32_t bs,
+                  uint32_t num_blocks) {
+  const uint32_t vec_per_row = hd / VW;
+  const uint32_t per_token = n_kv * vec_per_row;
+  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (uint64_t)n_tokens * per_token) return;
+  const uint32_t token = (uint32_t)(i / per_token);
+  const uint32_t j = (uint32_t)(i - (uint64_t)token * per_token);
+  const uint32_t head = j / vec_per_row;
+  const uint32_t d = (j - head * vec_per_row) * VW;
+  const uint32_t blk = slot_block[token];
+  const uint32_t off = slot_off[token];
+  if (blk >= num_blocks || off >= bs) return;  // out-of-range slot: skipped
+  const size_t src = (size_t)token * n_kv * hd + (size_t)head * hd + d;
+  const size_t dst =
+      (((size_t)blk * n_kv + head) * bs + off) * (size_t)hd + d;
+  if constexpr (VW == 8) {
+    uint4 ko, vo;
+    if constexpr (SRC_F32) {
+      const float4 *ks = reinterpret_cast<const float4 *>(
+          static_cast<const float *>(k) + src);
+      const float4 *vs = reinterpret_cast<const float4 *>(
+          static_cast<const float *>(v) + src);
+      float4 k0 = ks[0], k1 = ks[1], v0 = vs[0], v1 = vs[1];
+      // f32 -> f16 round-to-nearest-even (v_cvt_f16_f32, default mode).
+      ko.x = as_u32(h2{(_Float16)k0.x, (_Float16)k0.y});
+      ko.y = as_u32(h2{(_Float16)k0.z, (_Float16)k0.w});
+      ko.z = as_u32(h2{(_Float16)k1.x, (_Float16)k1.y});
+      ko.w = as_u32(h2{(_Float16)k1.z, (_Float16)k1.w});
+      vo.x = as_u32(h2{(_Float16)v0.x, (_Float16)v0.y});
+      vo.y = as_u32(h2{(_Float16)v0.z, (_Float16)v0.w});
+      vo.z = as_u32(h2{(_Float16)v1.x, (_Float16)v1.y});
+      vo.w = as_u32(h2{(_Float16)v1.z, (_Float16)v1.w});
+    } else {
+      ko = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(k) +
+                                            src);
+      vo = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(v) +
+                                            src);
+    }
+    *reinterpret_cast<uint4 *>(kc + dst) = ko;
+    *reinterpret_cast<uint4 *>(vc + dst) = vo;
+  } else {
+    if constexpr (SRC_F32) {
+      kc[dst] = __builtin_bit_cast(
+          uint16_t, (_Float16)(static_cast<const float *>(k)[src]));
+      vc[dst] = __builtin_bit_cast(
+          uint16_t, (_Float16)(static_cast<const float *>(v)[src]));
+    } else {
+      kc[dst] = static_cast<const uint16_t *>(k)[src];
+      vc[dst] = static_cast<const uint16_t *>(v)[src];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// a4: block-table gather into rvllm's padded [batch, n_kv, ctx_len, hd].
+// Replaces kv_gather.cu. One thread per VW output elements.
+// ---------------------------------------------------------------------------
+template <int VW, bool OUT_F32>
+__global__ void __launch_bounds__(256)
+    gather_kernel(const uint16_t *__restrict__ kc,
+                  const uint16_t *__restrict__ vc,
+                  const uint32_t *__restrict__ block_idx, void *__restrict__ ok,
+                  void *__restrict__ ov, uint32_t batch, uint32_t max_blocks,
+                  uint32_t ctx_len, uint32_t n_kv, uint32_t hd, uint32_t bs,
+                  uint32_t num_blocks) {
+  const uint32_t vec_per_row = hd / VW;
+  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const uint64_t rows = (uint64_t)batch * n_kv * ctx_len;
+  if (i >= rows * vec_per_row) return;
+  const uint64_t row = i / vec_per_row;  // (b, head, pos)
+  const uint32_t d = (uint32_t)(i - row * vec_per_row) * VW;
+  const uint32_t pos = (uint32_t)(row % ctx_len);
+  const uint64_t bh = row / ctx_len;
+  const uint32_t head = (uint32_t)(bh % n_kv);
+  const uint32_t b = (uint32_t)(bh / n_kv);
+  const uint32_t blk = block_idx[(size_t)b * max_blocks + pos / bs];
+  const size_t dst = row * hd + d;
+  const bool ok_blk = blk < num_blocks;
+  const size_t src =
+      (((size_t)(ok_blk ? blk : 0) * n_kv + head) * bs + pos % bs) * hd + d;
+  if constexpr (VW == 8) {
+    uint4 kr = ok_blk ? *reinterpret_cast<const uint4 *>(kc + src)
+                      : make_uint4(0, 0, 0, 0);
+    uint4 vr = ok_blk ? *reinterpret_cast<const uint4 *>(vc + src)
+                      : make_uint4(0, 0, 0, 0);
+    if constexpr (OUT_F32) {
+      float *kf = static_cast<float *>(ok) + dst;
+      float *vf = static_cast<float *>(ov) + dst;
+      const uint32_t kw[4] = {kr.x, kr.y, kr.z, kr.w};
+      const uint32_t vw[4] = {vr.x, vr.y, vr.z, vr.w};
+      float ko[8], vo[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        h2 kh = as_h2(kw[e]), vh = as_h2(vw[e]);
+        ko[2 * e] = (float)kh.x;
+        ko[2 * e + 1] = (float)kh.y;
+        vo[2 * e] = (float)vh.x;
+        vo[2 * e + 1] = (float)vh.y;
+      }
+      reinterpret_cast<float4 *>(kf)[0] = make_float4(ko[0], ko[1], ko[2], ko[3]);
+      reinterpret_cast<float4 *>(kf)[1] = make_float4(ko[4], ko[5], ko[6], ko[7]);
+      reinterpret_cast<float4 *>(vf)[0] = make_float4(vo[0], vo[1], vo[2], vo[3]);
+      reinterpret_cast<float4 *>(vf)[1] = make_float4(vo[4], vo[5], vo[6], vo[7]);
+    } else {
+      *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(ok) + dst) = kr;
+      *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(ov) + dst) = vr;
+    }
+  } else {
+    uint16_t kr = ok_blk ? kc[src] : 0, vr = ok_blk ? vc[src] : 0;
+    if constexpr (OUT_F32) {
+      static_cast<float *>(ok)[dst] = (float)__builtin_bit_cast(_Float16, kr);
+      static_cast<float *>(ov)[dst] = (float)__builtin_bit_cast(_Float16, vr);
+    } else {
+      static_cast<uint16_t *>(ok)[dst] = kr;
+      static_cast<uint16_t *>(ov)[dst] = vr;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// a10: copy-on-write block copy, every layer, K and V. grid.y = pair,
+// grid.z = tensor (2 * n_layers); threads stride over the block's 16-byte
+// (or 2-byte) words.
+// ---------------------------------------------------------------------------
+template <typename W>
+__global__ void __launch_bounds__(256)
+    copy_blocks_kernel(uint16_t *__restrict__ base,
+                       const uint32_t *__restrict__ src,
+                       const uint32_t *__restrict__ dst, size_t tensor_elems,
+                       size_t block_elems, uint32_t num_blocks) {
+  const uint32_t s = src[blockIdx.y], d = dst[blockIdx.y];
+  if (s >= num_blocks || d >= num_blocks) return;
+  uint16_t *t = base + (size_t)blockIdx.z * tensor_elems;
+  const W *from = reinterpret_cast<const W *>(t + (size_t)s * block_elems);
+  W *to = reinterpret_cast<W *>(t + (size_t)d * block_elems);
+  const size_t words = block_elems * 2 / sizeof(W);
+  for (size_t w = (size_t)blockIdx.x * blockDim.x + threadIdx.x; w < words;
+       w += (size_t)gridDim.x * blockDim.x)
+    to[w] = from[w];
+}
+
+// Logical [n, bs, n_kv, hd] view of listed blocks (test/inspection path).
+__global__ void __launch_bounds__(256)
+    read_blocks_kernel(const uint16_t *__restrict__ t,
+                       const uint32_t *__restrict__ ids, uint32_t n,
+                       uint16_t *__restrict__ out, uint32_t bs, uint32_t n_kv,
+                       uint32_t hd, uint32_t num_blocks) {
+  const size_t per_block = (size_t)bs * n_kv * hd;
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= per_block * n) return;
+  const uint32_t bi = (uint32_t)(i / per_block);
+  const size_t r = i - (size_t)bi * per_block;  // (slot, head, d) logical
+  const uint32_t d = (uint32_t)(r % hd);
+  const uint32_t head = (uint32_t)((r / hd) % n_kv);
+  const uint32_t slot = (uint32_t)(r / ((size_t)hd * n_kv));
+  const uint32_t blk = ids[bi];
+  out[i] = blk < num_blocks
+               ? t[(((size_t)blk * n_kv + head) * bs + slot) * hd + d]
+               : (uint16_t)0;
+}
+
+// FNV-1a 64 over the logical little-endian bytes of each listed block.
+__global__ void __launch_bounds__(64)
+    checksum_kernel(const uint16_t *__restrict__ t,
+                    const uint32_t *__restrict__ ids, uint32_t n,
+                    uint64_t *__restrict__ out, uint32_t bs, uint32_t n_kv,
+                    uint32_t hd, uint32_t num_blocks) {
+  const uint32_t bi = blockIdx.x * blockDim.x + threadIdx.x;
+  if (bi >= n) return;
+  const uint32_t blk = ids[bi];
+  uint64_t h = 0xcbf29ce484222325ull;
+  if (blk < num_blocks) {
+    for (uint32_t slot = 0; slot < bs; ++slot)
+      for (uint32_t head = 0; head < n_kv; ++head) {
+        const uint16_t *row =
+            t + (((size_t)blk * n_kv + head) * bs + slot) * hd;
+        for (uint32_t d = 0; d < hd; ++d) {
+          h = (h ^ (row[d] & 0xffu)) * 0x100000001b3ull;
+          h = (h ^ (row[d] >> 8)) * 0x100000001b3ull;
+        }
+      }
+  }
+  out[bi] = h;
+}
+
+// ---------------------------------------------------------------------------
+// a5 + a6: paged GQA decode attention.
+//
+// Work unit: one wavefront per (sequence, KV head, query sub-group of <= 8
+// heads, context partition of P tokens). The wave streams its partition's
+// K and V straight through the block table:
+//   * a K/V row of head_dim f16 is R = head_dim/8 lanes x 16 bytes, so one
+//     wave-wide load covers RPL = 64/R consecutive tokens of ONE block
+//     (block_size is a power of two >= RPL): the block id is wave-uniform
+//     and lives in an SGPR, every lane issues one 128-bit load;
+//   * each group of R lanes ("row group") owns every RPL-th token and keeps
+//     its own online-softmax state (running max m, sum l, acc[8] per head)
+//     in registers, so the P.V update needs no cross-lane traffic;
+//   * q.k: v_dot2_f32_f16 (f16 products, f32 accumulate) over the lane's 8
+//     elements, then a DPP butterfly (quad_perm, row_half_mirror,
+//     row_mirror) sums the R lanes of the row;
+//   * P.V: probabilities rounded to f16 (the running sum l uses the same
+//     rounded values, so the normalisation stays consistent), paired over
+//     two tokens and fed to v_dot2_f32_f16 against V re-paired with
+//     v_perm_b32;
+//   * at the end the RPL row groups merge with cross-lane shuffles and the
+//     partial (m, l, acc) goes to the workspace, or - when the whole
+//     context fits one partition - the normalised output goes straight to
+//     `out`.
+// Scores are kept in the log2 domain (q pre-scaled by scale*log2(e)) and
+// exponentiated with v_exp_f32.
+// A second kernel merges the partitions of each (sequence, query head).
+// ---------------------------------------------------------------------------
+struct DecodeArgs {
+  const uint16_t *kc;
+  const uint16_t *vc;
+  const float *q;
+  float *out;
+  const uint32_t *tables;
+  const uint32_t *ctx_lens;
+  float *ws_acc;  // [batch][n_heads][n_parts][hd]
+  float *ws_ml;   // [batch][n_heads][n_parts][2]
+  uint64_t block_stride;  // elements per block (all heads)
+  uint32_t head_stride;   // elements per (block, head) tile
+  uint32_t max_blocks, num_blocks, n_kv, n_heads, group, n_sub;
+  uint32_t bs_log2, part_tokens, n_parts, ctx_cap;
+  float qscale;
+  int32_t window;
+  int32_t direct;
+};
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL,
+                                         0xF, 0xF, false));
+}
+
+// Sum over the R lanes of a row group (R in {4, 8, 16, 32}); every lane of
+// the group ends with the total.
+template <int R>
+__device__ __forceinline__ float row_group_sum(float x) {
+  x += dpp<0xB1>(x);  // quad_perm [1,0,3,2]: lane ^ 1
+  x += dpp<0x4E>(x);  // quad_perm [2,3,0,1]: lane ^ 2
+  if constexpr (R >= 8) x += dpp<0x141>(x);  // row_half_mirror: 8-lane total
+  if constexpr (R >= 16) x += dpp<0x140>(x);  // row_mirror: 16-lane total
+  if constexpr (R >= 32)
+    x += __builtin_bit_cast(
+        float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x),
+                                           0x401F));  // lane ^ 16
+  return x;
+}
+
+constexpr float kNegBig = -1.0e30f;  // finite "minus infinity" for m
+
+template <int HD, int GT, int U>
+__global__ void __launch_bounds__(64) decode_part_kernel(DecodeArgs a) {
+  constexpr int R = HD / 8;      // lanes per K/V row
+  constexpr int RPL = 64 / R;    // rows (tokens) per wave-wide load
+  constexpr int TC = U * RPL;    // tokens per chunk
+  static_assert(U % 2 == 0, "tokens are paired for the P.V dot2");
+
+  const int lane = threadIdx.x;
+  const int rg = lane / R;
+  const int c = lane % R;
+  const uint32_t part = blockIdx.x;
+  const uint32_t kvh = blockIdx.y / a.n_sub;
+  const uint32_t sub = blockIdx.y - kvh * a.n_sub;
+  const uint32_t b = blockIdx.z;
+  const uint32_t h0 = kvh * a.group + sub * GT;
+  const uint32_t ng = min((uint32_t)GT, a.group - sub * GT);
+
+  uint32_t ctx = a.ctx_lens[b];
+  ctx = min(ctx, a.ctx_cap);
+  const uint32_t lo =
+      (a.window > 0 && ctx > (uint32_t)a.window) ? ctx - (uint32_t)a.window : 0;
+  const uint32_t t0 = part * a.part_tokens;
+  const uint32_t t1 = min(t0 + a.part_tokens, ctx);
+
+  if (t0 >= t1 || t1 <= lo) {
+    if (a.direct) {
+      // Only partition 0 exists; an empty context gives a zero row.
+      if (rg == 0)
+        for (uint32_t g = 0; g < ng; ++g) {
+          float4 *o = reinterpret_cast<float4 *>(
+              a.out + ((size_t)b * a.n_heads + h0 + g) * HD + c * 8);
+          o[0] = make_float4(0.f, 0.f, 0.f, 0.f);
+          o[1] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    } else if (t0 < ctx && lane == 0) {
+      for (uint32_t g = 0; g < ng; ++g) {
+        size_t idx = ((size_t)b * a.n_heads + h0 + g) * a.n_parts + part;
+        a.ws_ml[idx * 2] = kNegBig;
+        a.ws_ml[idx * 2 + 1] = 0.f;
+      }
+    }
+    return;
+  }
+
+  // q for the GT heads, 8 elements per lane, pre-scaled, as f16 pairs.
+  h2 qh[GT][4];
+#pragma unroll
+  for (int g = 0; g < GT; ++g) {
+    const uint32_t hg = h0 + ((uint32_t)g < ng ? g : 0);
+    const float4 *qp = reinterpret_cast<const float4 *>(
+        a.q + ((size_t)b * a.n_heads + hg) * HD + c * 8);
+    float4 x0 = qp[0], x1 = qp[1];
+    qh[g][0] = h2{(_Float16)(x0.x * a.qscale), (_Float16)(x0.y * a.qscale)};
+    qh[g][1] = h2{(_Float16)(x0.z * a.qscale), (_Float16)(x0.w * a.qscale)};
+    qh[g][2] = h2{(_Float16)(x1.x * a.qscale), (_Float16)(x1.y * a.qscale)};
+    qh[g][3] = h2{(_Float16)(x1.z * a.qscale), (_Float16)(x1.w * a.qscale)};
+  }
+
+  float m[GT], l[GT], acc[GT][8];
+#pragma unroll
+  for (int g = 0; g < GT; ++g) {
+    m[g] = kNegBig;
+    l[g] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
+  }
+
+  const uint32_t bs_mask = (1u << a.bs_log2) - 1u;
+  const uint32_t last_blk = (ctx - 1) >> a.bs_log2;
+  const uint32_t *table = a.tables + (size_t)b * a.max_blocks;
+  const size_t head_off = (size_t)kvh * a.head_stride + c * 8;
+  const uint32_t start = max(t0, lo & ~(uint32_t)(RPL - 1));
+
+  // Block ids of the next chunk are fetched (scalar loads) one chunk ahead,
+  // so the K/V loads of a chunk never wait on the block table.
+  uint32_t nblk[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    nblk[u] = table[min((start + u * RPL) >> a.bs_log2, last_blk)];
+
+  for (uint32_t ch = start; ch < t1; ch += TC) {
+    uint4 kr[U], vr[U];
+    bool okb[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t tb = ch + u * RPL;  // first token of this load (uniform)
+      okb[u] = nblk[u] < a.num_blocks;
+      const uint32_t blk = okb[u] ? nblk[u] : 0;
+      const size_t off = (size_t)blk * a.block_stride + head_off +
+                         (size_t)((tb & bs_mask) + rg) * HD;
+      kr[u] = *reinterpret_cast<const uint4 *>(a.kc + off);
+      vr[u] = *reinterpret_cast<const uint4 *>(a.vc + off);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      nblk[u] = table[min((ch + TC + u * RPL) >> a.bs_log2, last_blk)];
+
+    float s[U][GT];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t tok = ch + u * RPL + rg;
+      const bool valid = okb[u] && tok >= lo && tok < t1;
+#pragma unroll
+      for (int g = 0; g < GT; ++g) {
+        float d = __builtin_amdgcn_fdot2(qh[g][0], as_h2(kr[u].x), 0.f, false);
+        d = __builtin_amdgcn_fdot2(qh[g][1], as_h2(kr[u].y), d, false);
+        d = __builtin_amdgcn_fdot2(qh[g][2], as_h2(kr[u].z), d, false);
+        d = __builtin_amdgcn_fdot2(qh[g][3], as_h2(kr[u].w), d, false);
+        d = row_group_sum<R>(d);
+        s[u][g] = valid ? d : -__builtin_inff();
+      }
+    }
+
+    h2 pp[U / 2][GT];  // f16 probabilities, paired over tokens (u, u+1)
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+      float mx = m[g];
+#pragma unroll
+      for (int u = 0; u < U; ++u) mx = fmaxf(mx, s[u][g]);
+      const float corr = __builtin_amdgcn_exp2f(m[g] - mx);
+      m[g] = mx;
+      float lsum = l[g] * corr;
+#pragma unroll
+      for (int u = 0; u < U; u += 2) {
+        const _Float16 p0 = (_Float16)__builtin_amdgcn_exp2f(s[u][g] - mx);
+        const _Float16 p1 = (_Float16)__builtin_amdgcn_exp2f(s[u + 1][g] - mx);
+        lsum += (float)p0 + (float)p1;
+        pp[u / 2][g] = h2{p0, p1};
+      }
+      l[g] = lsum;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[g][e] *= corr;
+    }
+
+#pragma unroll
+    for (int u = 0; u < U; u += 2) {
+      const uint32_t a0[4] = {vr[u].x, vr[u].y, vr[u].z, vr[u].w};
+      const uint32_t a1[4] = {vr[u + 1].x, vr[u + 1].y, vr[u + 1].z,
+                              vr[u + 1].w};
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        // (V[u][2w], V[u+1][2w]) and (V[u][2w+1], V[u+1][2w+1])
+        const h2 lo2 = as_h2(__builtin_amdgcn_perm(a1[w], a0[w], 0x05040100u));
+        const h2 hi2 = as_h2(__builtin_amdgcn_perm(a1[w], a0[w], 0x07060302u));
+#pragma unroll
+        for (int g = 0; g < GT; ++g) {
+          acc[g][2 * w] =
+              __builtin_amdgcn_fdot2(pp[u / 2][g], lo2, acc[g][2 * w], false);
+          acc[g][2 * w + 1] = __builtin_amdgcn_fdot2(pp[u / 2][g], hi2,
+                                                     acc[g][2 * w + 1], false);
+        }
+      }
+    }
+  }
+
+  // Merge the RPL row groups of the wave (lanes c, c+R, c+2R, ...).
+#pragma unroll
+  for (int g = 0; g < GT; ++g) {
+#pragma unroll
+    for (int off = R; off < 64; off <<= 1) {
+      const float mo = __shfl_xor(m[g], off);
+      const float lo_ = __shfl_xor(l[g], off);
+      const float mx = fmaxf(m[g], mo);
+      const float ws = __builtin_amdgcn_exp2f(m[g] - mx);
+      const float wo = __builtin_amdgcn_exp2f(mo - mx);
+      l[g] = l[g] * ws + lo_ * wo;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float ao = __shfl_xor(acc[g][e], off);
+        acc[g][e] = acc[g][e] * ws + ao * wo;
+      }
+      m[g] = mx;
+    }
+  }
+
+  if (rg != 0) return;
+#pragma unroll
+  for (int g = 0; g < GT; ++g) {
+    if ((uint32_t)g >= ng) break;
+    const size_t hrow = (size_t)b * a.n_heads + h0 + g;
+    if (a.direct) {
+      const float inv = 1.0f / l[g];
+      float4 *o = reinterpret_cast<float4 *>(a.out + hrow * HD + c * 8);
+      o[0] = make_float4(acc[g][0] * inv, acc[g][1] * inv, acc[g][2] * inv,
+                         acc[g][3] * inv);
+      o[1] = make_float4(acc[g][4] * inv, acc[g][5] * inv, acc[g][6] * inv,
+                         acc[g][7] * inv);
+    } else {
+      const size_t idx = hrow * a.n_parts + part;
+      float4 *o = reinterpret_cast<float4 *>(a.ws_acc + idx * HD + c * 8);
+      o[0] = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
+      o[1] = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
+      if (c == 0) {
+        a.ws_ml[idx * 2] = m[g];
+        a.ws_ml[idx * 2 + 1] = l[g];
+      }
+    }
+  }
+}
+
+// Reduction pass: one wave per (sequence, query head) merges the written
+// partitions: M = max m_i, out = sum_i 2^(m_i - M) acc_i / sum_i 2^(m_i - M)
+// l_i. Partitions that saw no valid key carry l = 0 and are skipped.
+template <int HD>
+__global__ void __launch_bounds__(64) decode_reduce_kernel(DecodeArgs a) {
+  constexpr int EPL = HD / 64 > 0 ? HD / 64 : 1;  // elements per lane
+  const uint32_t h = blockIdx.x, b = blockIdx.y;
+  const int lane = threadIdx.x;
+  const uint32_t ctx = min(a.ctx_lens[b], a.ctx_cap);
+  const uint32_t np = (ctx + a.part_tokens - 1) / a.part_tokens;
+  const size_t hrow = (size_t)b * a.n_heads + h;
+  float acc[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
+  float M = kNegBig, L = 0.f;
+  for (uint32_t p = 0; p < np; ++p) {
+    const size_t idx = hrow * a.n_parts + p;
+    const float mp = a.ws_ml[idx * 2], lp = a.ws_ml[idx * 2 + 1];
+    if (lp == 0.f) continue;
+    const float mx = fmaxf(M, mp);
+    const float w_old = __builtin_amdgcn_exp2f(M - mx);
+    const float w_new = __builtin_amdgcn_exp2f(mp - mx);
+    L = L * w_old + lp * w_new;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      const int d = lane * EPL + e;
+      const float x = d < HD ? a.ws_acc[idx * HD + d] : 0.f;
+      acc[e] = acc[e] * w_old + x * w_new;
+    }
+    M = mx;
+  }
+  const float inv = L > 0.f ? 1.0f / L : 0.f;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    const int d = lane * EPL + e;
+    if (d < HD) a.out[hrow * HD + d] = acc[e] * inv;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr int kSupportedHd[] = {32, 64, 128, 256};
+
+bool hd_supported(uint32_t hd) {
+  for (int x : kSupportedHd)
+    if ((uint32_t)x == hd) return true;
+  return false;
+}
+
+uint32_t ilog2(uint32_t x) {
+  uint32_t r = 0;
+  while ((1u << r) < x) ++r;
+  return r;
+}
+
+uint32_t div_up(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
+
+// Query heads one wave serves: group split into sub-groups of <= 8.
+void subgroups(uint32_t group, uint32_t *n_sub, uint32_t *gt) {
+  *n_sub = div_up(group, 8);
+  *gt = div_up(group, *n_sub);
+}
+
+// Tokens per context partition: the smallest power of two >= 256 for which
+// the grid has at most ~8192 partition waves (32 per CU on 256 CUs), so long
+// contexts keep enough waves in flight without a large reduction.
+uint32_t partition_tokens(const rvkv_pool *p, uint32_t batch, uint32_t n_heads,
+                          uint32_t max_ctx) {
+  uint32_t group = n_heads / (p->n_kv ? p->n_kv : 1);
+  uint32_t n_sub, gt;
+  subgroups(group ? group : 1, &n_sub, &gt);
+  const uint64_t pairs = (uint64_t)batch * p->n_kv * n_sub;
+  uint32_t P = 256;
+  while (P < 8192 && pairs * div_up(max_ctx ? max_ctx : 1, P) > 8192) P *= 2;
+  return P;
+}
+
+struct WsLayout {
+  size_t acc_off, ml_off, bytes;
+  uint32_t n_parts;
+};
+
+WsLayout ws_layout(const rvkv_pool *p, uint32_t batch, uint32_t n_heads,
+                   uint32_t max_ctx) {
+  WsLayout w{};
+  const uint32_t P = partition_tokens(p, batch, n_heads, max_ctx);
+  w.n_parts = div_up(max_ctx ? max_ctx : 1, P);
+  if (w.n_parts <= 1) return w;  // direct write, no workspace
+  const size_t slots = (size_t)batch * n_heads * w.n_parts;
+  w.acc_off = 0;
+  w.ml_off = (slots * p->head_dim * 4 + 255) & ~(size_t)255;
+  w.bytes = w.ml_off + ((slots * 2 * 4 + 255) & ~(size_t)255);
+  return w;
+}
+
+template <int HD, int GT>
+void launch_decode(const DecodeArgs &a, dim3 grid, hipStream_t st) {
+  constexpr int U = GT <= 4 ? 8 : 4;
+  hipLaunchKernelGGL((decode_part_kernel<HD, GT, U>), grid, dim3(64), 0, st, a);
+}
+
+template <int HD>
+void dispatch_gt(uint32_t gt, const DecodeArgs &a, dim3 grid, hipStream_t st) {
+  switch (gt) {
+    case 1: launch_decode<HD, 1>(a, grid, st); break;
+    case 2: launch_decode<HD, 2>(a, grid, st); break;
+    case 3: launch_decode<HD, 3>(a, grid, st); break;
+    case 4: launch_decode<HD, 4>(a, grid, st); break;
+    case 5: launch_decode<HD, 5>(a, grid, st); break;
+    case 6: launch_decode<HD, 6>(a, grid, st); break;
+    case 7: launch_decode<HD, 7>(a, grid, st); break;
+    default: launch_decode<HD, 8>(a, grid, st); break;
+  }
+}
+
+uint32_t grid_1d(uint64_t threads, uint32_t block) {
+  return (uint32_t)((threads + block - 1) / block);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *rvkv_last_error(void) { return g_last_error.c_str(); }
+
+int rvkv_pool_create(uint32_t n_layers, uint32_t num_blocks,
+                     uint32_t block_size, uint32_t n_kv_heads,
+                     uint32_t head_dim, rvkv_dtype cache_dtype,
+                     rvkv_stream stream, rvkv_pool **out) {
+  const char *op = "pool_create";
+  if (!out) return fail(RVKV_EINVAL, op, "out is NULL");
+  *out = nullptr;
+  if (n_layers == 0 || num_blocks == 0 || block_size == 0 || n_kv_heads == 0 ||
+      head_dim == 0)
+    return fail(RVKV_EINVAL, op,
+                "n_layers/num_blocks/block_size/n_kv_heads/head_dim must be "
+                "positive");
+  if (cache_dtype != RVKV_F16)
+    return fail(RVKV_EUNSUPPORTED, op, "only an f16 cache is supported");
+  rvkv_pool *p = new rvkv_pool();
+  p->n_layers = n_layers;
+  p->num_blocks = num_blocks;
+  p->block_size = block_size;
+  p->n_kv = n_kv_heads;
+  p->head_dim = head_dim;
+  p->stream = static_cast<hipStream_t>(stream);
+  p->block_elems = (size_t)n_kv_heads * block_size * head_dim;
+  p->tensor_elems = p->block_elems * num_blocks;
+  hipError_t e = hipGetDevice(&p->device);
+  if (e != hipSuccess) {
+    delete p;
+    return hip_fail(op, e);
+  }
+  const size_t bytes = p->tensor_elems * 2 * 2 * n_layers;
+  e = hipMalloc(&p->base, bytes);
+  if (e != hipSuccess) {
+    delete p;
+    (void)hipGetLastError();
+    return fail(RVKV_ENOMEM, op, "hipMalloc of the pool failed");
+  }
+  e = hipMemsetAsync(p->base, 0, bytes, p->stream);
+  if (e != hipSuccess) {
+    (void)hipFree(p->base);
+    delete p;
+    return hip_fail(op, e);
+  }
+  *out = p;
+  return RVKV_OK;
+}
+
+void rvkv_pool_destroy(rvkv_pool *pool) {
+  if (!pool) return;
+  (void)hipStreamSynchronize(pool->stream);
+  (void)hipFree(pool->base);
+  delete pool;
+}
+
+size_t rvkv_pool_bytes(const rvkv_pool *pool) {
+  return pool ? pool->tensor_elems * 4 * pool->n_layers : 0;
+}
+
+int rvkv_pool_set_stream(rvkv_pool *pool, rvkv_stream stream) {
+  if (!pool) return fail(RVKV_EINVAL, "pool_set_stream", "pool is NULL");
+  pool->stream = static_cast<hipStream_t>(stream);
+  return RVKV_OK;
+}
+
+int rvkv_append(rvkv_pool *pool, uint32_t layer, const void *k, const void *v,
+                rvkv_dtype src_dtype, const uint32_t *slot_block,
+                const uint32_t *slot_off, uint32_t n_tokens) {
+  const char *op = "kv_write";
+  if (!pool) return fail(RVKV_EINVAL, op, "pool is NULL");
+  if (layer >= pool->n_layers)
+    return fail(RVKV_EINVAL, op, "layer out of range");
+  if (n_tokens == 0) return fail(RVKV_EINVAL, op, "k/v len is 0");
+  if (!k || !v || !slot_block || !slot_off)
+    return fail(RVKV_EINVAL, op, "NULL k/v/block_ids/offsets");
+  if (src_dtype != RVKV_F16 && src_dtype != RVKV_F32)
+    return fail(RVKV_EINVAL, op, "src dtype must be F16 or F32");
+  const uint32_t hd = pool->head_dim;
+  const bool v8 = hd % 8 == 0;
+  if (v8 && src_dtype == RVKV_F32 &&
+      ((uintptr_t)k % 16 || (uintptr_t)v % 16))
+    return fail(RVKV_EINVAL, op, "f32 k/v must be 16-byte aligned");
+  if (v8 && src_dtype == RVKV_F16 && ((uintptr_t)k % 16 || (uintptr_t)v % 16))
+    return fail(RVKV_EINVAL, op, "f16 k/v must be 16-byte aligned");
+  const uint64_t threads = (uint64_t)n_tokens * pool->n_kv * (v8 ? hd / 8 : hd);
+  const dim3 grid(grid_1d(threads, 256));
+  uint16_t *kc = pool->tensor(layer, 0), *vc = pool->tensor(layer, 1);
+  if (v8) {
+    if (src_dtype == RVKV_F32)
+      hipLaunchKernelGGL((append_kernel<8, true>), grid, dim3(256), 0,
+                         pool->stream, k, v, slot_block, slot_off, kc, vc,
+                         n_tokens, pool->n_kv, hd, pool->block_size,
+                         pool->num_blocks);
+    else
+      hipLaunchKernelGGL((append_kernel<8, false>), grid, dim3(256), 0,
+                         pool->stream, k, v, slot_block, slot_off, kc, vc,
+                         n_tokens, pool->n_kv, hd, pool->block_size,
+                         pool->num_blocks);
+  } else {
+    if (src_dtype == RVKV_F32)
+      hipLaunchKernelGGL((append_kernel<1, true>), grid, dim3(256), 0,
+                         pool->stream, k, v, slot_block, slot_off, kc, vc,
+                         n_tokens, pool->n_kv, hd, pool->block_size,
+                         pool->num_blocks);
+    else
+      hipLaunchKernelGGL((append_kernel<1, false>), grid, dim3(256), 0,
+                         pool->stream, k, v, slot_block, slot_off, kc, vc,
+                         n_tokens, pool->n_kv, hd, pool->block_size,
+                         pool->num_blocks);
+  }
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? RVKV_OK : hip_fail(op, e);
+}
+
+int rvkv_gather(const rvkv_pool *pool, uint32_t layer,
+                const uint32_t *block_idx, uint32_t batch, uint32_t max_blocks,
+                uint32_t ctx_len, void *out_k, void *out_v,
+                rvkv_dtype out_dtype) {
+  const char *op = "kv_gather";
+  if (!pool) return fail(RVKV_EINVAL, op, "pool is NULL");
+  if (layer >= pool->n_layers)
+    return fail(RVKV_EINVAL, op, "layer out of range");
+  if (batch == 0 || max_blocks == 0 || ctx_len == 0)
+    return fail(RVKV_EINVAL, op,
+                "batch/max_blocks/ctx_len/block_size/n_kv_heads/head_dim must "
+                "be positive");
+  if ((uint64_t)ctx_len > (uint64_t)max_blocks * pool->block_size)
+    return fail(RVKV_EINVAL, op,
+                "ctx_len must not exceed max_blocks * block_size");
+  if (!block_idx || !out_k || !out_v)
+    return fail(RVKV_EINVAL, op, "NULL block_idx/out_k/out_v");
+  if (out_dtype != RVKV_F16 && out_dtype != RVKV_F32)
+    return fail(RVKV_EINVAL, op, "out dtype must be F16 or F32");
+  const uint32_t hd = pool->head_dim;
+  const bool v8 = hd % 8 == 0 && (uintptr_t)out_k % 16 == 0 &&
+                  (uintptr_t)out_v % 16 == 0;
+  const uint64_t rows = (uint64_t)batch * pool->n_kv * ctx_len;
+  const dim3 grid(grid_1d(rows * (v8 ? hd / 8 : hd), 256));
+  const uint16_t *kc = pool->tensor(layer, 0), *vc = pool->tensor(layer, 1);
+#define RVKV_GATHER(VW, F32)                                                  \
+  hipLaunchKernelGGL((gather_kernel<VW, F32>), grid, dim3(256), 0,            \
+                     pool->stream, kc, vc, block_idx, out_k, out_v, batch,    \
+                     max_blocks, ctx_len, pool->n_kv, hd, pool->block_size,   \
+                     pool->num_blocks)
+  if (v8) {
+    if (out_dtype == RVKV_F32) RVKV_GATHER(8, true);
+    else RVKV_GATHER(8, false);
+  } else {
+    if (out_dtype == RVKV_F32) RVKV_GATHER(1, true);
+    else RVKV_GATHER(1, false);
+  }
+#undef RVKV_GATHER
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? RVKV_OK : hip_fail(op, e);
+}
+
+uint32_t rvkv_decode_partition_tokens(const rvkv_pool *pool, uint32_t batch,
+                                      uint32_t n_heads, uint32_t max_ctx_len) {
+  if (!pool) return 0;
+  return partition_tokens(pool, batch, n_heads, max_ctx_len);
+}
+
+size_t rvkv_decode_workspace_bytes(const rvkv_pool *pool, uint32_t batch,
+                                   uint32_t n_heads, uint32_t max_ctx_len) {
+  if (!pool) return 0;
+  return ws_layout(pool, batch, n_heads, max_ctx_len).bytes;
+}
+
+int rvkv_paged_decode(const rvkv_pool *pool, uint32_t layer, const float *q,
+                      const uint32_t *block_tables, const uint32_t *ctx_lens,
+                      uint32_t batch, uint32_t max_blocks, uint32_t n_heads,
+                      uint32_t max_ctx_len, float scale, int32_t window,
+                      float *out, void *ws, size_t ws_bytes) {
+  const char *op = "paged_decode";
+  if (!pool) return fail(RVKV_EINVAL, op, "pool is NULL");
+  if (layer >= pool->n_layers)
+    return fail(RVKV_EINVAL, op, "layer out of range");
+  if (batch == 0) return RVKV_OK;
+  if (max_blocks == 0) return fail(RVKV_EINVAL, op, "max_blocks must be positive");
+  if (n_heads == 0 || n_heads % pool->n_kv != 0)
+    return fail(RVKV_EINVAL, op,
+                "n_heads must be a positive multiple of n_kv_heads");
+  const uint32_t hd = pool->head_dim;
+  if (!hd_supported(hd))
+    return fail(RVKV_EUNSUPPORTED, op,
+                "head_dim must be one of 32, 64, 128, 256");
+  const uint32_t bs = pool->block_size;
+  if ((bs & (bs - 1)) != 0 || bs < 512 / hd)
+    return fail(RVKV_EUNSUPPORTED, op,
+                "block_size must be a power of two >= 512 / head_dim");
+  if (!q || !block_tables || !ctx_lens || !out)
+    return fail(RVKV_EINVAL, op, "NULL q/block_tables/ctx_lens/out");
+  if ((uintptr_t)q % 16 || (uintptr_t)out % 16)
+    return fail(RVKV_EINVAL, op, "q and out must be 16-byte aligned");
+  if (max_ctx_len == 0) max_ctx_len = 1;
+  const uint64_t cap64 = (uint64_t)max_blocks * bs;
+  const uint32_t cap = (uint32_t)(cap64 < max_ctx_len ? cap64 : max_ctx_len);
+  const WsLayout w = ws_layout(pool, batch, n_heads, max_ctx_len);
+  if (w.n_parts > 1) {
+    if (!ws) return fail(RVKV_EINVAL, op, "workspace is NULL");
+    if (ws_bytes < w.bytes)
+      return fail(RVKV_EINVAL, op,
+                  "workspace smaller than rvkv_decode_workspace_bytes()");
+    if ((uintptr_t)ws % 256)
+      return fail(RVKV_EINVAL, op, "workspace must be 256-byte aligned");
+  }
+  const uint32_t group = n_heads / pool->n_kv;
+  uint32_t n_sub, gt;
+  subgroups(group, &n_sub, &gt);
+  if ((uint64_t)pool->n_kv * n_sub > 65535 || batch > 65535)
+    return fail(RVKV_EUNSUPPORTED, op, "batch or head count too large");
+
+  DecodeArgs a{};
+  a.kc = pool->tensor(layer, 0);
+  a.vc = pool->tensor(layer, 1);
+  a.q = q;
+  a.out = out;
+  a.tables = block_tables;
+  a.ctx_lens = ctx_lens;
+  a.ws_acc = w.n_parts > 1 ? (float *)((char *)ws + w.acc_off) : nullptr;
+  a.ws_ml = w.n_parts > 1 ? (float *)((char *)ws + w.ml_off) : nullptr;
+  a.block_stride = pool->block_elems;
+  a.head_stride = bs * hd;
+  a.max_blocks = max_blocks;
+  a.num_blocks = pool->num_blocks;
+  a.n_kv = pool->n_kv;
+  a.n_heads = n_heads;
+  a.group = group;
+  a.n_sub = n_sub;
+  a.bs_log2 = ilog2(bs);
+  a.part_tokens = partition_tokens(pool, batch, n_heads, max_ctx_len);
+  a.n_parts = w.n_parts;
+  a.ctx_cap = cap;
+  a.qscale = scale * 1.4426950408889634f;  // log2(e)
+  a.window = window;
+  a.direct = w.n_parts <= 1;
+
+  const dim3 grid(w.n_parts, pool->n_kv * n_sub, batch);
+  hipStream_t st = pool->stream;
+  switch (hd) {
+    case 32: dispatch_gt<32>(gt, a, grid, st); break;
+    case 64: dispatch_gt<64>(gt, a, grid, st); break;
+    case 128: dispatch_gt<128>(gt, a, grid, st); break;
+    default: dispatch_gt<256>(gt, a, grid, st); break;
+  }
+  if (!a.direct) {
+    const dim3 rgrid(n_heads, batch);
+    switch (hd) {
+      case 32: hipLaunchKernelGGL(decode_reduce_kernel<32>, rgrid, dim3(64), 0, st, a); break;
+      case 64: hipLaunchKernelGGL(decode_reduce_kernel<64>, rgrid, dim3(64), 0, st, a); break;
+      case 128: hipLaunchKernelGGL(decode_reduce_kernel<128>, rgrid, dim3(64), 0, st, a); break;
+      default: hipLaunchKernelGGL(decode_reduce_kernel<256>, rgrid, dim3(64), 0, st, a); break;
+    }
+  }
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? RVKV_OK : hip_fail(op, e);
+}
+
+int rvkv_copy_blocks(rvkv_pool *pool, const uint32_t *src, const uint32_t *dst,
+                     uint32_t n) {
+  const char *op = "copy_blocks";
+  if (!pool) return fail(RVKV_EINVAL, op, "pool is NULL");
+  if (n == 0) return RVKV_OK;
+  if (!src || !dst) return fail(RVKV_EINVAL, op, "NULL src/dst");
+  if (n > 65535) return fail(RVKV_EUNSUPPORTED, op, "at most 65535 pairs per call");
+  const size_t bytes = pool->block_elems * 2;
+  const bool w16 = bytes % 16 == 0;
+  const size_t words = w16 ? bytes / 16 : bytes / 2;
+  uint32_t gx = grid_1d(words, 256);
+  if (gx > 64) gx = 64;
+  const dim3 grid(gx, n, 2 * pool->n_layers);
+  if (w16)
+    hipLaunchKernelGGL(copy_blocks_kernel<uint4>, grid, dim3(256), 0,
+                       pool->stream, pool->base, src, dst, pool->tensor_elems,
+                       pool->block_elems, pool->num_blocks);
+  else
+    hipLaunchKernelGGL(copy_blocks_kernel<uint16_t>, grid, dim3(256), 0,
+                       pool->stream, pool->base, src, dst, pool->tensor_elems,
+                       pool->block_elems, pool->num_blocks);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? RVKV_OK : hip_fail(op, e);
+}
+
+int rvkv_read_blocks(const rvkv_pool *pool, uint32_t layer, uint32_t which,
+                     const uint32_t *block_ids, uint32_t n, void *out) {
+  const char *op = "read_blocks";
+  if (!pool) return fail(RVKV_EINVAL, op, "pool is NULL");
+  if (layer >= pool->n_layers || which > 1)
+    return fail(RVKV_EINVAL, op, "layer or which out of range");
+  if (n == 0) return RVKV_OK;
+  if (!block_ids || !out) return fail(RVKV_EINVAL, op, "NULL block_ids/out");
+  const dim3 grid(grid_1d((uint64_t)pool->block_elems * n, 256));
+  hipLaunchKernelGGL(read_blocks_kernel, grid, dim3(256), 0, pool->stream,
+                     pool->tensor(layer, which), block_ids, n,
+                     static_cast<uint16_t *>(out), pool->block_size,
+                     pool->n_kv, pool->head_dim, pool->num_blocks);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? RVKV_OK : hip_fail(op, e);
+}
+
+int rvkv_block_checksums(const rvkv_pool *pool, uint32_t layer,
+                         uint32_t which, const uint32_t *block_ids, uint32_t n,
+                         uint64_t *out) {
+  const char *op = "block_checksums";
+  if (!pool) return fail(RVKV_EINVAL, op, "pool is NULL");
+  if (layer >= pool->n_layers || which > 1)
+    return fail(RVKV_EINVAL, op, "layer or which out of range");
+  if (n == 0) return RVKV_OK;
+  if (!block_ids || !out) return fail(RVKV_EINVAL, op, "NULL block_ids/out");
+  hipLaunchKernelGGL(checksum_kernel, dim3(grid_1d(n, 64)), dim3(64), 0,
+                     pool->stream, pool->tensor(layer, which), block_ids, n,
+                     out, pool->block_size, pool->n_kv, pool->head_dim,
+                     pool->num_blocks);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? RVKV_OK : hip_fail(op, e);
+}
+
+}  // extern "C"

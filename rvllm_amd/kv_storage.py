@@ -1,0 +1,235 @@
+"""Host-side mirror of rvllm's device KV storage API over librvkv.so.
+
+``HipKvStorage`` / ``HipGatherPlan`` keep the names, argument meaning and
+error strings of ``CudaKvStorage`` / ``CudaGatherPlan``
+(src/cuda/kv_storage.rs:17-164) and of the validating wrappers
+``kv_write_wrapper`` / ``kv_gather_wrapper`` (src/cuda/ops.rs:313-445), and
+add the fused paged decode attention and the copy-on-write block copy. Device
+buffers are torch tensors on the GPU, used only as memory: every byte of
+work runs in the HIP kernels of librvkv.so. Length checks the C ABI cannot
+see (it gets raw pointers) are done here, before the call, with the
+reference's messages.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Optional, Sequence, Tuple
+
+import torch
+
+from . import _lib
+from ._lib import RVKV_F16, RVKV_F32, RvkvError, check
+
+_DT = {torch.float32: RVKV_F32, torch.float16: RVKV_F16}
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _need(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RvkvError(msg)
+
+
+def _dev_u32(x, device) -> torch.Tensor:
+    """u32 data as an int32 device tensor (same bits)."""
+    if isinstance(x, torch.Tensor):
+        t = x.to(device=device)
+        if t.dtype != torch.int32:
+            t = t.to(torch.int64).to(torch.int32)
+        return t.contiguous()
+    import numpy as np
+    arr = np.asarray(x, dtype=np.uint32).view(np.int32)
+    return torch.from_numpy(arr.copy()).to(device)
+
+
+class HipGatherPlan:
+    """CudaGatherPlan::new (src/cuda/kv_storage.rs:26-54): each sequence's
+    block table padded to max_blocks with its own last block, uploaded once
+    per forward and shared by all layers. items: [(blocks, n_tokens)]."""
+
+    def __init__(self, items: Sequence[Tuple[Sequence[int], int]], device=None):
+        device = device or torch.device("cuda", torch.cuda.current_device())
+        self.batch = len(items)
+        self.ctx_len = max((n for _, n in items), default=0)
+        self.max_blocks = max((len(b) for b, _ in items), default=0)
+        idx = []
+        for blocks, _ in items:
+            blocks = [int(x) for x in blocks]
+            pad = blocks[-1] if blocks else 0
+            idx.extend(blocks + [pad] * (self.max_blocks - len(blocks)))
+        self.block_idx = _dev_u32(idx, device)
+
+
+class HipKvStorage:
+    """CudaKvStorage (src/cuda/kv_storage.rs:65-164) on MI355X: one zeroed f16
+    pool for all layers' K and V, owned by librvkv."""
+
+    def __init__(self, n_layers: int, num_blocks: int, block_size: int,
+                 n_kv_heads: int, head_dim: int, stream=None):
+        self._L = _lib.load()
+        self.n_layers, self.num_blocks = n_layers, num_blocks
+        self.block_size, self.n_kv_heads, self.head_dim = (block_size,
+                                                           n_kv_heads,
+                                                           head_dim)
+        self.device = torch.device("cuda", torch.cuda.current_device())
+        if stream is None:
+            stream = torch.cuda.current_stream(self.device)
+        self.stream = stream
+        handle = ctypes.c_void_p()
+        check(self._L.rvkv_pool_create(n_layers, num_blocks, block_size,
+                                       n_kv_heads, head_dim, RVKV_F16,
+                                       ctypes.c_void_p(stream.cuda_stream),
+                                       ctypes.byref(handle)))
+        self._pool = handle
+
+    # -- lifetime ---------------------------------------------------------
+    def close(self) -> None:
+        if getattr(self, "_pool", None):
+            self._L.rvkv_pool_destroy(self._pool)
+            self._pool = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def nbytes(self) -> int:
+        return self._L.rvkv_pool_bytes(self._pool)
+
+    # -- a2: append ---------------------------------------------------------
+    def write_tokens(self, layer: int, block_ids: torch.Tensor,
+                     offsets: torch.Tensor, k: torch.Tensor,
+                     v: torch.Tensor) -> None:
+        """CudaKvStorage::write_tokens -> kv_write_wrapper
+        (src/cuda/ops.rs:313-373). k, v: [n_tokens, n_kv, hd] f32 (rounded
+        to f16, nearest-even) or f16 (copied); block_ids/offsets: one u32
+        per token (int32 device tensors carrying the same bits)."""
+        _need(k.numel() == v.numel(), "kv_write: k and v have different lengths")
+        n = k.numel()
+        _need(n != 0, "kv_write: k/v len is 0")
+        per_token = self.n_kv_heads * self.head_dim
+        _need(n % per_token == 0,
+              "kv_write: k/v length is not a multiple of n_kv_heads * head_dim")
+        n_tokens = n // per_token
+        _need(block_ids.numel() == n_tokens and offsets.numel() == n_tokens,
+              "kv_write: block_ids/offsets length must equal n_tokens")
+        _need(k.dtype == v.dtype and k.dtype in _DT,
+              "kv_write: k/v must both be float32 or float16")
+        _need(k.is_contiguous() and v.is_contiguous() and
+              block_ids.is_contiguous() and offsets.is_contiguous(),
+              "kv_write: inputs must be contiguous")
+        check(self._L.rvkv_append(self._pool, layer, _ptr(k), _ptr(v),
+                                  _DT[k.dtype], _ptr(block_ids),
+                                  _ptr(offsets), n_tokens))
+
+    # -- a4: gather ---------------------------------------------------------
+    def gather(self, layer: int, plan: HipGatherPlan, out_k: torch.Tensor,
+               out_v: torch.Tensor) -> None:
+        """CudaKvStorage::gather -> kv_gather_wrapper
+        (src/cuda/ops.rs:381-445): [batch, n_kv, ctx_len, hd] into
+        caller-owned outputs (f32, or f16 for raw bits)."""
+        _need(plan.batch > 0 and plan.max_blocks > 0 and plan.ctx_len > 0,
+              "kv_gather: batch/max_blocks/ctx_len/block_size/n_kv_heads/"
+              "head_dim must be positive")
+        _need(plan.block_idx.numel() == plan.batch * plan.max_blocks,
+              "kv_gather: block_idx length must equal batch * max_blocks")
+        n = plan.batch * self.n_kv_heads * plan.ctx_len * self.head_dim
+        _need(out_k.numel() == n and out_v.numel() == n,
+              "kv_gather: output length must equal batch * n_kv_heads * "
+              "ctx_len * head_dim")
+        _need(plan.ctx_len <= plan.max_blocks * self.block_size,
+              "kv_gather: ctx_len must not exceed max_blocks * block_size")
+        _need(out_k.dtype == out_v.dtype and out_k.dtype in _DT,
+              "kv_gather: outputs must both be float32 or float16")
+        check(self._L.rvkv_gather(self._pool, layer, _ptr(plan.block_idx),
+                                  plan.batch, plan.max_blocks, plan.ctx_len,
+                                  _ptr(out_k), _ptr(out_v), _DT[out_k.dtype]))
+
+    # -- a5 + a6: paged decode attention -----------------------------------
+    def decode_workspace_bytes(self, batch: int, n_heads: int,
+                               max_ctx_len: int) -> int:
+        return self._L.rvkv_decode_workspace_bytes(self._pool, batch, n_heads,
+                                                   max_ctx_len)
+
+    def decode_partition_tokens(self, batch: int, n_heads: int,
+                                max_ctx_len: int) -> int:
+        return self._L.rvkv_decode_partition_tokens(self._pool, batch,
+                                                    n_heads, max_ctx_len)
+
+    def alloc_workspace(self, batch: int, n_heads: int,
+                        max_ctx_len: int) -> torch.Tensor:
+        nbytes = self.decode_workspace_bytes(batch, n_heads, max_ctx_len)
+        return torch.empty(max(nbytes, 256), dtype=torch.uint8,
+                           device=self.device)
+
+    def paged_decode(self, layer: int, q: torch.Tensor,
+                     block_tables: torch.Tensor, ctx_lens: torch.Tensor,
+                     max_ctx_len: int, out: Optional[torch.Tensor] = None,
+                     ws: Optional[torch.Tensor] = None,
+                     scale: Optional[float] = None,
+                     window: int = 0) -> torch.Tensor:
+        """One decode step of attention for every sequence (q_len 1), read
+        straight through the block tables: the fused replacement of
+        kv_gather + attention_scores + mask_add_broadcast + softmax +
+        attention_apply (src/cuda/model.rs:528-569). q: [batch, n_heads,
+        hd] f32; block_tables: [batch, max_blocks] u32; ctx_lens: [batch]
+        u32 (read_num_tokens, including this step's token)."""
+        _need(q.dim() == 3 and q.shape[2] == self.head_dim,
+              "paged_decode: q must be [batch, n_heads, head_dim]")
+        _need(q.dtype == torch.float32 and q.is_contiguous(),
+              "paged_decode: q must be contiguous float32")
+        batch, n_heads, hd = q.shape
+        _need(block_tables.dim() == 2 and block_tables.shape[0] == batch,
+              "paged_decode: block_tables must be [batch, max_blocks]")
+        _need(ctx_lens.numel() == batch,
+              "paged_decode: ctx_lens length must equal batch")
+        max_blocks = block_tables.shape[1]
+        if out is None:
+            out = torch.empty_like(q)
+        _need(out.shape == q.shape and out.dtype == torch.float32 and
+              out.is_contiguous(), "paged_decode: out must match q")
+        need = self.decode_workspace_bytes(batch, n_heads, max_ctx_len)
+        if ws is None and need:
+            ws = self.alloc_workspace(batch, n_heads, max_ctx_len)
+        if scale is None:
+            scale = 1.0 / math.sqrt(hd)
+        check(self._L.rvkv_paged_decode(
+            self._pool, layer, _ptr(q), _ptr(block_tables), _ptr(ctx_lens),
+            batch, max_blocks, n_heads, max_ctx_len, float(scale),
+            int(window or 0), _ptr(out), _ptr(ws),
+            ws.numel() if ws is not None else 0))
+        return out
+
+    # -- a10: copy-on-write -------------------------------------------------
+    def copy_blocks(self, src: torch.Tensor, dst: torch.Tensor) -> None:
+        """Copies src[i] -> dst[i] for all layers, K and V."""
+        _need(src.numel() == dst.numel(),
+              "copy_blocks: src and dst have different lengths")
+        check(self._L.rvkv_copy_blocks(self._pool, _ptr(src), _ptr(dst),
+                                       src.numel()))
+
+    # -- inspection ---------------------------------------------------------
+    def read_blocks(self, layer: int, which: int,
+                    block_ids: torch.Tensor) -> torch.Tensor:
+        """Logical [n, block_size, n_kv, hd] f16 contents of the blocks."""
+        n = block_ids.numel()
+        out = torch.empty((n, self.block_size, self.n_kv_heads,
+                           self.head_dim), dtype=torch.float16,
+                          device=self.device)
+        check(self._L.rvkv_read_blocks(self._pool, layer, which,
+                                       _ptr(block_ids), n, _ptr(out)))
+        return out
+
+    def block_checksums(self, layer: int, which: int,
+                        block_ids: torch.Tensor) -> torch.Tensor:
+        """FNV-1a 64 of each block's logical f16 bytes (int64 bits)."""
+        n = block_ids.numel()
+        out = torch.empty(n, dtype=torch.int64, device=self.device)
+        check(self._L.rvkv_block_checksums(self._pool, layer, which,
+                                           _ptr(block_ids), n, _ptr(out)))
+        return out

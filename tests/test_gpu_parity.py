@@ -1,0 +1,463 @@
+"""GPU parity: librvkv's HIP kernels (through the C ABI) against the oracle.
+
+Append, gather and copy are bit-exact on cache contents; decode attention
+agrees with the oracle's float64 paged attention over the SAME f16 cache
+within 2e-3 max-abs (f16 storage, f32 accumulation). Full-size configs are
+checked on sampled sequences plus size-independent properties.
+"""
+import math
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from rvllm_amd import workloads as W
+from rvllm_amd._lib import RvkvError
+from rvllm_amd.kv_storage import HipGatherPlan, HipKvStorage
+from tests.golden.make_golden import METAL_CASES, metal_case_inputs
+from tests.gpu_util import dev_u32, fill_layer, oracle_subset
+
+pytestmark = pytest.mark.gpu
+
+ATOL = 2e-3  # north-star tolerance, f16 KV with f32 accumulation
+
+
+@pytest.fixture(autouse=True)
+def _announce(request):
+    print(f"\n[gpu] {request.node.name}", flush=True)
+    sys.stdout.flush()
+    yield
+    torch.cuda.synchronize()
+
+
+def f16_from(x_f32: np.ndarray) -> torch.Tensor:
+    bits = orc.f32_to_f16_bits(x_f32)
+    return torch.from_numpy(bits.view(np.int16).copy()).view(
+        torch.float16).cuda()
+
+
+def bits(t: torch.Tensor) -> np.ndarray:
+    return t.cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+# ---- the reference's KATs through the C ABI -------------------------------
+def test_kat_round_trip_across_blocks(golden):
+    g = golden["reference_kats"]["round_trip_across_blocks"]
+    st = HipKvStorage(1, 3, 2, 1, 2)
+    k = torch.tensor(g["k"], dtype=torch.float32).reshape(4, 1, 2).cuda()
+    st.write_tokens(0, dev_u32(g["block_ids"]), dev_u32(g["offsets"]), k, k)
+    raw = st.read_blocks(0, 0, dev_u32([0, 1, 2])).float().cpu().reshape(-1)
+    assert raw.tolist() == g["raw_cache"]
+    plan = HipGatherPlan([(g["tables"][0], 3), (g["tables"][1], 1)])
+    assert plan.ctx_len == 3
+    assert plan.block_idx.cpu().tolist() == g["plan_block_idx"]
+    ok = torch.zeros(2 * 1 * 3 * 2, device="cuda")
+    ov = torch.zeros_like(ok)
+    st.gather(0, plan, ok, ov)
+    got = ok.cpu().tolist()
+    assert got == ov.cpu().tolist()
+    assert got[:6] == g["gather_prefix_a"]
+    assert got[6:8] == g["gather_prefix_b"]
+
+
+def test_kat_untouched_slots(golden):
+    g = golden["reference_kats"]["untouched_slots"]
+    st = HipKvStorage(1, 1, 4, 1, 2)
+    t = torch.tensor(g["k"], dtype=torch.float32).reshape(1, 1, 2).cuda()
+    st.write_tokens(0, dev_u32([0]), dev_u32([2]), t, t)
+    plan = HipGatherPlan([([0], 4)])
+    ok = torch.zeros(8, device="cuda")
+    ov = torch.zeros(8, device="cuda")
+    st.gather(0, plan, ok, ov)
+    assert ok.cpu().tolist() == g["gather"]
+
+
+def test_kat_copy_is_independent_of_original(golden):
+    """KvStorage::clone independence (src/kv_storage.rs:239-255) at block
+    granularity: copy block 0 -> 1, then write block 0; the copy keeps the
+    old contents."""
+    st = HipKvStorage(1, 2, 2, 1, 2)
+    st.copy_blocks(dev_u32([0]), dev_u32([1]))
+    t = torch.tensor([1.0, 1.5]).reshape(1, 1, 2).cuda()
+    st.write_tokens(0, dev_u32([0]), dev_u32([0]), t, t)
+    raw = st.read_blocks(0, 0, dev_u32([0, 1])).float().cpu().reshape(-1)
+    assert raw[:2].tolist() == [1.0, 1.5]
+    assert raw[4:6].tolist() == [0.0, 0.0]
+
+
+def test_rejections_mirror_the_reference():
+    st = HipKvStorage(1, 4, 4, 1, 2)
+    k = torch.zeros(2, device="cuda")
+    v = torch.zeros(4, device="cuda")
+    ids = dev_u32([0])
+    with pytest.raises(RvkvError, match="kv_write: k and v have different"):
+        st.write_tokens(0, ids, ids, k, v)
+    k4 = torch.zeros(4, device="cuda")
+    with pytest.raises(RvkvError, match="kv_write: block_ids/offsets length"):
+        st.write_tokens(0, ids, ids, k4, k4)  # 2 tokens, 1 position
+    plan = HipGatherPlan([([0, 1], 2), ([0, 1], 2)])
+    with pytest.raises(RvkvError, match="kv_gather: output length"):
+        st.gather(0, plan, torch.zeros(3, device="cuda"),
+                  torch.zeros(3, device="cuda"))
+    plan.ctx_len = 9
+    with pytest.raises(RvkvError, match="kv_gather: ctx_len must not exceed"):
+        n = 2 * 1 * 9 * 2
+        st.gather(0, plan, torch.zeros(n, device="cuda"),
+                  torch.zeros(n, device="cuda"))
+    with pytest.raises(RvkvError, match="kv_write: layer out of range"):
+        st.write_tokens(1, ids, ids, k, k)
+
+
+# ---- append: bit-exact f32 -> f16 and f16 copies --------------------------
+SPECIALS = np.array([0.0, -0.0, 1.0, -1.0, 65504.0, 65519.99, 65520.0,
+                     -1e6, np.inf, -np.inf, 6.1e-5, 6.0e-5, 5.96e-8, 2.98e-8,
+                     2.9802326e-08, 1 + 2**-11, 1 + 3 * 2**-11, 1e-9, -3e-6,
+                     0.333333], np.float32)
+
+
+@pytest.mark.parametrize("nkv,hd,bs", [(8, 64, 16), (8, 128, 16), (1, 256, 16),
+                                       (2, 64, 32), (3, 2, 2), (5, 12, 3)])
+def test_append_bit_exact_f32_source(nkv, hd, bs):
+    rng = np.random.default_rng(hd * 7 + nkv)
+    nb = 37
+    st = HipKvStorage(2, nb, bs, nkv, hd)
+    ref = orc.KvCache(nb, bs, nkv, hd, orc.F16)
+    slots = rng.permutation(nb * bs)[: nb * bs // 2]
+    n = len(slots)
+    k = (rng.standard_normal((n, nkv, hd)) * 4).astype(np.float32)
+    v = (rng.standard_normal((n, nkv, hd)) * 1e-4).astype(np.float32)
+    flat = k.reshape(-1)
+    flat[: len(SPECIALS)] = SPECIALS[: min(len(SPECIALS), flat.size)]
+    blk, off = slots // bs, slots % bs
+    st.write_tokens(1, dev_u32(blk), dev_u32(off), torch.from_numpy(k).cuda(),
+                    torch.from_numpy(v).cuda())
+    ref.write_tokens(blk, off, k, v)
+    ids = dev_u32(np.arange(nb))
+    assert np.array_equal(bits(st.read_blocks(1, 0, ids)), ref.k)
+    assert np.array_equal(bits(st.read_blocks(1, 1, ids)), ref.v)
+    # layer 0 untouched
+    assert not bits(st.read_blocks(0, 0, ids)).any()
+
+
+def test_append_f16_source_copies_bits():
+    rng = np.random.default_rng(11)
+    nb, bs, nkv, hd = 20, 16, 4, 64
+    st = HipKvStorage(1, nb, bs, nkv, hd)
+    ref = orc.KvCache(nb, bs, nkv, hd, orc.F16)
+    slots = rng.permutation(nb * bs)[:150]
+    kb = rng.integers(0, 65536, (150, nkv, hd), dtype=np.uint16)
+    kb[(kb & 0x7C00) == 0x7C00] = 0x3C00  # keep values finite
+    vb = kb[::-1].copy()
+    kt = torch.from_numpy(kb.view(np.int16)).view(torch.float16).cuda()
+    vt = torch.from_numpy(vb.view(np.int16)).view(torch.float16).cuda()
+    st.write_tokens(0, dev_u32(slots // bs), dev_u32(slots % bs), kt, vt)
+    ref.write_tokens_f16(slots // bs, slots % bs, kb, vb)
+    ids = dev_u32(np.arange(nb))
+    assert np.array_equal(bits(st.read_blocks(0, 0, ids)), ref.k)
+    assert np.array_equal(bits(st.read_blocks(0, 1, ids)), ref.v)
+
+
+def test_append_skips_out_of_range_slots():
+    st = HipKvStorage(1, 4, 16, 1, 64)
+    k = torch.ones(3, 1, 64, device="cuda")
+    st.write_tokens(0, dev_u32([0, 99, 1]), dev_u32([0, 0, 40]), k, k)
+    raw = st.read_blocks(0, 0, dev_u32([0, 1, 2, 3])).float().cpu()
+    assert raw[0, 0].eq(1).all() and raw.sum().item() == 64
+
+
+# ---- gather: bit-exact, padded plan ---------------------------------------
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("nkv,hd,bs", [(8, 64, 16), (2, 6, 4), (1, 256, 16)])
+def test_gather_bit_exact(out_dtype, nkv, hd, bs):
+    rng = np.random.default_rng(hd + nkv)
+    nb = 50
+    st = HipKvStorage(1, nb, bs, nkv, hd)
+    fill_layer(st, 0, seed=hd)
+    ids = dev_u32(np.arange(nb))
+    ref = orc.KvCache(nb, bs, nkv, hd, orc.F16)
+    ref.k[:] = bits(st.read_blocks(0, 0, ids))
+    ref.v[:] = bits(st.read_blocks(0, 1, ids))
+    perm = rng.permutation(nb)
+    lens = [3 * bs + 1, bs, 1, 5 * bs]
+    tables, at = [], 0
+    for n in lens:
+        p = -(-n // bs)
+        tables.append(perm[at:at + p].tolist())
+        at += p
+    plan = HipGatherPlan(list(zip(tables, lens)))
+    idx, mb, cl = orc.gather_plan(tables, lens)
+    assert plan.block_idx.cpu().numpy().view(np.uint32).tolist() == idx.tolist()
+    n = len(lens) * nkv * cl * hd
+    ok = torch.empty(n, dtype=out_dtype, device="cuda")
+    ov = torch.empty(n, dtype=out_dtype, device="cuda")
+    st.gather(0, plan, ok, ov)
+    wk, wv = ref.gather(idx, len(lens), mb, cl)
+    if out_dtype == torch.float32:
+        assert np.array_equal(ok.cpu().numpy().reshape(wk.shape), wk)
+        assert np.array_equal(ov.cpu().numpy().reshape(wv.shape), wv)
+    else:
+        assert np.array_equal(bits(ok).reshape(wk.shape),
+                              orc.f32_to_f16_bits(wk))
+        assert np.array_equal(bits(ov).reshape(wv.shape),
+                              orc.f32_to_f16_bits(wv))
+
+
+# ---- copy-on-write --------------------------------------------------------
+def test_copy_blocks_all_layers_bit_exact():
+    nl, nb, bs, nkv, hd = 3, 24, 16, 2, 64
+    st = HipKvStorage(nl, nb, bs, nkv, hd)
+    for layer in range(nl):
+        fill_layer(st, layer, seed=100 + layer)
+    ids = dev_u32(np.arange(nb))
+    before = [[bits(st.read_blocks(l, w, ids)) for w in (0, 1)]
+              for l in range(nl)]
+    src, dst = [3, 10, 17], [20, 0, 5]
+    st.copy_blocks(dev_u32(src), dev_u32(dst))
+    for l in range(nl):
+        for w in (0, 1):
+            ref = orc.KvCache(nb, bs, nkv, hd, orc.F16)
+            ref.k[:] = before[l][w]
+            ref.v[:] = before[l][w]
+            ref.copy_blocks(src, dst)
+            after = bits(st.read_blocks(l, w, ids))
+            assert np.array_equal(after, ref.k)
+    # checksums agree with the oracle's FNV-1a
+    csum = st.block_checksums(2, 1, ids).cpu().numpy().view(np.uint64)
+    ref = orc.KvCache(nb, bs, nkv, hd, orc.F16)
+    ref.v[:] = bits(st.read_blocks(2, 1, ids))
+    assert np.array_equal(csum, ref.checksums(1, np.arange(nb)))
+
+
+def test_cow_then_append_touches_only_the_copy():
+    """The sharer's append after a CoW changes its private block only; the
+    other sharer's view (its gather) is unchanged (parity unpinned:
+    invariant)."""
+    nb, bs, nkv, hd = 8, 16, 2, 64
+    st = HipKvStorage(1, nb, bs, nkv, hd)
+    fill_layer(st, 0, seed=5)
+    plan_a = HipGatherPlan([([0, 1], 24)])
+    n = 1 * nkv * 24 * hd
+    before = torch.empty(n, device="cuda")
+    st.gather(0, plan_a, before, torch.empty_like(before))
+    st.copy_blocks(dev_u32([1]), dev_u32([6]))
+    k = torch.full((1, nkv, hd), 7.0, device="cuda")
+    st.write_tokens(0, dev_u32([6]), dev_u32([8]), k, k)
+    after = torch.empty_like(before)
+    st.gather(0, plan_a, after, torch.empty_like(after))
+    assert torch.equal(before, after)
+    plan_b = HipGatherPlan([([0, 6], 25)])
+    nb_ = 1 * nkv * 25 * hd
+    gb = torch.empty(nb_, device="cuda")
+    st.gather(0, plan_b, gb, torch.empty_like(gb))
+    gb = gb.reshape(nkv, 25, hd)
+    assert gb[:, 24].eq(7.0).all()
+    assert torch.equal(gb[:, :24].reshape(-1),
+                       before.reshape(nkv, 24, hd).reshape(-1))
+
+
+# ---- paged decode attention ----------------------------------------------
+def _decode_vs_oracle(st, layer, db, q, window=0, sample=None):
+    tables_pad = dev_u32(db.padded_tables())
+    ctx = dev_u32(db.ctx_lens)
+    max_ctx = int(db.ctx_lens.max())
+    out = st.paged_decode(layer, q, tables_pad, ctx, max_ctx, window=window)
+    out = out.cpu().numpy()
+    idx = range(db.batch) if sample is None else sample
+    tables = [db.tables[b] for b in idx]
+    lens = db.ctx_lens[list(idx)]
+    cache, padded, mb = oracle_subset(st, layer, tables, lens)
+    qn = q.cpu().numpy()[list(idx)]
+    want = orc.paged_decode_f64(cache, qn, padded.reshape(-1), mb, lens,
+                                window=window)
+    err = np.abs(out[list(idx)] - want).max()
+    assert np.isfinite(out).all()
+    return err
+
+
+@pytest.mark.parametrize("case", [0, 1, 2, 4])
+def test_decode_metal_cases(golden, case):
+    """attn_decode cases of src/metal/ops.rs:684-691 at q_len 1 (the decode
+    kernel), xorshift data stored as f16, ragged ctx - 2b, reversed block
+    tables."""
+    c = metal_case_inputs(case)
+    B, H, D, bs = c["batch"], c["n_heads"], c["hd"], c["bs"]
+    st = HipKvStorage(1, c["num_blocks"], bs, c["n_kv"], D)
+    nslot = c["num_blocks"] * bs
+    slots = np.arange(nslot)
+    st.write_tokens(0, dev_u32(slots // bs), dev_u32(slots % bs),
+                    torch.from_numpy(c["cache_k"].reshape(nslot, c["n_kv"],
+                                                          D)).cuda(),
+                    torch.from_numpy(c["cache_v"].reshape(nslot, c["n_kv"],
+                                                          D)).cuda())
+    q = torch.from_numpy(c["q"][: B * H * D].reshape(B, H, D)).cuda()
+    ctx = np.array([c["ctx"] - 2 * b for b in range(B)], np.uint32)
+    tables = dev_u32(c["block_idx"].reshape(B, c["max_blocks"]))
+    out = st.paged_decode(0, q, tables, dev_u32(ctx), c["ctx"]).cpu().numpy()
+    ref = orc.KvCache(c["num_blocks"], bs, c["n_kv"], D, orc.F16)
+    ref.write_tokens(slots // bs, slots % bs,
+                     c["cache_k"].reshape(nslot, c["n_kv"], D),
+                     c["cache_v"].reshape(nslot, c["n_kv"], D))
+    want = orc.paged_decode_f64(ref, q.cpu().numpy(), c["block_idx"],
+                                c["max_blocks"], ctx)
+    assert np.abs(out - want).max() < ATOL
+    if case in (0, 1):  # q_len 1 in the reference too: the golden applies
+        exp = np.array(golden["metal_attn_decode"][case]["expected"],
+                       np.float32).reshape(B, H, D)
+        # golden is over the f32 cache; f16 storage adds <= ~1e-3
+        assert np.abs(out - exp).max() < ATOL
+
+
+def test_decode_unsupported_head_dims_raise():
+    for hd in (6, 200):
+        st = HipKvStorage(1, 4, 16, 1, hd)
+        q = torch.zeros(1, 2, hd, device="cuda")
+        with pytest.raises(RvkvError, match="paged_decode: head_dim"):
+            st.paged_decode(0, q, dev_u32([[0]]), dev_u32([4]), 4)
+
+
+def test_decode_edge_cases():
+    """ctx 0 -> zero row; ctx 1; lengths off every boundary; an
+    out-of-range block id in a table is read as masked (no fault)."""
+    nb, bs, nkv, hd, H = 64, 16, 2, 64, 8
+    st = HipKvStorage(1, nb, bs, nkv, hd)
+    fill_layer(st, 0, seed=9)
+    rng = np.random.default_rng(1)
+    perm = rng.permutation(nb).astype(np.uint32)
+    lens = np.array([0, 1, 15, 16, 17, 255, 256, 257], np.uint32)
+    tables, at = [], 0
+    for n in lens:
+        p = max(1, -(-int(n) // bs))
+        tables.append(perm[at:at + p])
+        at += p
+    cfg = W.Config("edge", 9, 1, H, nkv, hd, bs, len(lens))
+    db = W.DecodeBatch(cfg, nb, lens, tables, np.zeros(len(lens), np.uint32),
+                       np.zeros(len(lens), np.uint32))
+    q = torch.randn(len(lens), H, hd, device="cuda")
+    out = st.paged_decode(0, q, dev_u32(db.padded_tables()),
+                          dev_u32(lens), int(lens.max()))
+    assert out[0].eq(0).all()
+    err = _decode_vs_oracle(st, 0, db, q, sample=list(range(1, len(lens))))
+    assert err < ATOL
+    # A table entry past the pool: no fault, finite output.
+    bad = db.padded_tables()
+    bad[7, 3] = 10_000
+    out2 = st.paged_decode(0, q, dev_u32(bad), dev_u32(lens), 257)
+    assert torch.isfinite(out2).all()
+    assert torch.equal(out2[:7], out[:7])
+
+
+@pytest.mark.parametrize("max_ctx", [300, 5000])
+def test_decode_multi_partition_and_window(max_ctx):
+    """Partition split + reduction pass (several partitions) and the
+    sliding window (keys j >= ctx - window)."""
+    bs, nkv, hd, H = 16, 4, 128, 8
+    rng = np.random.default_rng(2)
+    lens = rng.integers(1, max_ctx + 1, 6).astype(np.uint32)
+    lens[0] = max_ctx
+    cfg = W.Config("mp", 9, 1, H, nkv, hd, bs, len(lens))
+    db = W.ragged_batch(cfg, lens, seed=3, extra_blocks=7)
+    st = HipKvStorage(1, db.num_blocks, bs, nkv, hd)
+    fill_layer(st, 0, seed=max_ctx)
+    q = torch.randn(len(lens), H, hd, device="cuda")
+    assert st.decode_partition_tokens(len(lens), H, max_ctx) >= 256
+    for window in (0, 100, 4096):
+        err = _decode_vs_oracle(st, 0, db, q, window=window)
+        assert err < ATOL, (window, err)
+
+
+@pytest.mark.parametrize("G", [1, 2, 3, 5, 7, 8, 9, 16])
+def test_decode_group_sizes(G):
+    nb, bs, nkv, hd = 96, 16, 2, 64
+    st = HipKvStorage(1, nb, bs, nkv, hd)
+    fill_layer(st, 0, seed=G)
+    cfg = W.Config("g", 9, 1, nkv * G, nkv, hd, bs, 4)
+    db = W.ragged_batch(cfg, [300, 17, 700, 64], seed=G)
+    q = torch.randn(4, nkv * G, hd, device="cuda")
+    assert _decode_vs_oracle(st, 0, db, q) < ATOL
+
+
+# ---- BASELINE configs (one layer each, full batch and context) ------------
+def test_config_smollm2():
+    db = W.smollm2_batch()
+    c = db.cfg
+    st = HipKvStorage(1, db.num_blocks, c.block_size, c.n_kv_heads,
+                      c.head_dim)
+    fill_layer(st, 0, seed=c.seed)
+    rng = W.Rng(c.seed + 1)
+    # append this step's token (f32 source, reference dtype), then decode
+    nk = rng.normal((db.batch, c.n_kv_heads, c.head_dim))
+    nv = rng.normal((db.batch, c.n_kv_heads, c.head_dim))
+    st.write_tokens(0, dev_u32(db.slot_block), dev_u32(db.slot_off),
+                    torch.from_numpy(nk).cuda(), torch.from_numpy(nv).cuda())
+    q = torch.from_numpy(rng.normal((db.batch, c.n_heads, c.head_dim))).cuda()
+    assert _decode_vs_oracle(st, 0, db, q) < ATOL
+    # the oracle's reference pipeline (f32 gqa over the padded gather)
+    # agrees too, and its append is bit-identical to the HIP append
+    ids = dev_u32(np.arange(db.num_blocks))
+    cache = orc.KvCache(db.num_blocks, c.block_size, c.n_kv_heads,
+                        c.head_dim, orc.F16)
+    cache.k[:] = bits(st.read_blocks(0, 0, ids))
+    cache.v[:] = bits(st.read_blocks(0, 1, ids))
+    before_k = cache.k.copy()
+    idx, mb, _ = orc.gather_plan(db.tables, db.ctx_lens)
+    out_ref = orc.decode_step(cache, db.slot_block, db.slot_off, nk, nv, idx,
+                              mb, db.ctx_lens, q.cpu().numpy(), n_threads=4)
+    assert np.array_equal(cache.k, before_k)  # re-append: same bits
+    out = st.paged_decode(0, q, dev_u32(db.padded_tables()),
+                          dev_u32(db.ctx_lens), int(db.ctx_lens.max()))
+    assert np.abs(out.cpu().numpy() - out_ref).max() < ATOL
+
+
+@pytest.mark.parametrize("name", ["llama-3.2-1b", "qwen3-0.6b",
+                                  "gemma-3-270m"])
+def test_config_uniform_full_size(name):
+    c = W.CONFIGS[name]
+    ctx = {"llama-3.2-1b": 2048, "qwen3-0.6b": 4096, "gemma-3-270m": 1024}[name]
+    db = W.uniform_batch(c, ctx)
+    st = HipKvStorage(1, db.num_blocks, c.block_size, c.n_kv_heads,
+                      c.head_dim)
+    fill_layer(st, 0, seed=c.seed, scale=c.value_scale)
+    q = torch.randn(db.batch, c.n_heads, c.head_dim, device="cuda",
+                    generator=torch.Generator("cuda").manual_seed(c.seed))
+    rng = np.random.default_rng(c.seed)
+    sample = sorted(rng.choice(db.batch, 8, replace=False).tolist())
+    assert _decode_vs_oracle(st, 0, db, q, sample=sample) < ATOL
+    # size-independent property: a duplicate of every sequence through the
+    # same table gives bit-identical rows (deterministic kernel, no races).
+    tp = db.padded_tables()
+    tables2 = dev_u32(np.concatenate([tp, tp]))
+    ctx2 = dev_u32(np.concatenate([db.ctx_lens, db.ctx_lens]))
+    out = st.paged_decode(0, torch.cat([q, q]), tables2, ctx2, ctx)
+    assert torch.equal(out[: db.batch], out[db.batch:])
+    if name == "gemma-3-270m":  # gemma's local layers: 512-token window
+        assert _decode_vs_oracle(st, 0, db, q, window=512,
+                                 sample=sample) < ATOL
+
+
+def test_config_qwen25_ragged_prefix_cow():
+    db = W.qwen25_batch()
+    c = db.cfg
+    st = HipKvStorage(2, db.num_blocks, c.block_size, c.n_kv_heads,
+                      c.head_dim)
+    for layer in range(2):
+        fill_layer(st, layer, seed=c.seed + layer)
+    assert len(db.cow_src) > 0
+    # CoW first (all layers), then the append, then decode.
+    st.copy_blocks(dev_u32(db.cow_src), dev_u32(db.cow_dst))
+    ids = dev_u32(db.cow_dst)
+    src_ids = dev_u32(db.cow_src)
+    for layer in range(2):
+        assert torch.equal(st.read_blocks(layer, 1, ids),
+                           st.read_blocks(layer, 1, src_ids))
+    g = torch.Generator("cuda").manual_seed(1)
+    nk = torch.randn(db.batch, c.n_kv_heads, c.head_dim, device="cuda",
+                     generator=g)
+    st.write_tokens(1, dev_u32(db.slot_block), dev_u32(db.slot_off), nk, nk)
+    q = torch.randn(db.batch, c.n_heads, c.head_dim, device="cuda",
+                    generator=g)
+    sharers = db.shared_prefix["sharers"]
+    rng = np.random.default_rng(0)
+    sample = sorted(set(sharers[:6]) | set(rng.choice(db.batch, 6).tolist()))
+    assert _decode_vs_oracle(st, 1, db, q, sample=sample) < ATOL
