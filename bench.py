@@ -33,15 +33,48 @@ def parse():
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--config", default="llama-3.2-1b")
+    p.add_argument("--batch", type=int, default=0,
+                   help="override the number of sequences (uniform configs)")
     p.add_argument("--no-cpu", action="store_true",
                    help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="wall-clock budget of the CPU baseline sample")
+    p.add_argument("--graph", action="store_true",
+                   help="time the step as one HIP graph replay (all layers' "
+                        "append + decode launches captured once)")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="only time a plain 2 GiB device-to-device copy (the "
+                        "achievable-bandwidth and PMC-counter reference)")
     return p.parse_args()
 
 
-def build_workload(W, name):
+def copy_calibration(torch, steps):
+    """Times torch's device copy of a 2 GiB buffer into another: 4 GiB of
+    HBM traffic per launch (read + write)."""
+    n = (2 << 30) // 4
+    a = torch.randn(n, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        b.copy_(a)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    print(json.dumps({"copy_calibration": {
+        "bytes_per_launch": 2 * n * 4, "avg_launch_ms": round(ms, 4),
+        "GB/s": round(2 * n * 4 / (ms * 1e-3) / 1e9, 1)}}), flush=True)
+
+
+def build_workload(W, name, batch=0):
     c = W.CONFIGS[name]
+    if batch:
+        import dataclasses
+        c = dataclasses.replace(c, batch=batch)
     if name == "llama-3.2-1b":
         return W.uniform_batch(c, 2048)
     if name == "qwen3-0.6b":
@@ -49,7 +82,7 @@ def build_workload(W, name):
     if name == "gemma-3-270m":
         return W.uniform_batch(c, 1024)
     if name == "qwen2.5-0.5b":
-        return W.qwen25_batch()
+        return W.qwen25_batch(batch=c.batch)
     if name == "smollm2-360m":
         return W.smollm2_batch()
     raise SystemExit(f"unknown config {name}")
@@ -101,7 +134,7 @@ def cpu_baseline(orc, W, st, db, budget_s):
     q = rng.normal((db.batch, c.n_heads, c.head_dim))
     idx = db.padded_tables().reshape(-1)
     reps, t_total = 0, 0.0
-    while reps < 1 or (t_total < budget_s and reps < 50):
+    while reps < 1 or (t_total < budget_s and reps < 1000):
         t0 = time.perf_counter()
         orc.decode_step(cache, db.slot_block, db.slot_off, nk, nv, idx,
                         db.max_blocks, db.ctx_lens, q, n_threads=threads)
@@ -137,7 +170,10 @@ def main():
     from rvllm_amd.kv_storage import HipKvStorage
 
     torch.cuda.set_device(0)
-    db = build_workload(W, args.config)
+    if args.copy_calibration:
+        copy_calibration(torch, max(args.steps, 5))
+        return
+    db = build_workload(W, args.config, args.batch)
     c = db.cfg
     st = HipKvStorage(c.n_layers, db.num_blocks, c.block_size, c.n_kv_heads,
                       c.head_dim)
@@ -178,12 +214,27 @@ def main():
             if record:
                 ev[layer][1].record()
 
+    run = step
+    if args.graph:
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            st.set_stream(side)
+            step()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            st.set_stream(torch.cuda.current_stream())
+            step()
+        st.set_stream(torch.cuda.current_stream())
+        run = graph.replay
+
     for _ in range(args.warmup):
-        step()
+        run()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        step()
+        run()
     torch.cuda.synchronize()
     dt = (time.perf_counter() - t0) / args.steps
 
@@ -224,6 +275,7 @@ def main():
             "global_batch": B,
             "seq_len": max_ctx,
             "parallelism": "single GPU",
+            "launch": "hip graph" if args.graph else "eager",
             "partition_tokens": part,
         },
         "pct_of_peak": round(100 * step_bytes / dt / 1e9 / HBM_PEAK_GBS, 2),

@@ -13,6 +13,7 @@
 
 #include <cstdint>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 
@@ -288,8 +289,8 @@ struct DecodeArgs {
   float *out;
   const uint32_t *tables;
   const uint32_t *ctx_lens;
-  float *ws_acc;  // [batch][n_heads][n_parts][hd]
-  float *ws_ml;   // [batch][n_heads][n_parts][2]
+  float *ws_acc;     // [batch][n_heads][n_parts][hd]
+  float *ws_ml;      // [batch][n_heads][n_parts][2]
   uint64_t block_stride;  // elements per block (all heads)
   uint32_t head_stride;   // elements per (block, head) tile
   uint32_t max_blocks, num_blocks, n_kv, n_heads, group, n_sub;
@@ -306,12 +307,12 @@ __device__ __forceinline__ float dpp(float x) {
                                          0xF, 0xF, false));
 }
 
-// Sum over the R lanes of a row group (R in {4, 8, 16, 32}); every lane of
+// Sum over the R lanes of a row group (R in {2, 4, 8, 16, 32}); every lane of
 // the group ends with the total.
 template <int R>
 __device__ __forceinline__ float row_group_sum(float x) {
   x += dpp<0xB1>(x);  // quad_perm [1,0,3,2]: lane ^ 1
-  x += dpp<0x4E>(x);  // quad_perm [2,3,0,1]: lane ^ 2
+  if constexpr (R >= 4) x += dpp<0x4E>(x);  // quad_perm [2,3,0,1]: lane ^ 2
   if constexpr (R >= 8) x += dpp<0x141>(x);  // row_half_mirror: 8-lane total
   if constexpr (R >= 16) x += dpp<0x140>(x);  // row_mirror: 16-lane total
   if constexpr (R >= 32)
@@ -323,145 +324,77 @@ __device__ __forceinline__ float row_group_sum(float x) {
 
 constexpr float kNegBig = -1.0e30f;  // finite "minus infinity" for m
 
-template <int HD, int GT, int U>
-__global__ void __launch_bounds__(64) decode_part_kernel(DecodeArgs a) {
-  constexpr int R = HD / 8;      // lanes per K/V row
-  constexpr int RPL = 64 / R;    // rows (tokens) per wave-wide load
-  constexpr int TC = U * RPL;    // tokens per chunk
-  static_assert(U % 2 == 0, "tokens are paired for the P.V dot2");
+// Online-softmax state of one row group for GT query heads: running max m
+// (log2 domain), running sum l and acc over the lane's NL*8 elements.
+template <int GT, int NL>
+struct SoftmaxState {
+  float m[GT], l[GT], acc[GT][NL * 8];
+};
 
-  const int lane = threadIdx.x;
-  const int rg = lane / R;
-  const int c = lane % R;
-  const uint32_t part = blockIdx.x;
-  const uint32_t kvh = blockIdx.y / a.n_sub;
-  const uint32_t sub = blockIdx.y - kvh * a.n_sub;
-  const uint32_t b = blockIdx.z;
-  const uint32_t h0 = kvh * a.group + sub * GT;
-  const uint32_t ng = min((uint32_t)GT, a.group - sub * GT);
-
-  uint32_t ctx = a.ctx_lens[b];
-  ctx = min(ctx, a.ctx_cap);
-  const uint32_t lo =
-      (a.window > 0 && ctx > (uint32_t)a.window) ? ctx - (uint32_t)a.window : 0;
-  const uint32_t t0 = part * a.part_tokens;
-  const uint32_t t1 = min(t0 + a.part_tokens, ctx);
-
-  if (t0 >= t1 || t1 <= lo) {
-    if (a.direct) {
-      // Only partition 0 exists; an empty context gives a zero row.
-      if (rg == 0)
-        for (uint32_t g = 0; g < ng; ++g) {
-          float4 *o = reinterpret_cast<float4 *>(
-              a.out + ((size_t)b * a.n_heads + h0 + g) * HD + c * 8);
-          o[0] = make_float4(0.f, 0.f, 0.f, 0.f);
-          o[1] = make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-    } else if (t0 < ctx && lane == 0) {
-      for (uint32_t g = 0; g < ng; ++g) {
-        size_t idx = ((size_t)b * a.n_heads + h0 + g) * a.n_parts + part;
-        a.ws_ml[idx * 2] = kNegBig;
-        a.ws_ml[idx * 2 + 1] = 0.f;
-      }
-    }
-    return;
-  }
-
-  // q for the GT heads, 8 elements per lane, pre-scaled, as f16 pairs.
-  h2 qh[GT][4];
+// One chunk of U wave-wide loads (U*RPL tokens): scores, online softmax
+// update and P.V. MASKED handles partial chunks (keys outside [lo, t1) or
+// unreadable blocks get probability 0); full chunks skip every test.
+template <int R, int GT, int U, int NL, bool MASKED>
+__device__ __forceinline__ void decode_chunk(SoftmaxState<GT, NL> &st,
+                                             const h2 (&qh)[GT][NL][4],
+                                             const uint4 (&kr)[U][NL],
+                                             const uint4 (&vr)[U][NL],
+                                             uint32_t tok0, uint32_t lo,
+                                             uint32_t t1, uint32_t okmask) {
+  constexpr int RPL = 64 / R;
+  float s[U][GT];
 #pragma unroll
-  for (int g = 0; g < GT; ++g) {
-    const uint32_t hg = h0 + ((uint32_t)g < ng ? g : 0);
-    const float4 *qp = reinterpret_cast<const float4 *>(
-        a.q + ((size_t)b * a.n_heads + hg) * HD + c * 8);
-    float4 x0 = qp[0], x1 = qp[1];
-    qh[g][0] = h2{(_Float16)(x0.x * a.qscale), (_Float16)(x0.y * a.qscale)};
-    qh[g][1] = h2{(_Float16)(x0.z * a.qscale), (_Float16)(x0.w * a.qscale)};
-    qh[g][2] = h2{(_Float16)(x1.x * a.qscale), (_Float16)(x1.y * a.qscale)};
-    qh[g][3] = h2{(_Float16)(x1.z * a.qscale), (_Float16)(x1.w * a.qscale)};
-  }
-
-  float m[GT], l[GT], acc[GT][8];
-#pragma unroll
-  for (int g = 0; g < GT; ++g) {
-    m[g] = kNegBig;
-    l[g] = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
-  }
-
-  const uint32_t bs_mask = (1u << a.bs_log2) - 1u;
-  const uint32_t last_blk = (ctx - 1) >> a.bs_log2;
-  const uint32_t *table = a.tables + (size_t)b * a.max_blocks;
-  const size_t head_off = (size_t)kvh * a.head_stride + c * 8;
-  const uint32_t start = max(t0, lo & ~(uint32_t)(RPL - 1));
-
-  // Block ids of the next chunk are fetched (scalar loads) one chunk ahead,
-  // so the K/V loads of a chunk never wait on the block table.
-  uint32_t nblk[U];
-#pragma unroll
-  for (int u = 0; u < U; ++u)
-    nblk[u] = table[min((start + u * RPL) >> a.bs_log2, last_blk)];
-
-  for (uint32_t ch = start; ch < t1; ch += TC) {
-    uint4 kr[U], vr[U];
-    bool okb[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const uint32_t tb = ch + u * RPL;  // first token of this load (uniform)
-      okb[u] = nblk[u] < a.num_blocks;
-      const uint32_t blk = okb[u] ? nblk[u] : 0;
-      const size_t off = (size_t)blk * a.block_stride + head_off +
-                         (size_t)((tb & bs_mask) + rg) * HD;
-      kr[u] = *reinterpret_cast<const uint4 *>(a.kc + off);
-      vr[u] = *reinterpret_cast<const uint4 *>(a.vc + off);
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-      nblk[u] = table[min((ch + TC + u * RPL) >> a.bs_log2, last_blk)];
-
-    float s[U][GT];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const uint32_t tok = ch + u * RPL + rg;
-      const bool valid = okb[u] && tok >= lo && tok < t1;
-#pragma unroll
-      for (int g = 0; g < GT; ++g) {
-        float d = __builtin_amdgcn_fdot2(qh[g][0], as_h2(kr[u].x), 0.f, false);
-        d = __builtin_amdgcn_fdot2(qh[g][1], as_h2(kr[u].y), d, false);
-        d = __builtin_amdgcn_fdot2(qh[g][2], as_h2(kr[u].z), d, false);
-        d = __builtin_amdgcn_fdot2(qh[g][3], as_h2(kr[u].w), d, false);
-        d = row_group_sum<R>(d);
-        s[u][g] = valid ? d : -__builtin_inff();
-      }
-    }
-
-    h2 pp[U / 2][GT];  // f16 probabilities, paired over tokens (u, u+1)
+  for (int u = 0; u < U; ++u) {
 #pragma unroll
     for (int g = 0; g < GT; ++g) {
-      float mx = m[g];
+      float d = 0.f;
 #pragma unroll
-      for (int u = 0; u < U; ++u) mx = fmaxf(mx, s[u][g]);
-      const float corr = __builtin_amdgcn_exp2f(m[g] - mx);
-      m[g] = mx;
-      float lsum = l[g] * corr;
-#pragma unroll
-      for (int u = 0; u < U; u += 2) {
-        const _Float16 p0 = (_Float16)__builtin_amdgcn_exp2f(s[u][g] - mx);
-        const _Float16 p1 = (_Float16)__builtin_amdgcn_exp2f(s[u + 1][g] - mx);
-        lsum += (float)p0 + (float)p1;
-        pp[u / 2][g] = h2{p0, p1};
+      for (int j = 0; j < NL; ++j) {
+        d = __builtin_amdgcn_fdot2(qh[g][j][0], as_h2(kr[u][j].x), d, false);
+        d = __builtin_amdgcn_fdot2(qh[g][j][1], as_h2(kr[u][j].y), d, false);
+        d = __builtin_amdgcn_fdot2(qh[g][j][2], as_h2(kr[u][j].z), d, false);
+        d = __builtin_amdgcn_fdot2(qh[g][j][3], as_h2(kr[u][j].w), d, false);
       }
-      l[g] = lsum;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[g][e] *= corr;
+      s[u][g] = row_group_sum<R>(d);
     }
+    if constexpr (MASKED) {
+      const uint32_t tok = tok0 + u * RPL;
+      const bool valid = ((okmask >> u) & 1u) && tok >= lo && tok < t1;
+#pragma unroll
+      for (int g = 0; g < GT; ++g)
+        s[u][g] = valid ? s[u][g] : -__builtin_inff();
+    }
+  }
 
+  h2 pp[U / 2][GT];  // f16 probabilities, paired over tokens (u, u+1)
+  const h2 ones = h2{(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+  for (int g = 0; g < GT; ++g) {
+    float mx = st.m[g];
+#pragma unroll
+    for (int u = 0; u < U; ++u) mx = fmaxf(mx, s[u][g]);
+    const float corr = __builtin_amdgcn_exp2f(st.m[g] - mx);
+    st.m[g] = mx;
+    float lsum = st.l[g] * corr;
 #pragma unroll
     for (int u = 0; u < U; u += 2) {
-      const uint32_t a0[4] = {vr[u].x, vr[u].y, vr[u].z, vr[u].w};
-      const uint32_t a1[4] = {vr[u + 1].x, vr[u + 1].y, vr[u + 1].z,
-                              vr[u + 1].w};
+      pp[u / 2][g] = h2{(_Float16)__builtin_amdgcn_exp2f(s[u][g] - mx),
+                        (_Float16)__builtin_amdgcn_exp2f(s[u + 1][g] - mx)};
+      // The sum uses the same rounded probabilities the P.V product does.
+      lsum = __builtin_amdgcn_fdot2(pp[u / 2][g], ones, lsum, false);
+    }
+    st.l[g] = lsum;
+#pragma unroll
+    for (int e = 0; e < NL * 8; ++e) st.acc[g][e] *= corr;
+  }
+
+#pragma unroll
+  for (int u = 0; u < U; u += 2) {
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+      const uint32_t a0[4] = {vr[u][j].x, vr[u][j].y, vr[u][j].z, vr[u][j].w};
+      const uint32_t a1[4] = {vr[u + 1][j].x, vr[u + 1][j].y,
+                              vr[u + 1][j].z, vr[u + 1][j].w};
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
         // (V[u][2w], V[u+1][2w]) and (V[u][2w+1], V[u+1][2w+1])
@@ -469,63 +402,245 @@ __global__ void __launch_bounds__(64) decode_part_kernel(DecodeArgs a) {
         const h2 hi2 = as_h2(__builtin_amdgcn_perm(a1[w], a0[w], 0x07060302u));
 #pragma unroll
         for (int g = 0; g < GT; ++g) {
-          acc[g][2 * w] =
-              __builtin_amdgcn_fdot2(pp[u / 2][g], lo2, acc[g][2 * w], false);
-          acc[g][2 * w + 1] = __builtin_amdgcn_fdot2(pp[u / 2][g], hi2,
-                                                     acc[g][2 * w + 1], false);
+          float &x0 = st.acc[g][j * 8 + 2 * w];
+          float &x1 = st.acc[g][j * 8 + 2 * w + 1];
+          x0 = __builtin_amdgcn_fdot2(pp[u / 2][g], lo2, x0, false);
+          x1 = __builtin_amdgcn_fdot2(pp[u / 2][g], hi2, x1, false);
         }
-      }
-    }
-  }
-
-  // Merge the RPL row groups of the wave (lanes c, c+R, c+2R, ...).
-#pragma unroll
-  for (int g = 0; g < GT; ++g) {
-#pragma unroll
-    for (int off = R; off < 64; off <<= 1) {
-      const float mo = __shfl_xor(m[g], off);
-      const float lo_ = __shfl_xor(l[g], off);
-      const float mx = fmaxf(m[g], mo);
-      const float ws = __builtin_amdgcn_exp2f(m[g] - mx);
-      const float wo = __builtin_amdgcn_exp2f(mo - mx);
-      l[g] = l[g] * ws + lo_ * wo;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float ao = __shfl_xor(acc[g][e], off);
-        acc[g][e] = acc[g][e] * ws + ao * wo;
-      }
-      m[g] = mx;
-    }
-  }
-
-  if (rg != 0) return;
-#pragma unroll
-  for (int g = 0; g < GT; ++g) {
-    if ((uint32_t)g >= ng) break;
-    const size_t hrow = (size_t)b * a.n_heads + h0 + g;
-    if (a.direct) {
-      const float inv = 1.0f / l[g];
-      float4 *o = reinterpret_cast<float4 *>(a.out + hrow * HD + c * 8);
-      o[0] = make_float4(acc[g][0] * inv, acc[g][1] * inv, acc[g][2] * inv,
-                         acc[g][3] * inv);
-      o[1] = make_float4(acc[g][4] * inv, acc[g][5] * inv, acc[g][6] * inv,
-                         acc[g][7] * inv);
-    } else {
-      const size_t idx = hrow * a.n_parts + part;
-      float4 *o = reinterpret_cast<float4 *>(a.ws_acc + idx * HD + c * 8);
-      o[0] = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
-      o[1] = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
-      if (c == 0) {
-        a.ws_ml[idx * 2] = m[g];
-        a.ws_ml[idx * 2 + 1] = l[g];
       }
     }
   }
 }
 
-// Reduction pass: one wave per (sequence, query head) merges the written
-// partitions: M = max m_i, out = sum_i 2^(m_i - M) acc_i / sum_i 2^(m_i - M)
-// l_i. Partitions that saw no valid key carry l = 0 and are skipped.
+// Lane mapping: a K/V row of HD f16 is R = HD/(8*NL) lanes; lane c of a
+// row group holds elements (j*R + c)*8 .. +7 for j < NL, so load j of a
+// wave covers bytes [j*R*16, (j+1)*R*16) of RPL = 64/R consecutive rows:
+// every wave-wide load instruction reads whole contiguous runs.
+// Decode kernel: one workgroup of W = blockDim.x/64 wavefronts per
+// (sequence, KV head, query sub-group, context partition). The waves take
+// the partition's chunks of TC tokens round-robin (wave w: chunks w, w+W,
+// ...), so the W waves of a workgroup stream neighbouring tiles together.
+// Each wave keeps per-row-group online-softmax state in registers, merges
+// its row groups with cross-lane shuffles, then the W wave results merge
+// through LDS. A workgroup covering the whole context writes the
+// normalised output; otherwise it writes its partial (m, l, acc) and the
+// reduction kernel merges the partitions.
+template <int HD, int GT, int U, int NL>
+__global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
+  constexpr int R = HD / (8 * NL);  // lanes per K/V row
+  constexpr int RPL = 64 / R;       // rows (tokens) per wave-wide load
+  constexpr int TC = U * RPL;       // tokens per chunk
+  static_assert(U % 2 == 0, "tokens are paired for the P.V dot2");
+  static_assert(R >= 2 && R <= 32, "row must span 2..32 lanes");
+  extern __shared__ float lds[];  // [W][GT][HD + 2]
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int W = blockDim.x >> 6;
+  const int rg = lane / R;
+  const int c = lane % R;
+  const uint32_t part = blockIdx.x;
+  const uint32_t hy = blockIdx.y;  // (KV head, query sub-group)
+  const uint32_t kvh = hy / a.n_sub;
+  const uint32_t sub = hy - kvh * a.n_sub;
+  const uint32_t b = blockIdx.z;
+  const uint32_t h0 = kvh * a.group + sub * GT;
+  const uint32_t ng = min((uint32_t)GT, a.group - sub * GT);
+  const uint32_t *table = a.tables + (size_t)b * a.max_blocks;
+  const uint32_t t0 = part * a.part_tokens;
+  const uint32_t first = t0 + (uint32_t)wave * TC;  // this wave's 1st chunk
+
+  // The first block ids depend only on the partition: their scalar loads go
+  // out together with the ctx_len load (clamped to the table for now).
+  const uint32_t mb1 = a.max_blocks - 1;
+  uint32_t ids[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    ids[u] = table[min((first + u * RPL) >> a.bs_log2, mb1)];
+
+  // q rows of the GT heads (this lane's elements) are loaded up front too.
+  float4 qraw[GT][NL][2];
+#pragma unroll
+  for (int g = 0; g < GT; ++g) {
+    const uint32_t hg = h0 + ((uint32_t)g < ng ? g : 0);
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+      const float4 *qp = reinterpret_cast<const float4 *>(
+          a.q + ((size_t)b * a.n_heads + hg) * HD + (j * R + c) * 8);
+      qraw[g][j][0] = qp[0];
+      qraw[g][j][1] = qp[1];
+    }
+  }
+
+  uint32_t ctx = a.ctx_lens[b];
+  ctx = min(ctx, a.ctx_cap);
+  const uint32_t lo =
+      (a.window > 0 && ctx > (uint32_t)a.window) ? ctx - (uint32_t)a.window : 0;
+  const uint32_t t1 = min(t0 + a.part_tokens, ctx);
+
+  if (t0 >= t1) {
+    // Past the end of this sequence (the reduction never reads it). An
+    // empty sequence (ctx_len 0) gets a zero row from its partition 0.
+    if (ctx == 0 && part == 0 && wave == 0 && rg == 0)
+      for (uint32_t g = 0; g < ng; ++g)
+#pragma unroll
+        for (int j = 0; j < NL; ++j) {
+          float4 *o = reinterpret_cast<float4 *>(
+              a.out + ((size_t)b * a.n_heads + h0 + g) * HD + (j * R + c) * 8);
+          o[0] = make_float4(0.f, 0.f, 0.f, 0.f);
+          o[1] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    return;
+  }
+
+  SoftmaxState<GT, NL> st;
+#pragma unroll
+  for (int g = 0; g < GT; ++g) {
+    st.m[g] = kNegBig;
+    st.l[g] = 0.f;
+#pragma unroll
+    for (int e = 0; e < NL * 8; ++e) st.acc[g][e] = 0.f;
+  }
+
+  // Chunks start at multiples of TC inside the partition; the window's
+  // lower edge skips whole chunks below it.
+  const uint32_t skip = lo > t0 ? (lo - t0) / (TC * W) * (TC * W) : 0;
+  const uint32_t start = first + skip;
+  if (start < t1) {
+    // q for the GT heads, this lane's elements, pre-scaled, as f16 pairs.
+    h2 qh[GT][NL][4];
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+#pragma unroll
+      for (int j = 0; j < NL; ++j) {
+        const float sc = a.qscale;
+        const float4 x0 = qraw[g][j][0], x1 = qraw[g][j][1];
+        qh[g][j][0] = h2{(_Float16)(x0.x * sc), (_Float16)(x0.y * sc)};
+        qh[g][j][1] = h2{(_Float16)(x0.z * sc), (_Float16)(x0.w * sc)};
+        qh[g][j][2] = h2{(_Float16)(x1.x * sc), (_Float16)(x1.y * sc)};
+        qh[g][j][3] = h2{(_Float16)(x1.z * sc), (_Float16)(x1.w * sc)};
+      }
+    }
+
+    const uint32_t bs_mask = (1u << a.bs_log2) - 1u;
+    const uint32_t last_blk = (ctx - 1) >> a.bs_log2;
+    // Byte offsets: the uniform part (block, head, first row of the load)
+    // is scalar; the per-lane part is a constant 32-bit offset.
+    const char *kbase = reinterpret_cast<const char *>(a.kc) +
+                        (size_t)kvh * a.head_stride * 2;
+    const char *vbase = reinterpret_cast<const char *>(a.vc) +
+                        (size_t)kvh * a.head_stride * 2;
+    const uint32_t lane_off = (uint32_t)(rg * HD * 2 + c * 16);
+    const uint64_t blk_bytes = a.block_stride * 2;
+    const uint32_t stride = (uint32_t)W * TC;
+    if (skip != 0 || last_blk < ((first + TC - 1) >> a.bs_log2)) {
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        ids[u] = table[min((start + u * RPL) >> a.bs_log2, last_blk)];
+    }
+
+    for (uint32_t ch = start; ch < t1; ch += stride) {
+      uint4 kr[U][NL], vr[U][NL];
+      uint32_t okmask = 0;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const uint32_t tb = ch + u * RPL;  // first token of this load
+        const bool ok = ids[u] < a.num_blocks;
+        okmask |= (uint32_t)ok << u;
+        const uint64_t uoff = (uint64_t)(ok ? ids[u] : 0u) * blk_bytes +
+                              (uint64_t)(tb & bs_mask) * (HD * 2);
+        const char *kp = kbase + uoff + lane_off;
+        const char *vp = vbase + uoff + lane_off;
+#pragma unroll
+        for (int j = 0; j < NL; ++j) {
+          kr[u][j] = *reinterpret_cast<const uint4 *>(kp + j * R * 16);
+          vr[u][j] = *reinterpret_cast<const uint4 *>(vp + j * R * 16);
+        }
+      }
+      // Block ids of this wave's next chunk: scalar loads one chunk ahead.
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        ids[u] = table[min((ch + stride + u * RPL) >> a.bs_log2, last_blk)];
+
+      const bool full = ch >= lo && ch + TC <= t1 && okmask == (1u << U) - 1u;
+      if (full)
+        decode_chunk<R, GT, U, NL, false>(st, qh, kr, vr, ch + rg, lo, t1,
+                                          okmask);
+      else
+        decode_chunk<R, GT, U, NL, true>(st, qh, kr, vr, ch + rg, lo, t1,
+                                         okmask);
+    }
+
+    // Merge the RPL row groups of the wave (lanes c, c+R, c+2R, ...).
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+#pragma unroll
+      for (int off = R; off < 64; off <<= 1) {
+        const float mo = __shfl_xor(st.m[g], off);
+        const float lo_ = __shfl_xor(st.l[g], off);
+        const float mx = fmaxf(st.m[g], mo);
+        const float ws = __builtin_amdgcn_exp2f(st.m[g] - mx);
+        const float wo = __builtin_amdgcn_exp2f(mo - mx);
+        st.l[g] = st.l[g] * ws + lo_ * wo;
+#pragma unroll
+        for (int e = 0; e < NL * 8; ++e) {
+          const float ao = __shfl_xor(st.acc[g][e], off);
+          st.acc[g][e] = st.acc[g][e] * ws + ao * wo;
+        }
+        st.m[g] = mx;
+      }
+    }
+  }
+
+  // Merge the W waves through LDS: wave w stores [g][m, l, acc[HD]].
+  constexpr int ROW = HD + 2;
+  if (rg == 0) {
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+      float *r = lds + ((size_t)wave * GT + g) * ROW;
+      if (c == 0) {
+        r[0] = st.m[g];
+        r[1] = st.l[g];
+      }
+#pragma unroll
+      for (int j = 0; j < NL; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) r[2 + (j * R + c) * 8 + e] = st.acc[g][j * 8 + e];
+    }
+  }
+  __syncthreads();
+
+  // Each thread finishes (g, d) elements of the GT x HD result.
+  for (int i = threadIdx.x; i < GT * HD; i += blockDim.x) {
+    const int g = i / HD, d = i - g * HD;
+    if ((uint32_t)g >= ng) break;
+    float M = kNegBig;
+    for (int w = 0; w < W; ++w) M = fmaxf(M, lds[((size_t)w * GT + g) * ROW]);
+    float L = 0.f, x = 0.f;
+    for (int w = 0; w < W; ++w) {
+      const float *r = lds + ((size_t)w * GT + g) * ROW;
+      const float wt = __builtin_amdgcn_exp2f(r[0] - M);
+      L += r[1] * wt;
+      x += r[2 + d] * wt;
+    }
+    const size_t hrow = (size_t)b * a.n_heads + h0 + g;
+    if (a.direct) {
+      a.out[hrow * HD + d] = x / L;
+    } else {
+      const size_t idx = hrow * a.n_parts + part;
+      a.ws_acc[idx * HD + d] = x;
+      if (d == 0) {
+        a.ws_ml[idx * 2] = M;
+        a.ws_ml[idx * 2 + 1] = L;
+      }
+    }
+  }
+}
+
+// Reduction pass (only when a sequence spans several partitions): one wave
+// per (sequence, query head) merges the written partitions: M = max m_i,
+// out = sum_i 2^(m_i - M) acc_i / sum_i 2^(m_i - M) l_i. Partitions that
+// saw no visible key carry l = 0 and are skipped.
 template <int HD>
 __global__ void __launch_bounds__(64) decode_reduce_kernel(DecodeArgs a) {
   constexpr int EPL = HD / 64 > 0 ? HD / 64 : 1;  // elements per lane
@@ -592,15 +707,36 @@ void subgroups(uint32_t group, uint32_t *n_sub, uint32_t *gt) {
 // Tokens per context partition: the smallest power of two >= 256 for which
 // the grid has at most ~8192 partition waves (32 per CU on 256 CUs), so long
 // contexts keep enough waves in flight without a large reduction.
+// Tuning overrides (RVKV_DECODE_PART_TOKENS, RVKV_DECODE_UNROLL); 0 = auto.
+uint32_t env_u32(const char *name) {
+  const char *v = getenv(name);
+  return v ? (uint32_t)strtoul(v, nullptr, 10) : 0u;
+}
+
 uint32_t partition_tokens(const rvkv_pool *p, uint32_t batch, uint32_t n_heads,
                           uint32_t max_ctx) {
+  static const uint32_t forced = env_u32("RVKV_DECODE_PART_TOKENS");
+  if (forced >= 256 && (forced & (forced - 1)) == 0) return forced;
   uint32_t group = n_heads / (p->n_kv ? p->n_kv : 1);
   uint32_t n_sub, gt;
   subgroups(group ? group : 1, &n_sub, &gt);
   const uint64_t pairs = (uint64_t)batch * p->n_kv * n_sub;
+  // Enough workgroups for two per CU (256 CUs); a whole context per
+  // workgroup whenever the batch alone provides that many.
+  const uint64_t want = 512;
+  const uint64_t parts = pairs >= want ? 1 : (want + pairs - 1) / pairs;
+  const uint64_t per = (max_ctx + parts - 1) / parts;
   uint32_t P = 256;
-  while (P < 8192 && pairs * div_up(max_ctx ? max_ctx : 1, P) > 8192) P *= 2;
+  while (P < per && P < (1u << 30)) P <<= 1;
   return P;
+}
+
+// Wavefronts per decode workgroup: enough that the grid holds ~2048 waves
+// (8 per CU) when the batch is small; RVKV_DECODE_WAVES overrides.
+uint32_t decode_waves(uint64_t workgroups) {
+  static const uint32_t forced = env_u32("RVKV_DECODE_WAVES");
+  if (forced == 1 || forced == 2 || forced == 4) return forced;
+  return workgroups >= 2048 ? 1 : workgroups >= 1024 ? 2 : 4;
 }
 
 struct WsLayout {
@@ -623,8 +759,16 @@ WsLayout ws_layout(const rvkv_pool *p, uint32_t batch, uint32_t n_heads,
 
 template <int HD, int GT>
 void launch_decode(const DecodeArgs &a, dim3 grid, hipStream_t st) {
-  constexpr int U = GT <= 4 ? 8 : 4;
-  hipLaunchKernelGGL((decode_part_kernel<HD, GT, U>), grid, dim3(64), 0, st, a);
+  static const uint32_t forced_u = env_u32("RVKV_DECODE_UNROLL");
+  const bool u8 = forced_u ? forced_u == 8 : (HD >= 256 || GT >= 5);
+  const uint32_t W = decode_waves((uint64_t)grid.x * grid.y * grid.z);
+  const size_t lds = (size_t)W * GT * (HD + 2) * sizeof(float);
+  if (u8)
+    hipLaunchKernelGGL((decode_part_kernel<HD, GT, 8, 1>), grid, dim3(64 * W),
+                       lds, st, a);
+  else
+    hipLaunchKernelGGL((decode_part_kernel<HD, GT, 4, 1>), grid, dim3(64 * W),
+                       lds, st, a);
 }
 
 template <int HD>

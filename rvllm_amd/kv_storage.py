@@ -97,6 +97,13 @@ class HipKvStorage:
         except Exception:
             pass
 
+    def set_stream(self, stream) -> None:
+        """Rebinds the pool to another stream (e.g. a graph-capture stream);
+        later calls enqueue there."""
+        check(self._L.rvkv_pool_set_stream(
+            self._pool, ctypes.c_void_p(stream.cuda_stream)))
+        self.stream = stream
+
     @property
     def nbytes(self) -> int:
         return self._L.rvkv_pool_bytes(self._pool)
