@@ -39,6 +39,10 @@ def parse():
                    help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="wall-clock budget of the CPU baseline sample")
+    p.add_argument("--plan", dest="plan", action="store_true", default=None,
+                   help="decode through a per-step decode plan (default: "
+                        "only for ragged batches)")
+    p.add_argument("--no-plan", dest="plan", action="store_false")
     p.add_argument("--graph", action="store_true",
                    help="time the step as one HIP graph replay (all layers' "
                         "append + decode launches captured once)")
@@ -201,16 +205,32 @@ def main():
     out = [torch.empty_like(q[0]) for _ in range(L)]
     ws = st.alloc_workspace(B, c.n_heads, max_ctx)
     part = st.decode_partition_tokens(B, c.n_heads, max_ctx)
+    # Ragged batches use the per-forward decode plan, rebuilt every step from
+    # the host-side context lengths (as the engine's GatherPlan is).
+    plan = None
+    if args.plan or (args.plan is None and
+                     int(db.ctx_lens.min()) != int(db.ctx_lens.max())):
+        from rvllm_amd.kv_storage import HipDecodePlan
+        plan = HipDecodePlan(st, db.ctx_lens, c.n_heads)
+        if args.graph:
+            raise SystemExit("--graph cannot capture the per-step plan "
+                             "rebuild; use --no-plan with --graph")
 
     ev = None
 
     def step(record=False):
+        if plan is not None:
+            plan.update(db.ctx_lens)
         for layer in range(L):
             st.write_tokens(layer, sb, so, nk[layer], nv[layer])
             if record:
                 ev[layer][0].record()
-            st.paged_decode(layer, q[layer], tables, ctx, max_ctx,
-                            out=out[layer], ws=ws)
+            if plan is not None:
+                st.paged_decode_planned(layer, plan, q[layer], tables, ctx,
+                                        out=out[layer])
+            else:
+                st.paged_decode(layer, q[layer], tables, ctx, max_ctx,
+                                out=out[layer], ws=ws)
             if record:
                 ev[layer][1].record()
 
@@ -276,7 +296,8 @@ def main():
             "seq_len": max_ctx,
             "parallelism": "single GPU",
             "launch": "hip graph" if args.graph else "eager",
-            "partition_tokens": part,
+            "partition_tokens": None if plan is not None else part,
+            "decode_plan_items": plan.items if plan is not None else None,
         },
         "pct_of_peak": round(100 * step_bytes / dt / 1e9 / HBM_PEAK_GBS, 2),
         "tok_per_s": round(B / dt, 1),

@@ -136,9 +136,48 @@ size_t rvkv_decode_workspace_bytes(const rvkv_pool *pool, uint32_t batch,
                                    uint32_t n_heads, uint32_t max_ctx_len);
 
 /* Tokens per context partition rvkv_paged_decode will use for this shape
- * (each partition is one wavefront per (sequence, KV head)). */
+ * (each partition is one workgroup per (sequence, KV head)). */
 uint32_t rvkv_decode_partition_tokens(const rvkv_pool *pool, uint32_t batch,
                                       uint32_t n_heads, uint32_t max_ctx_len);
+
+/* ---- a3 + a5 + a6: planned paged decode (ragged batches) ------------------
+ * The counterpart of GatherPlan::new / CudaGatherPlan::new
+ * (src/kv_storage.rs:50-75, src/cuda/kv_storage.rs:26-54): built once per
+ * forward from the host-side read_num_tokens (BatchItem::read_num_tokens,
+ * src/model.rs:430-433) and shared by every layer. It splits each
+ * sequence's visible context into work items of at most part_tokens tokens,
+ * orders them longest first so ragged batches balance across the GPU, sends
+ * single-item sequences straight to the output and reduces only the split
+ * ones. Creating a plan allocates device and pinned host memory for the
+ * item list and uploads it on the pool's stream.
+ * The device ctx_lens given to rvkv_paged_decode_planned must equal the
+ * host ones the plan was built from (larger values are clamped to them). */
+typedef struct rvkv_decode_plan rvkv_decode_plan;
+
+int rvkv_decode_plan_create(const rvkv_pool *pool,
+                            const uint32_t *ctx_lens_host, uint32_t batch,
+                            uint32_t n_heads, int32_t window,
+                            rvkv_decode_plan **out);
+/* Rebuilds the plan in place for this step's context lengths (same n_heads
+ * and window; batch may change), reusing its device and pinned buffers
+ * unless the work list outgrows them. Waits only for the plan's own previous
+ * upload. The plan keeps a pointer to the pool: destroy it first. */
+int rvkv_decode_plan_update(rvkv_decode_plan *plan,
+                            const uint32_t *ctx_lens_host, uint32_t batch);
+/* Waits for the pool's stream (queued decodes may read the plan), frees. */
+void rvkv_decode_plan_destroy(rvkv_decode_plan *plan);
+/* Device scratch rvkv_paged_decode_planned needs (0 if nothing is split). */
+size_t rvkv_decode_plan_workspace_bytes(const rvkv_decode_plan *plan);
+/* Work items (workgroups per KV head) of the plan. */
+uint32_t rvkv_decode_plan_items(const rvkv_decode_plan *plan);
+/* Same contract as rvkv_paged_decode, with batch, n_heads, window and the
+ * context bound taken from the plan. */
+int rvkv_paged_decode_planned(const rvkv_pool *pool,
+                              const rvkv_decode_plan *plan, uint32_t layer,
+                              const float *q, const uint32_t *block_tables,
+                              const uint32_t *ctx_lens, uint32_t max_blocks,
+                              float scale, float *out, void *ws,
+                              size_t ws_bytes);
 
 /* ---- a10: prefix-cache copy-on-write -------------------------------------
  * No counterpart in the reference (rvllm never mutates a shared block; its

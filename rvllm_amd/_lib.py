@@ -33,6 +33,14 @@ SIGNATURES = {
                                  _f32, _i32, _P, _P, _sz]),
     "rvkv_decode_workspace_bytes": (_sz, [_P, _u32, _u32, _u32]),
     "rvkv_decode_partition_tokens": (_u32, [_P, _u32, _u32, _u32]),
+    "rvkv_decode_plan_create": (_int, [_P, _P, _u32, _u32, _i32,
+                                       ctypes.POINTER(_P)]),
+    "rvkv_decode_plan_update": (_int, [_P, _P, _u32]),
+    "rvkv_decode_plan_destroy": (None, [_P]),
+    "rvkv_decode_plan_workspace_bytes": (_sz, [_P]),
+    "rvkv_decode_plan_items": (_u32, [_P]),
+    "rvkv_paged_decode_planned": (_int, [_P, _P, _u32, _P, _P, _P, _u32, _f32,
+                                         _P, _P, _sz]),
     "rvkv_copy_blocks": (_int, [_P, _P, _P, _u32]),
     "rvkv_read_blocks": (_int, [_P, _u32, _u32, _P, _u32, _P]),
     "rvkv_block_checksums": (_int, [_P, _u32, _u32, _P, _u32, _P]),

@@ -15,7 +15,9 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <algorithm>
 #include <string>
+#include <vector>
 
 #include "../../include/rvkv.h"
 
@@ -289,16 +291,25 @@ struct DecodeArgs {
   float *out;
   const uint32_t *tables;
   const uint32_t *ctx_lens;
-  float *ws_acc;     // [batch][n_heads][n_parts][hd]
-  float *ws_ml;      // [batch][n_heads][n_parts][2]
+  // Partial results of split sequences, indexed by (slot * n_heads + head):
+  // acc [slots][n_heads][hd], (m, l) [slots][n_heads][2].
+  float *ws_acc;
+  float *ws_ml;
+  // Planned mode: work items {seq, first token, end token, slot} (slot
+  // kNoSlot = the item is the whole visible context: write the output) and
+  // reduction rows {seq, first slot, slot count, 0}. NULL: uniform mode,
+  // where grid.x = partition and slot = seq * n_parts + partition.
+  const uint4 *items;
+  const uint4 *reds;
   uint64_t block_stride;  // elements per block (all heads)
   uint32_t head_stride;   // elements per (block, head) tile
   uint32_t max_blocks, num_blocks, n_kv, n_heads, group, n_sub;
   uint32_t bs_log2, part_tokens, n_parts, ctx_cap;
   float qscale;
   int32_t window;
-  int32_t direct;
 };
+
+constexpr uint32_t kNoSlot = 0xFFFFFFFFu;
 
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {
@@ -439,15 +450,25 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
   const int W = blockDim.x >> 6;
   const int rg = lane / R;
   const int c = lane % R;
-  const uint32_t part = blockIdx.x;
   const uint32_t hy = blockIdx.y;  // (KV head, query sub-group)
   const uint32_t kvh = hy / a.n_sub;
   const uint32_t sub = hy - kvh * a.n_sub;
-  const uint32_t b = blockIdx.z;
+  uint32_t b, t0, tend, slot;
+  if (a.items) {  // planned: one work item per grid.x
+    const uint4 it = a.items[blockIdx.x];
+    b = it.x;
+    t0 = it.y;
+    tend = it.z;
+    slot = it.w;
+  } else {  // uniform: fixed-size partitions of every sequence
+    b = blockIdx.z;
+    t0 = blockIdx.x * a.part_tokens;
+    tend = t0 + a.part_tokens;
+    slot = a.n_parts > 1 ? b * a.n_parts + blockIdx.x : kNoSlot;
+  }
   const uint32_t h0 = kvh * a.group + sub * GT;
   const uint32_t ng = min((uint32_t)GT, a.group - sub * GT);
   const uint32_t *table = a.tables + (size_t)b * a.max_blocks;
-  const uint32_t t0 = part * a.part_tokens;
   const uint32_t first = t0 + (uint32_t)wave * TC;  // this wave's 1st chunk
 
   // The first block ids depend only on the partition: their scalar loads go
@@ -476,12 +497,14 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
   ctx = min(ctx, a.ctx_cap);
   const uint32_t lo =
       (a.window > 0 && ctx > (uint32_t)a.window) ? ctx - (uint32_t)a.window : 0;
-  const uint32_t t1 = min(t0 + a.part_tokens, ctx);
+  const uint32_t t1 = min(tend, ctx);
+  // A sequence that one partition covers writes its output directly.
+  if (!a.items && ctx <= a.part_tokens) slot = kNoSlot;
 
   if (t0 >= t1) {
     // Past the end of this sequence (the reduction never reads it). An
-    // empty sequence (ctx_len 0) gets a zero row from its partition 0.
-    if (ctx == 0 && part == 0 && wave == 0 && rg == 0)
+    // empty sequence (ctx_len 0) gets a zero row from its first partition.
+    if (ctx == 0 && t0 == 0 && wave == 0 && rg == 0)
       for (uint32_t g = 0; g < ng; ++g)
 #pragma unroll
         for (int j = 0; j < NL; ++j) {
@@ -623,11 +646,10 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
       L += r[1] * wt;
       x += r[2 + d] * wt;
     }
-    const size_t hrow = (size_t)b * a.n_heads + h0 + g;
-    if (a.direct) {
-      a.out[hrow * HD + d] = x / L;
+    if (slot == kNoSlot) {
+      a.out[((size_t)b * a.n_heads + h0 + g) * HD + d] = x / L;
     } else {
-      const size_t idx = hrow * a.n_parts + part;
+      const size_t idx = (size_t)slot * a.n_heads + h0 + g;
       a.ws_acc[idx * HD + d] = x;
       if (d == 0) {
         a.ws_ml[idx * 2] = M;
@@ -637,24 +659,34 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
   }
 }
 
-// Reduction pass (only when a sequence spans several partitions): one wave
-// per (sequence, query head) merges the written partitions: M = max m_i,
-// out = sum_i 2^(m_i - M) acc_i / sum_i 2^(m_i - M) l_i. Partitions that
-// saw no visible key carry l = 0 and are skipped.
+// Reduction pass (only for sequences split over several partitions): one
+// wave per (sequence, query head) merges its partitions: M = max m_i,
+// out = sum_i 2^(m_i - M) acc_i / sum_i 2^(m_i - M) l_i. Partitions that saw
+// no visible key carry l = 0 and are skipped.
 template <int HD>
 __global__ void __launch_bounds__(64) decode_reduce_kernel(DecodeArgs a) {
   constexpr int EPL = HD / 64 > 0 ? HD / 64 : 1;  // elements per lane
-  const uint32_t h = blockIdx.x, b = blockIdx.y;
+  const uint32_t h = blockIdx.x;
   const int lane = threadIdx.x;
-  const uint32_t ctx = min(a.ctx_lens[b], a.ctx_cap);
-  const uint32_t np = (ctx + a.part_tokens - 1) / a.part_tokens;
-  const size_t hrow = (size_t)b * a.n_heads + h;
+  uint32_t b, slot0, np;
+  if (a.reds) {
+    const uint4 r = a.reds[blockIdx.y];
+    b = r.x;
+    slot0 = r.y;
+    np = r.z;
+  } else {
+    b = blockIdx.y;
+    const uint32_t ctx = min(a.ctx_lens[b], a.ctx_cap);
+    if (ctx <= a.part_tokens) return;  // written directly
+    slot0 = b * a.n_parts;
+    np = (ctx + a.part_tokens - 1) / a.part_tokens;
+  }
   float acc[EPL];
 #pragma unroll
   for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
   float M = kNegBig, L = 0.f;
   for (uint32_t p = 0; p < np; ++p) {
-    const size_t idx = hrow * a.n_parts + p;
+    const size_t idx = (size_t)(slot0 + p) * a.n_heads + h;
     const float mp = a.ws_ml[idx * 2], lp = a.ws_ml[idx * 2 + 1];
     if (lp == 0.f) continue;
     const float mx = fmaxf(M, mp);
@@ -670,6 +702,7 @@ __global__ void __launch_bounds__(64) decode_reduce_kernel(DecodeArgs a) {
     M = mx;
   }
   const float inv = L > 0.f ? 1.0f / L : 0.f;
+  const size_t hrow = (size_t)b * a.n_heads + h;
 #pragma unroll
   for (int e = 0; e < EPL; ++e) {
     const int d = lane * EPL + e;
@@ -760,8 +793,11 @@ WsLayout ws_layout(const rvkv_pool *p, uint32_t batch, uint32_t n_heads,
 template <int HD, int GT>
 void launch_decode(const DecodeArgs &a, dim3 grid, hipStream_t st) {
   static const uint32_t forced_u = env_u32("RVKV_DECODE_UNROLL");
-  const bool u8 = forced_u ? forced_u == 8 : (HD >= 256 || GT >= 5);
   const uint32_t W = decode_waves((uint64_t)grid.x * grid.y * grid.z);
+  // Eight loads per chunk pay off for 512-byte rows and for large groups
+  // in single-wave workgroups; otherwise four keep more waves resident.
+  const bool u8 =
+      forced_u ? forced_u == 8 : (HD >= 256 || (GT >= 5 && W == 1));
   const size_t lds = (size_t)W * GT * (HD + 2) * sizeof(float);
   if (u8)
     hipLaunchKernelGGL((decode_part_kernel<HD, GT, 8, 1>), grid, dim3(64 * W),
@@ -960,16 +996,20 @@ size_t rvkv_decode_workspace_bytes(const rvkv_pool *pool, uint32_t batch,
   return ws_layout(pool, batch, n_heads, max_ctx_len).bytes;
 }
 
-int rvkv_paged_decode(const rvkv_pool *pool, uint32_t layer, const float *q,
-                      const uint32_t *block_tables, const uint32_t *ctx_lens,
-                      uint32_t batch, uint32_t max_blocks, uint32_t n_heads,
-                      uint32_t max_ctx_len, float scale, int32_t window,
-                      float *out, void *ws, size_t ws_bytes) {
-  const char *op = "paged_decode";
+}  // extern "C"
+
+namespace {
+
+// Checks what every decode entry point needs and fills the common part of
+// DecodeArgs; returns 0 or an error code (message already set).
+int prepare_decode(const char *op, const rvkv_pool *pool, uint32_t layer,
+                   const float *q, const uint32_t *block_tables,
+                   const uint32_t *ctx_lens, uint32_t max_blocks,
+                   uint32_t n_heads, uint32_t max_ctx_len, float scale,
+                   int32_t window, float *out, DecodeArgs *a, uint32_t *gt) {
   if (!pool) return fail(RVKV_EINVAL, op, "pool is NULL");
   if (layer >= pool->n_layers)
     return fail(RVKV_EINVAL, op, "layer out of range");
-  if (batch == 0) return RVKV_OK;
   if (max_blocks == 0) return fail(RVKV_EINVAL, op, "max_blocks must be positive");
   if (n_heads == 0 || n_heads % pool->n_kv != 0)
     return fail(RVKV_EINVAL, op,
@@ -986,59 +1026,57 @@ int rvkv_paged_decode(const rvkv_pool *pool, uint32_t layer, const float *q,
     return fail(RVKV_EINVAL, op, "NULL q/block_tables/ctx_lens/out");
   if ((uintptr_t)q % 16 || (uintptr_t)out % 16)
     return fail(RVKV_EINVAL, op, "q and out must be 16-byte aligned");
+  const uint32_t group = n_heads / pool->n_kv;
+  uint32_t n_sub;
+  subgroups(group, &n_sub, gt);
+  if ((uint64_t)pool->n_kv * n_sub > 65535)
+    return fail(RVKV_EUNSUPPORTED, op, "head count too large");
   if (max_ctx_len == 0) max_ctx_len = 1;
   const uint64_t cap64 = (uint64_t)max_blocks * bs;
-  const uint32_t cap = (uint32_t)(cap64 < max_ctx_len ? cap64 : max_ctx_len);
-  const WsLayout w = ws_layout(pool, batch, n_heads, max_ctx_len);
-  if (w.n_parts > 1) {
-    if (!ws) return fail(RVKV_EINVAL, op, "workspace is NULL");
-    if (ws_bytes < w.bytes)
-      return fail(RVKV_EINVAL, op,
-                  "workspace smaller than rvkv_decode_workspace_bytes()");
-    if ((uintptr_t)ws % 256)
-      return fail(RVKV_EINVAL, op, "workspace must be 256-byte aligned");
-  }
-  const uint32_t group = n_heads / pool->n_kv;
-  uint32_t n_sub, gt;
-  subgroups(group, &n_sub, &gt);
-  if ((uint64_t)pool->n_kv * n_sub > 65535 || batch > 65535)
-    return fail(RVKV_EUNSUPPORTED, op, "batch or head count too large");
+  *a = DecodeArgs{};
+  a->kc = pool->tensor(layer, 0);
+  a->vc = pool->tensor(layer, 1);
+  a->q = q;
+  a->out = out;
+  a->tables = block_tables;
+  a->ctx_lens = ctx_lens;
+  a->block_stride = pool->block_elems;
+  a->head_stride = bs * hd;
+  a->max_blocks = max_blocks;
+  a->num_blocks = pool->num_blocks;
+  a->n_kv = pool->n_kv;
+  a->n_heads = n_heads;
+  a->group = group;
+  a->n_sub = n_sub;
+  a->bs_log2 = ilog2(bs);
+  a->ctx_cap = (uint32_t)(cap64 < max_ctx_len ? cap64 : max_ctx_len);
+  a->qscale = scale * 1.4426950408889634f;  // log2(e)
+  a->window = window;
+  return RVKV_OK;
+}
 
-  DecodeArgs a{};
-  a.kc = pool->tensor(layer, 0);
-  a.vc = pool->tensor(layer, 1);
-  a.q = q;
-  a.out = out;
-  a.tables = block_tables;
-  a.ctx_lens = ctx_lens;
-  a.ws_acc = w.n_parts > 1 ? (float *)((char *)ws + w.acc_off) : nullptr;
-  a.ws_ml = w.n_parts > 1 ? (float *)((char *)ws + w.ml_off) : nullptr;
-  a.block_stride = pool->block_elems;
-  a.head_stride = bs * hd;
-  a.max_blocks = max_blocks;
-  a.num_blocks = pool->num_blocks;
-  a.n_kv = pool->n_kv;
-  a.n_heads = n_heads;
-  a.group = group;
-  a.n_sub = n_sub;
-  a.bs_log2 = ilog2(bs);
-  a.part_tokens = partition_tokens(pool, batch, n_heads, max_ctx_len);
-  a.n_parts = w.n_parts;
-  a.ctx_cap = cap;
-  a.qscale = scale * 1.4426950408889634f;  // log2(e)
-  a.window = window;
-  a.direct = w.n_parts <= 1;
+int check_ws(const char *op, void *ws, size_t ws_bytes, size_t need) {
+  if (need == 0) return RVKV_OK;
+  if (!ws) return fail(RVKV_EINVAL, op, "workspace is NULL");
+  if (ws_bytes < need)
+    return fail(RVKV_EINVAL, op, "workspace smaller than the required bytes");
+  if ((uintptr_t)ws % 256)
+    return fail(RVKV_EINVAL, op, "workspace must be 256-byte aligned");
+  return RVKV_OK;
+}
 
-  const dim3 grid(w.n_parts, pool->n_kv * n_sub, batch);
-  hipStream_t st = pool->stream;
+// Launches the partition kernel on `grid` and, when some sequence is split,
+// the reduction kernel on `rgrid`.
+int launch_decode_pair(const char *op, const DecodeArgs &a, uint32_t hd,
+                       uint32_t gt, dim3 grid, dim3 rgrid, bool reduce,
+                       hipStream_t st) {
   switch (hd) {
     case 32: dispatch_gt<32>(gt, a, grid, st); break;
     case 64: dispatch_gt<64>(gt, a, grid, st); break;
     case 128: dispatch_gt<128>(gt, a, grid, st); break;
     default: dispatch_gt<256>(gt, a, grid, st); break;
   }
-  if (!a.direct) {
-    const dim3 rgrid(n_heads, batch);
+  if (reduce) {
     switch (hd) {
       case 32: hipLaunchKernelGGL(decode_reduce_kernel<32>, rgrid, dim3(64), 0, st, a); break;
       case 64: hipLaunchKernelGGL(decode_reduce_kernel<64>, rgrid, dim3(64), 0, st, a); break;
@@ -1048,6 +1086,242 @@ int rvkv_paged_decode(const rvkv_pool *pool, uint32_t layer, const float *q,
   }
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? RVKV_OK : hip_fail(op, e);
+}
+
+}  // namespace
+
+struct rvkv_decode_plan {
+  const rvkv_pool *pool;
+  uint32_t batch, n_heads, n_kv, head_dim, max_ctx;
+  int32_t window;
+  uint32_t part_tokens, n_items, n_reds, n_slots;
+  uint4 *d_buf = nullptr;   // items, then reduction rows (device)
+  uint4 *h_buf = nullptr;   // pinned staging copy of the same
+  size_t cap = 0;           // entries both buffers hold
+  hipEvent_t uploaded = nullptr;  // last upload done: staging is free
+  size_t acc_off, ml_off, ws_bytes;
+};
+
+namespace {
+
+// (Re)builds the work list of `pl` for these context lengths and uploads it
+// on the pool's stream. Device-side ordering after earlier decodes comes from
+// the stream; the pinned staging buffer is reused once the previous upload
+// has completed.
+int plan_build(rvkv_decode_plan *pl, const uint32_t *ctx_lens_host,
+               uint32_t batch) {
+  const char *op = "decode_plan";
+  const rvkv_pool *pool = pl->pool;
+  uint32_t n_sub, gt;
+  subgroups(pl->n_heads / pool->n_kv, &n_sub, &gt);
+  const uint64_t n_hy = (uint64_t)pool->n_kv * n_sub;
+  const int32_t window = pl->window;
+  // Visible tokens per sequence: [lo_b, ctx_b), lo_b from the window.
+  uint64_t total = 0;
+  uint32_t max_ctx = 1;
+  for (uint32_t b = 0; b < batch; ++b) {
+    const uint32_t n = ctx_lens_host[b];
+    const uint32_t lo = (window > 0 && n > (uint32_t)window) ? n - window : 0;
+    total += n - lo;
+    if (n > max_ctx) max_ctx = n;
+  }
+  // Tokens per work item: about one sequence, but at least enough that the
+  // grid has <= ~1024 workgroups and at most what keeps >= ~256 of them.
+  const double avg = (double)total / batch;
+  const double lo_p = (double)total * n_hy / 1024.0;
+  const double hi_p = (double)total * n_hy / 256.0;
+  double want = avg < lo_p ? lo_p : avg;
+  if (want > hi_p) want = hi_p;
+  uint32_t P = 256;
+  while (P < want && P < (1u << 30)) P <<= 1;
+
+  std::vector<uint4> items, reds;
+  items.reserve(batch);
+  uint32_t slots = 0;
+  for (uint32_t b = 0; b < batch; ++b) {
+    const uint32_t n = ctx_lens_host[b];
+    if (n == 0) {  // zero row
+      items.push_back(make_uint4(b, 0, 0, kNoSlot));
+      continue;
+    }
+    const uint32_t lo = (window > 0 && n > (uint32_t)window) ? n - window : 0;
+    const uint32_t start = lo & ~255u;
+    const uint32_t k = div_up(n - start, P);
+    if (k == 1) {
+      items.push_back(make_uint4(b, start, n, kNoSlot));
+      continue;
+    }
+    for (uint32_t i = 0; i < k; ++i) {
+      const uint32_t t0 = start + i * P;
+      items.push_back(make_uint4(b, t0, t0 + P < n ? t0 + P : n, slots + i));
+    }
+    reds.push_back(make_uint4(b, slots, k, 0));
+    slots += k;
+  }
+  // Longest items first: the short tail fills in behind them.
+  std::stable_sort(items.begin(), items.end(),
+                   [](const uint4 &x, const uint4 &y) {
+                     return (x.z - x.y) > (y.z - y.y);
+                   });
+  const size_t need = items.size() + reds.size();
+  hipError_t e = hipSuccess;
+  if (pl->uploaded) e = hipEventSynchronize(pl->uploaded);
+  if (e == hipSuccess && need > pl->cap) {
+    // Growing: the old device list may still be read by queued decodes.
+    if (pl->d_buf) e = hipStreamSynchronize(pool->stream);
+    if (e == hipSuccess && pl->d_buf) e = hipFree(pl->d_buf);
+    if (e == hipSuccess && pl->h_buf) e = hipHostFree(pl->h_buf);
+    pl->d_buf = nullptr;
+    pl->h_buf = nullptr;
+    pl->cap = 0;
+    const size_t cap = need + need / 4 + 16;
+    if (e == hipSuccess) e = hipMalloc(&pl->d_buf, cap * sizeof(uint4));
+    if (e == hipSuccess) e = hipHostMalloc(&pl->h_buf, cap * sizeof(uint4));
+    if (e == hipSuccess) pl->cap = cap;
+  }
+  if (e == hipSuccess && !pl->uploaded) e = hipEventCreate(&pl->uploaded);
+  if (e != hipSuccess) return hip_fail(op, e);
+  std::copy(items.begin(), items.end(), pl->h_buf);
+  std::copy(reds.begin(), reds.end(), pl->h_buf + items.size());
+  e = hipMemcpyAsync(pl->d_buf, pl->h_buf, need * sizeof(uint4),
+                     hipMemcpyHostToDevice, pool->stream);
+  if (e == hipSuccess) e = hipEventRecord(pl->uploaded, pool->stream);
+  if (e != hipSuccess) return hip_fail(op, e);
+
+  pl->batch = batch;
+  pl->max_ctx = max_ctx;
+  pl->part_tokens = P;
+  pl->n_items = (uint32_t)items.size();
+  pl->n_reds = (uint32_t)reds.size();
+  pl->n_slots = slots;
+  const size_t ent = (size_t)slots * pl->n_heads;
+  pl->acc_off = 0;
+  pl->ml_off = (ent * pool->head_dim * 4 + 255) & ~(size_t)255;
+  pl->ws_bytes = slots ? pl->ml_off + ((ent * 2 * 4 + 255) & ~(size_t)255) : 0;
+  return RVKV_OK;
+}
+
+int plan_check_args(const char *op, const rvkv_pool *pool,
+                    const uint32_t *ctx_lens_host, uint32_t batch,
+                    uint32_t n_heads) {
+  if (!pool) return fail(RVKV_EINVAL, op, "pool is NULL");
+  if (batch == 0 || !ctx_lens_host)
+    return fail(RVKV_EINVAL, op, "batch must be positive, ctx_lens non-NULL");
+  if (batch > 65535) return fail(RVKV_EUNSUPPORTED, op, "batch too large");
+  if (n_heads == 0 || n_heads % pool->n_kv != 0)
+    return fail(RVKV_EINVAL, op,
+                "n_heads must be a positive multiple of n_kv_heads");
+  return RVKV_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int rvkv_paged_decode(const rvkv_pool *pool, uint32_t layer, const float *q,
+                      const uint32_t *block_tables, const uint32_t *ctx_lens,
+                      uint32_t batch, uint32_t max_blocks, uint32_t n_heads,
+                      uint32_t max_ctx_len, float scale, int32_t window,
+                      float *out, void *ws, size_t ws_bytes) {
+  const char *op = "paged_decode";
+  if (pool && batch == 0) return RVKV_OK;
+  DecodeArgs a;
+  uint32_t gt;
+  int rc = prepare_decode(op, pool, layer, q, block_tables, ctx_lens,
+                          max_blocks, n_heads, max_ctx_len, scale, window,
+                          out, &a, &gt);
+  if (rc) return rc;
+  if (batch > 65535) return fail(RVKV_EUNSUPPORTED, op, "batch too large");
+  if (max_ctx_len == 0) max_ctx_len = 1;
+  const WsLayout w = ws_layout(pool, batch, n_heads, max_ctx_len);
+  if ((rc = check_ws(op, ws, ws_bytes, w.bytes))) return rc;
+  a.ws_acc = w.n_parts > 1 ? (float *)((char *)ws + w.acc_off) : nullptr;
+  a.ws_ml = w.n_parts > 1 ? (float *)((char *)ws + w.ml_off) : nullptr;
+  a.part_tokens = partition_tokens(pool, batch, n_heads, max_ctx_len);
+  a.n_parts = w.n_parts;
+  const dim3 grid(w.n_parts, pool->n_kv * a.n_sub, batch);
+  return launch_decode_pair(op, a, pool->head_dim, gt, grid,
+                            dim3(n_heads, batch), w.n_parts > 1, pool->stream);
+}
+
+int rvkv_decode_plan_create(const rvkv_pool *pool,
+                            const uint32_t *ctx_lens_host, uint32_t batch,
+                            uint32_t n_heads, int32_t window,
+                            rvkv_decode_plan **out) {
+  const char *op = "decode_plan";
+  if (!out) return fail(RVKV_EINVAL, op, "out is NULL");
+  *out = nullptr;
+  int rc = plan_check_args(op, pool, ctx_lens_host, batch, n_heads);
+  if (rc) return rc;
+  rvkv_decode_plan *pl = new rvkv_decode_plan();
+  pl->pool = pool;
+  pl->n_heads = n_heads;
+  pl->n_kv = pool->n_kv;
+  pl->head_dim = pool->head_dim;
+  pl->window = window;
+  if ((rc = plan_build(pl, ctx_lens_host, batch))) {
+    rvkv_decode_plan_destroy(pl);
+    return rc;
+  }
+  *out = pl;
+  return RVKV_OK;
+}
+
+int rvkv_decode_plan_update(rvkv_decode_plan *plan,
+                            const uint32_t *ctx_lens_host, uint32_t batch) {
+  const char *op = "decode_plan";
+  if (!plan) return fail(RVKV_EINVAL, op, "plan is NULL");
+  int rc = plan_check_args(op, plan->pool, ctx_lens_host, batch,
+                           plan->n_heads);
+  if (rc) return rc;
+  return plan_build(plan, ctx_lens_host, batch);
+}
+
+void rvkv_decode_plan_destroy(rvkv_decode_plan *plan) {
+  if (!plan) return;
+  // Decodes queued with this plan may still read its device list.
+  (void)hipStreamSynchronize(plan->pool->stream);
+  if (plan->uploaded) (void)hipEventDestroy(plan->uploaded);
+  if (plan->d_buf) (void)hipFree(plan->d_buf);
+  if (plan->h_buf) (void)hipHostFree(plan->h_buf);
+  delete plan;
+}
+
+size_t rvkv_decode_plan_workspace_bytes(const rvkv_decode_plan *plan) {
+  return plan ? plan->ws_bytes : 0;
+}
+
+uint32_t rvkv_decode_plan_items(const rvkv_decode_plan *plan) {
+  return plan ? plan->n_items : 0;
+}
+
+int rvkv_paged_decode_planned(const rvkv_pool *pool,
+                              const rvkv_decode_plan *plan, uint32_t layer,
+                              const float *q, const uint32_t *block_tables,
+                              const uint32_t *ctx_lens, uint32_t max_blocks,
+                              float scale, float *out, void *ws,
+                              size_t ws_bytes) {
+  const char *op = "paged_decode";
+  if (!plan) return fail(RVKV_EINVAL, op, "plan is NULL");
+  if (pool && (plan->n_kv != pool->n_kv || plan->head_dim != pool->head_dim))
+    return fail(RVKV_EINVAL, op, "plan was built for another pool shape");
+  DecodeArgs a;
+  uint32_t gt;
+  int rc = prepare_decode(op, pool, layer, q, block_tables, ctx_lens,
+                          max_blocks, plan->n_heads, plan->max_ctx, scale,
+                          plan->window, out, &a, &gt);
+  if (rc) return rc;
+  if ((rc = check_ws(op, ws, ws_bytes, plan->ws_bytes))) return rc;
+  a.ws_acc = plan->n_slots ? (float *)((char *)ws + plan->acc_off) : nullptr;
+  a.ws_ml = plan->n_slots ? (float *)((char *)ws + plan->ml_off) : nullptr;
+  a.items = plan->d_buf;
+  a.reds = plan->d_buf + plan->n_items;
+  a.part_tokens = plan->part_tokens;
+  a.n_parts = 1;
+  const dim3 grid(plan->n_items, pool->n_kv * a.n_sub, 1);
+  return launch_decode_pair(op, a, pool->head_dim, gt, grid,
+                            dim3(plan->n_heads, plan->n_reds ? plan->n_reds : 1),
+                            plan->n_reds > 0, pool->stream);
 }
 
 int rvkv_copy_blocks(rvkv_pool *pool, const uint32_t *src, const uint32_t *dst,

@@ -63,6 +63,61 @@ class HipGatherPlan:
         self.block_idx = _dev_u32(idx, device)
 
 
+class HipDecodePlan:
+    """Per-forward decode plan (rvkv_decode_plan_create): built from the
+    host-side context lengths (rvllm's read_num_tokens) and shared by every
+    layer's paged_decode_planned, like GatherPlan (src/kv_storage.rs:50-75).
+    """
+
+    def __init__(self, store: "HipKvStorage", ctx_lens, n_heads: int,
+                 window: int = 0):
+        import numpy as np
+        self._L = store._L
+        lens = np.ascontiguousarray(np.asarray(ctx_lens, dtype=np.uint32))
+        self.batch = int(lens.size)
+        self.n_heads = n_heads
+        self.window = int(window or 0)
+        self.ctx_lens_host = lens
+        handle = ctypes.c_void_p()
+        check(self._L.rvkv_decode_plan_create(
+            store._pool, lens.ctypes.data_as(ctypes.c_void_p), self.batch,
+            n_heads, self.window, ctypes.byref(handle)))
+        self._plan = handle
+        self._device = store.device
+        self.ws = None
+        self._sync()
+
+    def _sync(self) -> None:
+        self.workspace_bytes = self._L.rvkv_decode_plan_workspace_bytes(
+            self._plan)
+        self.items = self._L.rvkv_decode_plan_items(self._plan)
+        have = self.ws.numel() if self.ws is not None else 0
+        if self.workspace_bytes > have:
+            self.ws = torch.empty(self.workspace_bytes + (1 << 20),
+                                  dtype=torch.uint8, device=self._device)
+
+    def update(self, ctx_lens) -> None:
+        """rvkv_decode_plan_update: this step's context lengths."""
+        import numpy as np
+        lens = np.ascontiguousarray(np.asarray(ctx_lens, dtype=np.uint32))
+        check(self._L.rvkv_decode_plan_update(
+            self._plan, lens.ctypes.data_as(ctypes.c_void_p), lens.size))
+        self.batch = int(lens.size)
+        self.ctx_lens_host = lens
+        self._sync()
+
+    def close(self) -> None:
+        if getattr(self, "_plan", None):
+            self._L.rvkv_decode_plan_destroy(self._plan)
+            self._plan = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class HipKvStorage:
     """CudaKvStorage (src/cuda/kv_storage.rs:65-164) on MI355X: one zeroed f16
     pool for all layers' K and V, owned by librvkv."""
@@ -210,6 +265,35 @@ class HipKvStorage:
             batch, max_blocks, n_heads, max_ctx_len, float(scale),
             int(window or 0), _ptr(out), _ptr(ws),
             ws.numel() if ws is not None else 0))
+        return out
+
+    def paged_decode_planned(self, layer: int, plan: HipDecodePlan,
+                             q: torch.Tensor, block_tables: torch.Tensor,
+                             ctx_lens: torch.Tensor,
+                             out: Optional[torch.Tensor] = None,
+                             scale: Optional[float] = None) -> torch.Tensor:
+        """paged_decode driven by a per-forward HipDecodePlan (ragged
+        batches): same inputs and result."""
+        _need(q.dim() == 3 and q.shape[0] == plan.batch and
+              q.shape[1] == plan.n_heads and q.shape[2] == self.head_dim,
+              "paged_decode: q must be [batch, n_heads, head_dim] of the plan")
+        _need(q.dtype == torch.float32 and q.is_contiguous(),
+              "paged_decode: q must be contiguous float32")
+        _need(block_tables.dim() == 2 and block_tables.shape[0] == plan.batch,
+              "paged_decode: block_tables must be [batch, max_blocks]")
+        _need(ctx_lens.numel() == plan.batch,
+              "paged_decode: ctx_lens length must equal batch")
+        if out is None:
+            out = torch.empty_like(q)
+        _need(out.shape == q.shape and out.dtype == torch.float32 and
+              out.is_contiguous(), "paged_decode: out must match q")
+        if scale is None:
+            scale = 1.0 / math.sqrt(self.head_dim)
+        ws = plan.ws
+        check(self._L.rvkv_paged_decode_planned(
+            self._pool, plan._plan, layer, _ptr(q), _ptr(block_tables),
+            _ptr(ctx_lens), block_tables.shape[1], float(scale), _ptr(out),
+            _ptr(ws), ws.numel() if ws is not None else 0))
         return out
 
     # -- a10: copy-on-write -------------------------------------------------

@@ -461,3 +461,81 @@ def test_config_qwen25_ragged_prefix_cow():
     rng = np.random.default_rng(0)
     sample = sorted(set(sharers[:6]) | set(rng.choice(db.batch, 6).tolist()))
     assert _decode_vs_oracle(st, 1, db, q, sample=sample) < ATOL
+
+
+# ---- planned decode (ragged batches) --------------------------------------
+def _planned_vs_oracle(st, layer, db, q, window=0, sample=None):
+    from rvllm_amd.kv_storage import HipDecodePlan
+    plan = HipDecodePlan(st, db.ctx_lens, q.shape[1], window=window)
+    out = st.paged_decode_planned(layer, plan, q, dev_u32(db.padded_tables()),
+                                  dev_u32(db.ctx_lens)).cpu().numpy()
+    idx = list(range(db.batch)) if sample is None else list(sample)
+    cache, padded, mb = oracle_subset(st, layer, [db.tables[b] for b in idx],
+                                      db.ctx_lens[idx])
+    want = orc.paged_decode_f64(cache, q.cpu().numpy()[idx],
+                                padded.reshape(-1), mb, db.ctx_lens[idx],
+                                window=window)
+    assert np.isfinite(out).all()
+    return np.abs(out[idx] - want).max(), plan, out
+
+
+@pytest.mark.parametrize("window", [0, 300])
+def test_planned_decode_ragged_splits(window):
+    """One long sequence among short ones forces split work items (and the
+    reduction rows); an empty sequence gets a zero row."""
+    bs, nkv, hd, H = 32, 2, 64, 14
+    lens = np.array([9000, 0, 1, 31, 33, 700, 2048, 5], np.uint32)
+    cfg = W.Config("pl", 9, 1, H, nkv, hd, bs, len(lens))
+    db = W.ragged_batch(cfg, np.maximum(lens, 1), seed=4)
+    db.ctx_lens = lens
+    st = HipKvStorage(1, db.num_blocks, bs, nkv, hd)
+    fill_layer(st, 0, seed=21)
+    q = torch.randn(len(lens), H, hd, device="cuda")
+    err, plan, out = _planned_vs_oracle(st, 0, db, q, window=window,
+                                        sample=[0, 2, 3, 4, 5, 6, 7])
+    assert err < ATOL
+    assert plan.items > len(lens)  # the long sequence was split
+    assert (out[1] == 0).all()
+    # same numbers as the unplanned path within the tolerance
+    ref = st.paged_decode(0, q, dev_u32(db.padded_tables()), dev_u32(lens),
+                          int(lens.max()), window=window).cpu().numpy()
+    assert np.abs(ref - out).max() < ATOL
+
+
+def test_planned_decode_update_reuses_plan():
+    """update() with new lengths (a decode step later, batch change) gives
+    the same results as a freshly built plan."""
+    from rvllm_amd.kv_storage import HipDecodePlan
+    bs, nkv, hd, H = 16, 4, 128, 8
+    cfg = W.Config("pu", 9, 1, H, nkv, hd, bs, 6)
+    db = W.ragged_batch(cfg, [4000, 17, 900, 2500, 64, 3000], seed=5)
+    st = HipKvStorage(1, db.num_blocks, bs, nkv, hd)
+    fill_layer(st, 0, seed=22)
+    q = torch.randn(6, H, hd, device="cuda")
+    tables = dev_u32(db.padded_tables())
+    plan = HipDecodePlan(st, [10, 10, 10], H)
+    for lens in ([4000, 17, 900, 2500, 64, 3000], [3999, 16, 899, 2499, 63,
+                                                   2999]):
+        lens = np.array(lens, np.uint32)
+        plan.update(lens)
+        out = st.paged_decode_planned(0, plan, q, tables, dev_u32(lens))
+        fresh = HipDecodePlan(st, lens, H)
+        out2 = st.paged_decode_planned(0, fresh, q, tables, dev_u32(lens))
+        assert torch.equal(out, out2)
+        db.ctx_lens = lens
+        assert _decode_vs_oracle(st, 0, db, q) < ATOL
+
+
+def test_config_qwen25_planned():
+    db = W.qwen25_batch()
+    c = db.cfg
+    st = HipKvStorage(1, db.num_blocks, c.block_size, c.n_kv_heads,
+                      c.head_dim)
+    fill_layer(st, 0, seed=c.seed)
+    q = torch.randn(db.batch, c.n_heads, c.head_dim, device="cuda",
+                    generator=torch.Generator("cuda").manual_seed(3))
+    rng = np.random.default_rng(1)
+    longest = int(np.argmax(db.ctx_lens))
+    sample = sorted(set(rng.choice(db.batch, 10).tolist()) | {longest})
+    err, plan, _ = _planned_vs_oracle(st, 0, db, q, sample=sample)
+    assert err < ATOL
