@@ -74,6 +74,21 @@ def copy_calibration(torch, steps):
         "GB/s": round(2 * n * 4 / (ms * 1e-3) / 1e9, 1)}}), flush=True)
 
 
+def measured_traffic(config, batch):
+    """HBM bytes per decode launch measured by rocprofv3 --pmc (FETCH_SIZE +
+    WRITE_SIZE, each scaled by the same counter's reading for a copy of
+    known size) for this workload, from the committed summary, or None."""
+    if batch:
+        return None
+    path = os.path.join(ROOT, "profiles", "paged_decode_traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f).get(config)
+    except (OSError, ValueError):
+        return None
+    return rec.get("traffic_bytes_per_launch") if rec else None
+
+
 def build_workload(W, name, batch=0):
     c = W.CONFIGS[name]
     if batch:
@@ -216,23 +231,17 @@ def main():
             raise SystemExit("--graph cannot capture the per-step plan "
                              "rebuild; use --no-plan with --graph")
 
-    ev = None
-
-    def step(record=False):
+    def step():
         if plan is not None:
             plan.update(db.ctx_lens)
         for layer in range(L):
             st.write_tokens(layer, sb, so, nk[layer], nv[layer])
-            if record:
-                ev[layer][0].record()
             if plan is not None:
                 st.paged_decode_planned(layer, plan, q[layer], tables, ctx,
                                         out=out[layer])
             else:
                 st.paged_decode(layer, q[layer], tables, ctx, max_ctx,
                                 out=out[layer], ws=ws)
-            if record:
-                ev[layer][1].record()
 
     run = step
     if args.graph:
@@ -258,17 +267,27 @@ def main():
     torch.cuda.synchronize()
     dt = (time.perf_counter() - t0) / args.steps
 
-    # Per-launch decode duration with HIP events on the pool's stream
-    # (torch's current stream), over a second pass of the same steps.
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)]
-          for _ in range(L)]
-    durs = []
+    # Per-launch decode duration: HIP events on the pool's stream (torch's
+    # current stream) around `steps` rounds of back-to-back decode launches
+    # over all layers (each launch reads a different layer's pool, so no
+    # launch finds the previous one's data in the 256 MB MALL).
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
     for _ in range(args.steps):
-        step(record=True)
-        torch.cuda.synchronize()
-        durs.extend(ev[l][0].elapsed_time(ev[l][1]) for l in range(L))
-    dec_ms = float(np.mean(durs))
+        for layer in range(L):
+            if plan is not None:
+                st.paged_decode_planned(layer, plan, q[layer], tables, ctx,
+                                        out=out[layer])
+            else:
+                st.paged_decode(layer, q[layer], tables, ctx, max_ctx,
+                                out=out[layer], ws=ws)
+    e1.record()
+    torch.cuda.synchronize()
+    dec_ms = e0.elapsed_time(e1) / (args.steps * L)
 
+    traffic = measured_traffic(args.config, args.batch)
     dec_bytes = W.decode_bytes(db)
     app_bytes = W.append_bytes(B, c)
     step_bytes = L * (dec_bytes + app_bytes)
@@ -303,12 +322,12 @@ def main():
         "tok_per_s": round(B / dt, 1),
         "roofline": {
             "bound": "hbm",
-            "kernel": "paged_decode (partition + reduction launches)",
+            "kernel": "decode_part_kernel (+ decode_reduce_kernel for split sequences)",
             "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
             "algorithmic_bytes_per_launch": dec_bytes,
             "avg_launch_ms": round(dec_ms, 5),
         },
