@@ -43,6 +43,10 @@ def parse():
                    help="decode through a per-step decode plan (default: "
                         "only for ragged batches)")
     p.add_argument("--no-plan", dest="plan", action="store_false")
+    p.add_argument("--unfused", action="store_true",
+                   help="append and decode as two launches per layer "
+                        "(rvkv_append + rvkv_paged_decode) instead of the "
+                        "fused rvkv_decode_step")
     p.add_argument("--graph", action="store_true",
                    help="time the step as one HIP graph replay (all layers' "
                         "append + decode launches captured once)")
@@ -74,13 +78,14 @@ def copy_calibration(torch, steps):
         "GB/s": round(2 * n * 4 / (ms * 1e-3) / 1e9, 1)}}), flush=True)
 
 
-def measured_traffic(config, batch):
+def measured_traffic(config, batch, unfused):
     """HBM bytes per decode launch measured by rocprofv3 --pmc (FETCH_SIZE +
     WRITE_SIZE, each scaled by the same counter's reading for a copy of
     known size) for this workload, from the committed summary, or None."""
     if batch:
         return None
-    path = os.path.join(ROOT, "profiles", "paged_decode_traffic.json")
+    name = "paged_decode_traffic.json" if unfused else "decode_step_traffic.json"
+    path = os.path.join(ROOT, "profiles", name)
     try:
         with open(path) as f:
             rec = json.load(f).get(config)
@@ -231,17 +236,26 @@ def main():
             raise SystemExit("--graph cannot capture the per-step plan "
                              "rebuild; use --no-plan with --graph")
 
-    def step():
-        if plan is not None:
-            plan.update(db.ctx_lens)
-        for layer in range(L):
-            st.write_tokens(layer, sb, so, nk[layer], nv[layer])
+    def decode(layer):
+        if args.unfused:
             if plan is not None:
                 st.paged_decode_planned(layer, plan, q[layer], tables, ctx,
                                         out=out[layer])
             else:
                 st.paged_decode(layer, q[layer], tables, ctx, max_ctx,
                                 out=out[layer], ws=ws)
+        else:  # append + decode in one launch
+            st.decode_step(layer, nk[layer], nv[layer], sb, so, q[layer],
+                           tables, ctx, max_ctx, plan=plan, out=out[layer],
+                           ws=ws)
+
+    def step():
+        if plan is not None:
+            plan.update(db.ctx_lens)
+        for layer in range(L):
+            if args.unfused:
+                st.write_tokens(layer, sb, so, nk[layer], nv[layer])
+            decode(layer)
 
     run = step
     if args.graph:
@@ -277,20 +291,16 @@ def main():
     e0.record()
     for _ in range(args.steps):
         for layer in range(L):
-            if plan is not None:
-                st.paged_decode_planned(layer, plan, q[layer], tables, ctx,
-                                        out=out[layer])
-            else:
-                st.paged_decode(layer, q[layer], tables, ctx, max_ctx,
-                                out=out[layer], ws=ws)
+            decode(layer)
     e1.record()
     torch.cuda.synchronize()
     dec_ms = e0.elapsed_time(e1) / (args.steps * L)
 
-    traffic = measured_traffic(args.config, args.batch)
-    dec_bytes = W.decode_bytes(db)
+    traffic = measured_traffic(args.config, args.batch, args.unfused)
     app_bytes = W.append_bytes(B, c)
-    step_bytes = L * (dec_bytes + app_bytes)
+    # The fused launch also moves the appended rows (f32 in, f16 out).
+    dec_bytes = W.decode_bytes(db) + (0 if args.unfused else app_bytes)
+    step_bytes = L * (W.decode_bytes(db) + app_bytes)
     achieved = dec_bytes / (dec_ms * 1e-3) / 1e9
     res = {
         "metric": METRIC,
@@ -322,7 +332,9 @@ def main():
         "tok_per_s": round(B / dt, 1),
         "roofline": {
             "bound": "hbm",
-            "kernel": "decode_part_kernel (+ decode_reduce_kernel for split sequences)",
+            "kernel": ("decode_part_kernel (+ decode_reduce_kernel for split "
+                       "sequences)" + ("" if args.unfused else
+                                       ", fused append (rvkv_decode_step)")),
             "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

@@ -179,6 +179,27 @@ int rvkv_paged_decode_planned(const rvkv_pool *pool,
                               float scale, float *out, void *ws,
                               size_t ws_bytes);
 
+/* ---- a2 + a5 + a6 fused: one layer of a decode step ----------------------
+ * The per-layer order of src/model.rs:628-644 (write_tokens, then attend
+ * over the context including the new token) in ONE launch: row b of k/v
+ * ([batch, n_kv_heads, head_dim], F32 rounded to f16 nearest-even or F16) is
+ * sequence b's token at position ctx_lens[b]-1 and is stored at
+ * (slot_block[b], slot_off[b]); the workgroup that attends over that
+ * position uses the same f16 values, so the cache afterwards and the output
+ * equal rvkv_append followed by rvkv_paged_decode (or _planned). Precondition
+ * (as in the engine, src/engine.rs:446-451): the slot is the block-table slot
+ * of position ctx_lens[b]-1. plan may be NULL (uniform partitioning, same
+ * workspace as rvkv_paged_decode) or a plan built for this batch (then
+ * batch/n_heads/window must match it and max_ctx_len is ignored). */
+int rvkv_decode_step(rvkv_pool *pool, const rvkv_decode_plan *plan,
+                     uint32_t layer, const void *k, const void *v,
+                     rvkv_dtype src_dtype, const uint32_t *slot_block,
+                     const uint32_t *slot_off, const float *q,
+                     const uint32_t *block_tables, const uint32_t *ctx_lens,
+                     uint32_t batch, uint32_t max_blocks, uint32_t n_heads,
+                     uint32_t max_ctx_len, float scale, int32_t window,
+                     float *out, void *ws, size_t ws_bytes);
+
 /* ---- a10: prefix-cache copy-on-write -------------------------------------
  * No counterpart in the reference (rvllm never mutates a shared block; its
  * only copy is the whole-cache KvStorage::clone, src/kv_storage.rs:15-33).

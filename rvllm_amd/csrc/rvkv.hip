@@ -301,6 +301,14 @@ struct DecodeArgs {
   // where grid.x = partition and slot = seq * n_parts + partition.
   const uint4 *items;
   const uint4 *reds;
+  // Fused append (rvkv_decode_step): this step's K/V row of every sequence
+  // ([batch, n_kv, hd], f32 or f16) and its slot; NULL for a plain decode.
+  const void *new_k;
+  const void *new_v;
+  const uint32_t *new_blk;
+  const uint32_t *new_off;
+  int32_t new_f32;
+  uint32_t block_size;
   uint64_t block_stride;  // elements per block (all heads)
   uint32_t head_stride;   // elements per (block, head) tile
   uint32_t max_blocks, num_blocks, n_kv, n_heads, group, n_sub;
@@ -351,7 +359,8 @@ __device__ __forceinline__ void decode_chunk(SoftmaxState<GT, NL> &st,
                                              const uint4 (&kr)[U][NL],
                                              const uint4 (&vr)[U][NL],
                                              uint32_t tok0, uint32_t lo,
-                                             uint32_t t1, uint32_t okmask) {
+                                             uint32_t t1, uint32_t okmask,
+                                             uint32_t newtok) {
   constexpr int RPL = 64 / R;
   float s[U][GT];
 #pragma unroll
@@ -370,7 +379,10 @@ __device__ __forceinline__ void decode_chunk(SoftmaxState<GT, NL> &st,
     }
     if constexpr (MASKED) {
       const uint32_t tok = tok0 + u * RPL;
-      const bool valid = ((okmask >> u) & 1u) && tok >= lo && tok < t1;
+      // (newtok, the key appended by a fused decode step, is folded in
+      // separately from registers.)
+      const bool valid =
+          ((okmask >> u) & 1u) && tok >= lo && tok < t1 && tok != newtok;
 #pragma unroll
       for (int g = 0; g < GT; ++g)
         s[u][g] = valid ? s[u][g] : -__builtin_inff();
@@ -446,7 +458,9 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
   extern __shared__ float lds[];  // [W][GT][HD + 2]
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // Wave-uniform by construction; readfirstlane lets the compiler keep it
+  // (and every block id / address derived from it) in SGPRs.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int W = blockDim.x >> 6;
   const int rg = lane / R;
   const int c = lane % R;
@@ -525,6 +539,13 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
     for (int e = 0; e < NL * 8; ++e) st.acc[g][e] = 0.f;
   }
 
+  // Fused append (rvkv_decode_step): position ctx-1 holds the key appended
+  // this step; the workgroup whose range contains it stores the row and
+  // folds it in from registers after the main loop.
+  const uint32_t newtok = (a.new_k != nullptr && ctx - 1 >= t0 && ctx - 1 < t1)
+                              ? ctx - 1
+                              : 0xFFFFFFFFu;
+
   // Chunks start at multiples of TC inside the partition; the window's
   // lower edge skips whole chunks below it.
   const uint32_t skip = lo > t0 ? (lo - t0) / (TC * W) * (TC * W) : 0;
@@ -585,13 +606,94 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
       for (int u = 0; u < U; ++u)
         ids[u] = table[min((ch + stride + u * RPL) >> a.bs_log2, last_blk)];
 
-      const bool full = ch >= lo && ch + TC <= t1 && okmask == (1u << U) - 1u;
+      // The chunk holding this step's appended key takes the masked path,
+      // which leaves that key out.
+      const bool has_new = newtok >= ch && newtok < ch + TC;
+      const bool full = !has_new && ch >= lo && ch + TC <= t1 &&
+                        okmask == (1u << U) - 1u;
       if (full)
         decode_chunk<R, GT, U, NL, false>(st, qh, kr, vr, ch + rg, lo, t1,
-                                          okmask);
+                                          okmask, newtok);
       else
         decode_chunk<R, GT, U, NL, true>(st, qh, kr, vr, ch + rg, lo, t1,
-                                         okmask);
+                                         okmask, newtok);
+    }
+
+    if (newtok != 0xFFFFFFFFu && wave == 0) {
+      // The appended row: round to f16 exactly like append_kernel, store it
+      // (sub-group 0, row group 0), and add it to row group 0's softmax
+      // state as one more key.
+      uint4 nk[NL], nv[NL];
+      const size_t src = ((size_t)b * a.n_kv + kvh) * HD;
+#pragma unroll
+      for (int j = 0; j < NL; ++j) {
+        const uint32_t e0 = (j * R + c) * 8;
+        if (a.new_f32) {
+          const float4 *kp = reinterpret_cast<const float4 *>(
+              static_cast<const float *>(a.new_k) + src + e0);
+          const float4 *vp = reinterpret_cast<const float4 *>(
+              static_cast<const float *>(a.new_v) + src + e0);
+          const float4 k0 = kp[0], k1 = kp[1], v0 = vp[0], v1 = vp[1];
+          nk[j].x = as_u32(h2{(_Float16)k0.x, (_Float16)k0.y});
+          nk[j].y = as_u32(h2{(_Float16)k0.z, (_Float16)k0.w});
+          nk[j].z = as_u32(h2{(_Float16)k1.x, (_Float16)k1.y});
+          nk[j].w = as_u32(h2{(_Float16)k1.z, (_Float16)k1.w});
+          nv[j].x = as_u32(h2{(_Float16)v0.x, (_Float16)v0.y});
+          nv[j].y = as_u32(h2{(_Float16)v0.z, (_Float16)v0.w});
+          nv[j].z = as_u32(h2{(_Float16)v1.x, (_Float16)v1.y});
+          nv[j].w = as_u32(h2{(_Float16)v1.z, (_Float16)v1.w});
+        } else {
+          nk[j] = *reinterpret_cast<const uint4 *>(
+              static_cast<const uint16_t *>(a.new_k) + src + e0);
+          nv[j] = *reinterpret_cast<const uint4 *>(
+              static_cast<const uint16_t *>(a.new_v) + src + e0);
+        }
+      }
+      if (sub == 0 && rg == 0) {
+        const uint32_t blk = a.new_blk[b], off = a.new_off[b];
+        if (blk < a.num_blocks && off < a.block_size) {
+          const size_t dst =
+              ((size_t)blk * a.n_kv + kvh) * a.head_stride + (size_t)off * HD;
+          uint16_t *kc = const_cast<uint16_t *>(a.kc);
+          uint16_t *vc = const_cast<uint16_t *>(a.vc);
+#pragma unroll
+          for (int j = 0; j < NL; ++j) {
+            *reinterpret_cast<uint4 *>(kc + dst + (j * R + c) * 8) = nk[j];
+            *reinterpret_cast<uint4 *>(vc + dst + (j * R + c) * 8) = nv[j];
+          }
+        }
+      }
+#pragma unroll
+      for (int g = 0; g < GT; ++g) {
+        float d = 0.f;
+#pragma unroll
+        for (int j = 0; j < NL; ++j) {
+          d = __builtin_amdgcn_fdot2(qh[g][j][0], as_h2(nk[j].x), d, false);
+          d = __builtin_amdgcn_fdot2(qh[g][j][1], as_h2(nk[j].y), d, false);
+          d = __builtin_amdgcn_fdot2(qh[g][j][2], as_h2(nk[j].z), d, false);
+          d = __builtin_amdgcn_fdot2(qh[g][j][3], as_h2(nk[j].w), d, false);
+        }
+        d = row_group_sum<R>(d);
+        if (rg == 0) {
+          const float mx = fmaxf(st.m[g], d);
+          const float corr = __builtin_amdgcn_exp2f(st.m[g] - mx);
+          const _Float16 p = (_Float16)__builtin_amdgcn_exp2f(d - mx);
+          st.m[g] = mx;
+          st.l[g] = st.l[g] * corr + (float)p;
+#pragma unroll
+          for (int j = 0; j < NL; ++j) {
+            const uint32_t w4[4] = {nv[j].x, nv[j].y, nv[j].z, nv[j].w};
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+              const h2 vv = as_h2(w4[w]);
+              float &x0 = st.acc[g][j * 8 + 2 * w];
+              float &x1 = st.acc[g][j * 8 + 2 * w + 1];
+              x0 = x0 * corr + (float)p * (float)vv.x;
+              x1 = x1 * corr + (float)p * (float)vv.y;
+            }
+          }
+        }
+      }
     }
 
     // Merge the RPL row groups of the wave (lanes c, c+R, c+2R, ...).
@@ -1042,6 +1144,7 @@ int prepare_decode(const char *op, const rvkv_pool *pool, uint32_t layer,
   a->ctx_lens = ctx_lens;
   a->block_stride = pool->block_elems;
   a->head_stride = bs * hd;
+  a->block_size = bs;
   a->max_blocks = max_blocks;
   a->num_blocks = pool->num_blocks;
   a->n_kv = pool->n_kv;
@@ -1322,6 +1425,69 @@ int rvkv_paged_decode_planned(const rvkv_pool *pool,
   return launch_decode_pair(op, a, pool->head_dim, gt, grid,
                             dim3(plan->n_heads, plan->n_reds ? plan->n_reds : 1),
                             plan->n_reds > 0, pool->stream);
+}
+
+int rvkv_decode_step(rvkv_pool *pool, const rvkv_decode_plan *plan,
+                     uint32_t layer, const void *k, const void *v,
+                     rvkv_dtype src_dtype, const uint32_t *slot_block,
+                     const uint32_t *slot_off, const float *q,
+                     const uint32_t *block_tables, const uint32_t *ctx_lens,
+                     uint32_t batch, uint32_t max_blocks, uint32_t n_heads,
+                     uint32_t max_ctx_len, float scale, int32_t window,
+                     float *out, void *ws, size_t ws_bytes) {
+  const char *op = "decode_step";
+  if (!k || !v || !slot_block || !slot_off)
+    return fail(RVKV_EINVAL, op, "NULL k/v/block_ids/offsets");
+  if (src_dtype != RVKV_F16 && src_dtype != RVKV_F32)
+    return fail(RVKV_EINVAL, op, "src dtype must be F16 or F32");
+  if ((uintptr_t)k % 16 || (uintptr_t)v % 16)
+    return fail(RVKV_EINVAL, op, "k/v must be 16-byte aligned");
+  if (plan) {
+    if (plan->batch != batch)
+      return fail(RVKV_EINVAL, op, "batch differs from the plan's");
+    if (plan->n_heads != n_heads || plan->window != window)
+      return fail(RVKV_EINVAL, op, "n_heads/window differ from the plan's");
+  }
+  if (pool && batch == 0) return RVKV_OK;
+  DecodeArgs a;
+  uint32_t gt;
+  int rc = prepare_decode(op, pool, layer, q, block_tables, ctx_lens,
+                          max_blocks, n_heads,
+                          plan ? plan->max_ctx : max_ctx_len, scale, window,
+                          out, &a, &gt);
+  if (rc) return rc;
+  a.new_k = k;
+  a.new_v = v;
+  a.new_blk = slot_block;
+  a.new_off = slot_off;
+  a.new_f32 = src_dtype == RVKV_F32;
+  if (plan) {
+    if (plan->n_kv != pool->n_kv || plan->head_dim != pool->head_dim)
+      return fail(RVKV_EINVAL, op, "plan was built for another pool shape");
+    if ((rc = check_ws(op, ws, ws_bytes, plan->ws_bytes))) return rc;
+    a.ws_acc = plan->n_slots ? (float *)((char *)ws + plan->acc_off) : nullptr;
+    a.ws_ml = plan->n_slots ? (float *)((char *)ws + plan->ml_off) : nullptr;
+    a.items = plan->d_buf;
+    a.reds = plan->d_buf + plan->n_items;
+    a.part_tokens = plan->part_tokens;
+    a.n_parts = 1;
+    const dim3 grid(plan->n_items, pool->n_kv * a.n_sub, 1);
+    return launch_decode_pair(
+        op, a, pool->head_dim, gt, grid,
+        dim3(plan->n_heads, plan->n_reds ? plan->n_reds : 1),
+        plan->n_reds > 0, pool->stream);
+  }
+  if (batch > 65535) return fail(RVKV_EUNSUPPORTED, op, "batch too large");
+  if (max_ctx_len == 0) max_ctx_len = 1;
+  const WsLayout w = ws_layout(pool, batch, n_heads, max_ctx_len);
+  if ((rc = check_ws(op, ws, ws_bytes, w.bytes))) return rc;
+  a.ws_acc = w.n_parts > 1 ? (float *)((char *)ws + w.acc_off) : nullptr;
+  a.ws_ml = w.n_parts > 1 ? (float *)((char *)ws + w.ml_off) : nullptr;
+  a.part_tokens = partition_tokens(pool, batch, n_heads, max_ctx_len);
+  a.n_parts = w.n_parts;
+  const dim3 grid(w.n_parts, pool->n_kv * a.n_sub, batch);
+  return launch_decode_pair(op, a, pool->head_dim, gt, grid,
+                            dim3(n_heads, batch), w.n_parts > 1, pool->stream);
 }
 
 int rvkv_copy_blocks(rvkv_pool *pool, const uint32_t *src, const uint32_t *dst,

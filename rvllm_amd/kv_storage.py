@@ -296,6 +296,54 @@ class HipKvStorage:
             _ptr(ws), ws.numel() if ws is not None else 0))
         return out
 
+    def decode_step(self, layer: int, k: torch.Tensor, v: torch.Tensor,
+                    slot_block: torch.Tensor, slot_off: torch.Tensor,
+                    q: torch.Tensor, block_tables: torch.Tensor,
+                    ctx_lens: torch.Tensor, max_ctx_len: int = 0,
+                    plan: Optional[HipDecodePlan] = None,
+                    out: Optional[torch.Tensor] = None,
+                    ws: Optional[torch.Tensor] = None,
+                    scale: Optional[float] = None,
+                    window: int = 0) -> torch.Tensor:
+        """One layer of a decode step in one launch (rvkv_decode_step):
+        append each sequence's new K/V row (k, v: [batch, n_kv, hd]) at its
+        slot, then attend over ctx_lens keys including it. Equivalent to
+        write_tokens + paged_decode(_planned)."""
+        _need(q.dim() == 3 and q.shape[2] == self.head_dim and
+              q.dtype == torch.float32 and q.is_contiguous(),
+              "decode_step: q must be contiguous float32 [batch, n_heads, "
+              "head_dim]")
+        batch, n_heads, hd = q.shape
+        _need(k.shape == (batch, self.n_kv_heads, hd) and v.shape == k.shape
+              and k.dtype == v.dtype and k.dtype in _DT and
+              k.is_contiguous() and v.is_contiguous(),
+              "decode_step: k/v must be contiguous [batch, n_kv_heads, "
+              "head_dim] float32 or float16")
+        _need(slot_block.numel() == batch and slot_off.numel() == batch,
+              "decode_step: block_ids/offsets length must equal batch")
+        _need(block_tables.dim() == 2 and block_tables.shape[0] == batch and
+              ctx_lens.numel() == batch,
+              "decode_step: block_tables/ctx_lens must have batch rows")
+        if out is None:
+            out = torch.empty_like(q)
+        if scale is None:
+            scale = 1.0 / math.sqrt(hd)
+        if plan is not None:
+            ws = plan.ws
+            window = plan.window
+        elif ws is None:
+            need = self.decode_workspace_bytes(batch, n_heads, max_ctx_len)
+            if need:
+                ws = self.alloc_workspace(batch, n_heads, max_ctx_len)
+        check(self._L.rvkv_decode_step(
+            self._pool, plan._plan if plan is not None else None, layer,
+            _ptr(k), _ptr(v), _DT[k.dtype], _ptr(slot_block), _ptr(slot_off),
+            _ptr(q), _ptr(block_tables), _ptr(ctx_lens), batch,
+            block_tables.shape[1], n_heads, max_ctx_len, float(scale),
+            int(window or 0), _ptr(out), _ptr(ws),
+            ws.numel() if ws is not None else 0))
+        return out
+
     # -- a10: copy-on-write -------------------------------------------------
     def copy_blocks(self, src: torch.Tensor, dst: torch.Tensor) -> None:
         """Copies src[i] -> dst[i] for all layers, K and V."""

@@ -539,3 +539,52 @@ def test_config_qwen25_planned():
     sample = sorted(set(rng.choice(db.batch, 10).tolist()) | {longest})
     err, plan, _ = _planned_vs_oracle(st, 0, db, q, sample=sample)
     assert err < ATOL
+
+
+# ---- fused decode step (append + decode in one launch) --------------------
+@pytest.mark.parametrize("planned", [False, True])
+@pytest.mark.parametrize("src", [torch.float32, torch.float16])
+@pytest.mark.parametrize("G,hd,bs,window", [(4, 64, 16, 0), (2, 128, 16, 0),
+                                            (9, 64, 32, 0), (4, 256, 16, 300)])
+def test_decode_step_equals_append_then_decode(planned, src, G, hd, bs,
+                                               window):
+    """rvkv_decode_step leaves the same cache bits as rvkv_append followed by
+    the decode (uniform or planned) and the same output up to summation
+    order."""
+    from rvllm_amd.kv_storage import HipDecodePlan
+    nkv = 2
+    lens = np.array([5000, 1, 16, 17, 700, 2049, 64, 333], np.uint32)
+    cfg = W.Config("fs", 9, 1, nkv * G, nkv, hd, bs, len(lens))
+    db = W.ragged_batch(cfg, lens, seed=G + hd)
+    stores = [HipKvStorage(1, db.num_blocks, bs, nkv, hd) for _ in range(2)]
+    for st in stores:
+        fill_layer(st, 0, seed=31)
+    g = torch.Generator("cuda").manual_seed(7)
+    nk = torch.randn(len(lens), nkv, hd, device="cuda", generator=g).to(src)
+    nv = torch.randn(len(lens), nkv, hd, device="cuda", generator=g).to(src)
+    q = torch.randn(len(lens), nkv * G, hd, device="cuda", generator=g)
+    sb, so = dev_u32(db.slot_block), dev_u32(db.slot_off)
+    tables, ctx = dev_u32(db.padded_tables()), dev_u32(lens)
+    max_ctx = int(lens.max())
+    a, b = stores
+    if planned:
+        pa = HipDecodePlan(a, lens, nkv * G, window=window)
+        pb = HipDecodePlan(b, lens, nkv * G, window=window)
+        out_a = a.decode_step(0, nk, nv, sb, so, q, tables, ctx, plan=pa)
+        b.write_tokens(0, sb, so, nk, nv)
+        out_b = b.paged_decode_planned(0, pb, q, tables, ctx)
+    else:
+        out_a = a.decode_step(0, nk, nv, sb, so, q, tables, ctx, max_ctx,
+                              window=window)
+        b.write_tokens(0, sb, so, nk, nv)
+        out_b = b.paged_decode(0, q, tables, ctx, max_ctx, window=window)
+    ids = dev_u32(np.arange(db.num_blocks))
+    for which in (0, 1):
+        assert torch.equal(a.read_blocks(0, which, ids),
+                           b.read_blocks(0, which, ids))
+    # The fused launch folds the new key in after its chunk loop, so only the
+    # summation order (and the f16 rounding of that key's probability under
+    # a different running max) differs from append-then-decode.
+    assert (out_a - out_b).abs().max().item() < 5e-4
+    db.ctx_lens = lens
+    assert _decode_vs_oracle(a, 0, db, q, window=window) < ATOL
