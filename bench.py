@@ -47,6 +47,15 @@ def parse():
                    help="append and decode as two launches per layer "
                         "(rvkv_append + rvkv_paged_decode) instead of the "
                         "fused rvkv_decode_step")
+    p.add_argument("--churn", action="store_true",
+                   help="continuous-batching churn (BASELINE configs[4]): each "
+                        "step 10%% of sequences finish and as many are "
+                        "admitted with 64-token prompts, over a fragmented "
+                        "pool; --steps counts engine steps")
+    p.add_argument("--prefill", choices=["f32", "f16"], default=None,
+                   help="time the prefill append instead (BASELINE configs[2]: "
+                        "every sequence's whole context scattered into the "
+                        "paged cache, all layers; source dtype f32 or f16)")
     p.add_argument("--graph", action="store_true",
                    help="time the step as one HIP graph replay (all layers' "
                         "append + decode launches captured once)")
@@ -181,6 +190,175 @@ def cpu_baseline(orc, W, st, db, budget_s):
     }
 
 
+def run_prefill(args, torch, W):
+    """Scatter-only prefill append: every sequence's ctx tokens (K and V
+    rows [tokens, n_kv, hd] of the source dtype) appended into its
+    block-table slots, one rvkv_append per layer (the slot lists are built
+    once, like the engine's write_positions). The source rows are one
+    device buffer reused by every layer (each layer's write goes to its own
+    pool, and the source is far larger than the 256 MB MALL)."""
+    from rvllm_amd.kv_storage import HipKvStorage
+    db = build_workload(W, args.config, args.batch)
+    c = db.cfg
+    st = HipKvStorage(c.n_layers, db.num_blocks, c.block_size, c.n_kv_heads,
+                      c.head_dim)
+    bs = c.block_size
+    sb, so = [], []
+    for t, n in zip(db.tables, db.ctx_lens):
+        pos = np.arange(int(n))
+        sb.append(np.asarray(t, np.uint32)[pos // bs])
+        so.append((pos % bs).astype(np.uint32))
+    sb = torch.from_numpy(np.concatenate(sb).view(np.int32)).cuda()
+    so = torch.from_numpy(np.concatenate(so).view(np.int32)).cuda()
+    n_tok = sb.numel()
+    dt_src = torch.float32 if args.prefill == "f32" else torch.float16
+    g = torch.Generator(device="cuda")
+    g.manual_seed(c.seed)
+    k = (torch.randn((n_tok, c.n_kv_heads, c.head_dim), generator=g,
+                     device="cuda") * c.value_scale).to(dt_src)
+    v = (torch.randn((n_tok, c.n_kv_heads, c.head_dim), generator=g,
+                     device="cuda") * c.value_scale).to(dt_src)
+
+    def step():
+        for layer in range(c.n_layers):
+            st.write_tokens(layer, sb, so, k, v)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    launch_ms = e0.elapsed_time(e1) / (args.steps * c.n_layers)
+    src_bytes = 4 if args.prefill == "f32" else 2
+    per_launch = W.append_bytes(n_tok, c, src_bytes)
+    achieved = per_launch / (launch_ms * 1e-3) / 1e9
+    res = {
+        "metric": "prefill append (scatter) HBM GB/s, 1 MI355X",
+        "value": round(per_launch * c.n_layers / dt / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": f"{args.prefill} source -> f16 cache",
+        "data": "synthetic N(0,1)*scale rows, seeded permuted block tables",
+        "config": {
+            "workload": f"{c.name} prefill append: {n_tok} tokens "
+                        f"({db.batch} seqs x {int(db.ctx_lens.max())}) x "
+                        f"{c.n_layers} layers, {c.n_kv_heads} kv heads, "
+                        f"head_dim {c.head_dim}, block_size {bs}",
+            "global_batch": db.batch,
+            "seq_len": int(db.ctx_lens.max()),
+            "parallelism": "single GPU",
+        },
+        "tok_per_s": round(n_tok / dt, 1),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": f"append_kernel<8, {args.prefill == 'f32'}>",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "algorithmic_bytes_per_launch": per_launch,
+            "avg_launch_ms": round(launch_ms, 5),
+        },
+    }
+    print(json.dumps(res), flush=True)
+
+
+def run_churn(args, torch, W):
+    """gemma-3-270m shape, 1024 sequences starting at
+    1024 tokens; every engine step 10% finish and 10% are admitted with
+    64-token prompts (prefill append), then all decode one token (fused
+    append + decode per layer under a per-step decode plan). The pool is
+    1.25x the initial live blocks, with a seeded-shuffled free list."""
+    from rvllm_amd.engine_sim import ChurnDriver
+    c = W.CONFIGS[args.config]
+    batch = args.batch or c.batch
+    drv = ChurnDriver(c, batch, 1024, prompt_len=64, churn=0.10,
+                      steps=args.warmup + args.steps + 1)
+    for _ in range(args.warmup):
+        drv.step()
+    torch.cuda.synchronize()
+    b0 = drv.bytes_moved
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        drv.step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    step_bytes = (drv.bytes_moved - b0) / args.steps
+    # Per-launch decode time at the final state (back-to-back over layers).
+    st, plan = drv.st, drv.plan
+    db = drv.devb[(drv.step_index - 1) & 1]
+    lens = drv.last[1]
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    reps = max(args.steps // 10, 3)
+    e0.record()
+    for _ in range(reps):
+        for layer in range(c.n_layers):
+            st.decode_step(layer, drv.nk[layer], drv.nv[layer], db["sb"],
+                           db["so"], drv.q[layer], db["tables"], db["ctx"],
+                           plan=plan, out=drv.out[layer])
+    e1.record()
+    torch.cuda.synchronize()
+    dec_ms = e0.elapsed_time(e1) / (reps * c.n_layers)
+    dec_bytes = drv.decode_bytes(lens) + W.append_bytes(batch, c)
+    achieved = dec_bytes / (dec_ms * 1e-3) / 1e9
+    res = {
+        "metric": METRIC,
+        "value": round(step_bytes / dt / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 KV, f32 accumulate",
+        "data": "synthetic: K/V/q ~ N(0,1), seeded churn and free list",
+        "config": {
+            "workload": f"{c.name} churn: {c.n_layers} layers, {c.n_heads} q / "
+                        f"{c.n_kv_heads} kv heads, head_dim {c.head_dim}, "
+                        f"block_size {c.block_size}, {batch} seqs from 1024 "
+                        f"tokens, 10% finish/admit (64-token prompts) per "
+                        f"step, pool {drv.num_blocks} blocks (1.25x live, "
+                        f"shuffled free list)",
+            "global_batch": batch,
+            "seq_len": int(lens.max()),
+            "parallelism": "single GPU",
+            "decode_plan_items": plan.items,
+        },
+        "pct_of_peak": round(100 * step_bytes / dt / 1e9 / HBM_PEAK_GBS, 2),
+        "tok_per_s": round(batch / dt, 1),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "decode_part_kernel (fused append, decode plan) at the "
+                      "final step's lengths",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "algorithmic_bytes_per_launch": dec_bytes,
+            "avg_launch_ms": round(dec_ms, 5),
+        },
+    }
+    print(json.dumps(res), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -196,6 +374,12 @@ def main():
     torch.cuda.set_device(0)
     if args.copy_calibration:
         copy_calibration(torch, max(args.steps, 5))
+        return
+    if args.churn:
+        run_churn(args, torch, W)
+        return
+    if args.prefill:
+        run_prefill(args, torch, W)
         return
     db = build_workload(W, args.config, args.batch)
     c = db.cfg

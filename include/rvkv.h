@@ -256,6 +256,26 @@ int rvkv_bm_free_seq(rvkv_bm *bm, int64_t seq);
 int rvkv_bm_append_slot(rvkv_bm *bm, int64_t seq, uint32_t *block,
                         uint32_t *offset, uint32_t *cow_src,
                         uint32_t *cow_dst);
+/* Batch forms of free_seq / add_seq (an engine step's finishes and
+ * admissions). add_seqs is all-or-nothing: RVKV_ENOMEM if the pool cannot
+ * hold every prompt; ids[i] receives the new sequence ids. */
+int rvkv_bm_free_seqs(rvkv_bm *bm, const int64_t *seqs, uint32_t n);
+int rvkv_bm_add_seqs(rvkv_bm *bm, const uint32_t *n_tokens, uint32_t n,
+                     int64_t *ids);
+/* rvkv_bm_append_slot for seqs[0..n) in order (one decode step's writes,
+ * rvllm's DecodeRow.write, src/engine.rs:446-451): slot i -> blocks[i],
+ * offsets[i]; the copy-on-write pairs go to cow_src/cow_dst[0..*n_cow)
+ * (capacity n). Stops at the first failure (its code is returned). */
+int rvkv_bm_append_slots(rvkv_bm *bm, const int64_t *seqs, uint32_t n,
+                         uint32_t *blocks, uint32_t *offsets,
+                         uint32_t *cow_src, uint32_t *cow_dst,
+                         uint32_t *n_cow);
+/* The padded block tables and token counts of seqs[0..n): tables is
+ * [n, max_blocks], each row padded with its last block (GatherPlan's rule,
+ * src/kv_storage.rs:59-67); ctx_lens[i] = num_tokens. */
+int rvkv_bm_fill_tables(const rvkv_bm *bm, const int64_t *seqs, uint32_t n,
+                        uint32_t max_blocks, uint32_t *tables,
+                        uint32_t *ctx_lens);
 /* logical_to_physical(pos) of rvllm's BlockTable. */
 int rvkv_bm_slot(const rvkv_bm *bm, int64_t seq, uint32_t pos,
                  uint32_t *block, uint32_t *offset);

@@ -55,6 +55,10 @@ SIGNATURES = {
     "rvkv_bm_fork_seq": (_i64, [_P, _i64, _u32, _u32]),
     "rvkv_bm_free_seq": (_int, [_P, _i64]),
     "rvkv_bm_append_slot": (_int, [_P, _i64, _pu32, _pu32, _pu32, _pu32]),
+    "rvkv_bm_free_seqs": (_int, [_P, _P, _u32]),
+    "rvkv_bm_add_seqs": (_int, [_P, _P, _u32, _P]),
+    "rvkv_bm_append_slots": (_int, [_P, _P, _u32, _P, _P, _P, _P, _pu32]),
+    "rvkv_bm_fill_tables": (_int, [_P, _P, _u32, _u32, _P, _P]),
     "rvkv_bm_slot": (_int, [_P, _i64, _u32, _pu32, _pu32]),
     "rvkv_bm_num_tokens": (_u32, [_P, _i64]),
     "rvkv_bm_num_blocks": (_u32, [_P, _i64]),

@@ -74,6 +74,65 @@ class BlockManager:
         cow = None if cs.value == _U32_MAX else (cs.value, cd.value)
         return blk.value, off.value, cow
 
+    def free_seqs(self, seqs) -> None:
+        import numpy as np
+        seqs = np.ascontiguousarray(np.asarray(seqs, dtype=np.int64))
+        rc = self._L.rvkv_bm_free_seqs(
+            self._h, seqs.ctypes.data_as(ctypes.c_void_p), seqs.size)
+        if rc != 0:
+            raise RvkvError("block_manager: free_seqs: unknown sequence", rc)
+
+    def add_seqs(self, n_tokens):
+        """New sequences holding n_tokens[i] tokens each (all or none)."""
+        import numpy as np
+        n_tokens = np.ascontiguousarray(np.asarray(n_tokens, dtype=np.uint32))
+        ids = np.empty(n_tokens.size, np.int64)
+        rc = self._L.rvkv_bm_add_seqs(
+            self._h, n_tokens.ctypes.data_as(ctypes.c_void_p), n_tokens.size,
+            ids.ctypes.data_as(ctypes.c_void_p))
+        if rc != 0:
+            raise RvkvError("block_manager: pool full", rc)
+        return ids
+
+    def append_slots(self, seqs):
+        """Slots of one decode step for every sequence in `seqs` (in order):
+        (blocks u32[n], offsets u32[n], cow_src u32[k], cow_dst u32[k])."""
+        import numpy as np
+        seqs = np.ascontiguousarray(np.asarray(seqs, dtype=np.int64))
+        n = seqs.size
+        blocks = np.empty(n, np.uint32)
+        offs = np.empty(n, np.uint32)
+        cs = np.empty(max(n, 1), np.uint32)
+        cd = np.empty(max(n, 1), np.uint32)
+        k = ctypes.c_uint32()
+        P = ctypes.c_void_p
+        rc = self._L.rvkv_bm_append_slots(
+            self._h, seqs.ctypes.data_as(P), n, blocks.ctypes.data_as(P),
+            offs.ctypes.data_as(P), cs.ctypes.data_as(P),
+            cd.ctypes.data_as(P), ctypes.byref(k))
+        if rc != 0:
+            raise RvkvError("block_manager: append_slots failed "
+                            f"after {k.value} copies", rc)
+        return blocks, offs, cs[:k.value].copy(), cd[:k.value].copy()
+
+    def fill_tables(self, seqs, max_blocks: int, out=None, lens_out=None):
+        """Padded block tables [n, max_blocks] and token counts of `seqs`."""
+        import numpy as np
+        seqs = np.ascontiguousarray(np.asarray(seqs, dtype=np.int64))
+        n = seqs.size
+        tables = out if out is not None else np.empty((n, max_blocks),
+                                                      np.uint32)
+        lens = lens_out if lens_out is not None else np.empty(n, np.uint32)
+        assert tables.shape == (n, max_blocks) and tables.dtype == np.uint32
+        P = ctypes.c_void_p
+        rc = self._L.rvkv_bm_fill_tables(
+            self._h, seqs.ctypes.data_as(P), n, max_blocks,
+            tables.ctypes.data_as(P), lens.ctypes.data_as(P))
+        if rc != 0:
+            raise RvkvError("block_manager: fill_tables failed (unknown "
+                            "sequence or table longer than max_blocks)", rc)
+        return tables, lens
+
     def slot(self, seq: int, pos: int) -> Tuple[int, int]:
         """logical_to_physical(pos)."""
         blk, off = ctypes.c_uint32(), ctypes.c_uint32()

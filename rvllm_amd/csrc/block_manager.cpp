@@ -167,6 +167,69 @@ int rvkv_bm_append_slot(rvkv_bm *bm, int64_t seq, uint32_t *block,
   return RVKV_OK;
 }
 
+int rvkv_bm_free_seqs(rvkv_bm *bm, const int64_t *seqs, uint32_t n) {
+  if (!bm || (n && !seqs)) return RVKV_EINVAL;
+  for (uint32_t i = 0; i < n; ++i) {
+    const int rc = rvkv_bm_free_seq(bm, seqs[i]);
+    if (rc != RVKV_OK) return rc;
+  }
+  return RVKV_OK;
+}
+
+int rvkv_bm_add_seqs(rvkv_bm *bm, const uint32_t *n_tokens, uint32_t n,
+                     int64_t *ids) {
+  if (!bm || (n && (!n_tokens || !ids))) return RVKV_EINVAL;
+  uint64_t need = 0;
+  for (uint32_t i = 0; i < n; ++i) need += bm->blocks_for(n_tokens[i]);
+  if (need > bm->free_list.size()) return RVKV_ENOMEM;  // all or nothing
+  for (uint32_t i = 0; i < n; ++i) ids[i] = rvkv_bm_add_seq(bm, n_tokens[i]);
+  return RVKV_OK;
+}
+
+int rvkv_bm_append_slots(rvkv_bm *bm, const int64_t *seqs, uint32_t n,
+                         uint32_t *blocks, uint32_t *offsets,
+                         uint32_t *cow_src, uint32_t *cow_dst,
+                         uint32_t *n_cow) {
+  if (!bm || (n && (!seqs || !blocks || !offsets || !cow_src || !cow_dst)) ||
+      !n_cow)
+    return RVKV_EINVAL;
+  uint32_t k = 0;
+  for (uint32_t i = 0; i < n; ++i) {
+    uint32_t cs, cd;
+    const int rc =
+        rvkv_bm_append_slot(bm, seqs[i], &blocks[i], &offsets[i], &cs, &cd);
+    if (rc != RVKV_OK) {
+      *n_cow = k;
+      return rc;
+    }
+    if (cs != UINT32_MAX) {
+      cow_src[k] = cs;
+      cow_dst[k] = cd;
+      ++k;
+    }
+  }
+  *n_cow = k;
+  return RVKV_OK;
+}
+
+int rvkv_bm_fill_tables(const rvkv_bm *bm, const int64_t *seqs, uint32_t n,
+                        uint32_t max_blocks, uint32_t *tables,
+                        uint32_t *ctx_lens) {
+  if (!bm || (n && (!seqs || !tables || !ctx_lens))) return RVKV_EINVAL;
+  for (uint32_t i = 0; i < n; ++i) {
+    auto it = bm->seqs.find(seqs[i]);
+    if (it == bm->seqs.end()) return RVKV_EINVAL;
+    const auto &t = it->second.table;
+    if (t.size() > max_blocks) return RVKV_EINVAL;
+    uint32_t *row = tables + (size_t)i * max_blocks;
+    const uint32_t pad = t.empty() ? 0 : t.back();
+    for (uint32_t j = 0; j < max_blocks; ++j)
+      row[j] = j < t.size() ? t[j] : pad;
+    ctx_lens[i] = it->second.num_tokens;
+  }
+  return RVKV_OK;
+}
+
 int rvkv_bm_slot(const rvkv_bm *bm, int64_t seq, uint32_t pos, uint32_t *block,
                  uint32_t *offset) {
   if (!bm || !block || !offset) return RVKV_EINVAL;

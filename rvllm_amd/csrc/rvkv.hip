@@ -1249,14 +1249,21 @@ int plan_build(rvkv_decode_plan *pl, const uint32_t *ctx_lens_host,
     }
     const uint32_t lo = (window > 0 && n > (uint32_t)window) ? n - window : 0;
     const uint32_t start = lo & ~255u;
-    const uint32_t k = div_up(n - start, P);
+    // Items of at most P tokens, with 1/8 slack so a sequence just past a
+    // multiple of P does not get a sliver item; split evenly on 256-token
+    // boundaries.
+    const uint32_t span = n - start;
+    uint32_t k = div_up(span, P + P / 8);
+    const uint32_t step = ((div_up(span, k) + 255u) & ~255u);
+    k = div_up(span, step);
     if (k == 1) {
       items.push_back(make_uint4(b, start, n, kNoSlot));
       continue;
     }
     for (uint32_t i = 0; i < k; ++i) {
-      const uint32_t t0 = start + i * P;
-      items.push_back(make_uint4(b, t0, t0 + P < n ? t0 + P : n, slots + i));
+      const uint32_t t0 = start + i * step;
+      items.push_back(
+          make_uint4(b, t0, t0 + step < n ? t0 + step : n, slots + i));
     }
     reds.push_back(make_uint4(b, slots, k, 0));
     slots += k;

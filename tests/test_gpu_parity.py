@@ -588,3 +588,38 @@ def test_decode_step_equals_append_then_decode(planned, src, G, hd, bs,
     assert (out_a - out_b).abs().max().item() < 5e-4
     db.ctx_lens = lens
     assert _decode_vs_oracle(a, 0, db, q, window=window) < ATOL
+
+
+# ---- continuous-batching churn through the block manager -------------------
+def test_churn_driver_parity():
+    """A few churn steps (finish 10%, admit 64-token prompts, decode all)
+    over a shuffled pool: the last step's appended rows are in the cache bit
+    for bit at the block manager's slots, and its decode output matches the
+    oracle over the cache the tables point to."""
+    from rvllm_amd.engine_sim import ChurnDriver
+    cfg = W.Config("churn", 9, 2, 4, 1, 256, 16, 48)
+    drv = ChurnDriver(cfg, 48, 200, prompt_len=64, churn=0.1, steps=8,
+                      seed=77)
+    for _ in range(6):
+        drv.step()
+    torch.cuda.synchronize()
+    tables, lens, blocks, offs = drv.last
+    st = drv.st
+    for layer in range(cfg.n_layers):
+        rows = st.read_blocks(layer, 0, dev_u32(blocks)).cpu().numpy()
+        got = rows.view(np.uint16)[np.arange(len(blocks)), offs]
+        want = orc.f32_to_f16_bits(drv.nk[layer].cpu().numpy())
+        assert np.array_equal(got, want)
+    db = W.DecodeBatch(cfg, drv.num_blocks, lens,
+                       [tables[i, :-(-int(n) // 16)] for i, n in
+                        enumerate(lens)], blocks, offs)
+    sample = list(range(0, 48, 5))
+    layer = 1
+    cache, padded, mb = oracle_subset(st, layer, [db.tables[b] for b in sample],
+                                      lens[sample])
+    want = orc.paged_decode_f64(cache, drv.q[layer].cpu().numpy()[sample],
+                                padded.reshape(-1), mb, lens[sample])
+    got = drv.out[layer].cpu().numpy()[sample]
+    assert np.abs(got - want).max() < ATOL
+    assert drv.bm.available() + sum(
+        drv.bm.num_blocks_of(int(s)) for s in drv.running) == drv.num_blocks

@@ -159,3 +159,27 @@ def test_shuffled_free_list_is_a_permutation_and_seeded():
         return bm.table(s)
     a, b, c = order(1), order(1), order(2)
     assert a == b and a != c and sorted(a) == list(range(64))
+
+
+def test_batch_slots_and_tables_match_single_calls():
+    import numpy as np
+    bm = BlockManager(64, 4)
+    bm.shuffle_free(3)
+    owner = bm.add_seq(8)
+    a = bm.add_seq(3)
+    b = bm.fork_seq(owner, 8, 8)
+    c = bm.fork_seq(owner, 6, 6)  # partial shared last block -> CoW
+    seqs = [owner, a, b, c]
+    blocks, offs, cs, cd = bm.append_slots(seqs)
+    assert len(cs) == 1 and cd[0] == bm.table(c)[1]
+    for s, blk, off in zip(seqs, blocks, offs):
+        pos = bm.num_tokens(s) - 1
+        assert bm.slot(s, pos) == (blk, off)
+    tables, lens = bm.fill_tables(seqs, 5)
+    for i, s in enumerate(seqs):
+        t = bm.table(s)
+        assert list(tables[i, :len(t)]) == t
+        assert (tables[i, len(t):] == t[-1]).all()
+        assert lens[i] == bm.num_tokens(s)
+    with pytest.raises(RvkvError):
+        bm.fill_tables(seqs, 1)  # a table longer than max_blocks
