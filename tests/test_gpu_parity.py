@@ -623,3 +623,64 @@ def test_churn_driver_parity():
     assert np.abs(got - want).max() < ATOL
     assert drv.bm.available() + sum(
         drv.bm.num_blocks_of(int(s)) for s in drv.running) == drv.num_blocks
+
+
+# ---- full-size append / gather (size-independent checks) -------------------
+def test_full_size_gather_llama_layer():
+    """One full Llama-3.2-1B layer (8192 blocks, 64 x 2048): the padded
+    gather equals the oracle's gather of the same cache bit for bit."""
+    c = W.CONFIGS["llama-3.2-1b"]
+    db = W.uniform_batch(c, 2048)
+    st = HipKvStorage(1, db.num_blocks, c.block_size, c.n_kv_heads,
+                      c.head_dim)
+    fill_layer(st, 0, seed=41)
+    ids = dev_u32(np.arange(db.num_blocks))
+    ref = orc.KvCache(db.num_blocks, c.block_size, c.n_kv_heads, c.head_dim,
+                      orc.F16)
+    ref.k[:] = bits(st.read_blocks(0, 0, ids))
+    ref.v[:] = bits(st.read_blocks(0, 1, ids))
+    plan = HipGatherPlan([(t, 2048) for t in db.tables])
+    n = db.batch * c.n_kv_heads * 2048 * c.head_dim
+    ok = torch.empty(n, dtype=torch.float16, device="cuda")
+    ov = torch.empty(n, dtype=torch.float16, device="cuda")
+    st.gather(0, plan, ok, ov)
+    idx, mb, cl = orc.gather_plan(db.tables, db.ctx_lens)
+    wk, wv = ref.gather(idx, db.batch, mb, cl)
+    assert np.array_equal(bits(ok).reshape(wk.shape), orc.f32_to_f16_bits(wk))
+    assert np.array_equal(bits(ov).reshape(wv.shape), orc.f32_to_f16_bits(wv))
+
+
+def test_full_size_prefill_append_checksums():
+    """Qwen3-0.6B prefill at full size for one layer (256 x 4096 tokens
+    scattered through permuted tables, f32 source): per-block FNV-1a
+    checksums computed on the GPU equal the oracle's for a seeded 2 %
+    sample of blocks, plus every block of one sequence."""
+    c = W.CONFIGS["qwen3-0.6b"]
+    db = W.uniform_batch(c, 4096)
+    bs = c.block_size
+    st = HipKvStorage(1, db.num_blocks, bs, c.n_kv_heads, c.head_dim)
+    sb = np.concatenate([np.repeat(t, bs) for t in db.tables])
+    so = np.tile(np.arange(bs, dtype=np.uint32), db.num_blocks)
+    g = torch.Generator("cuda").manual_seed(5)
+    n_tok = sb.size
+    k = torch.randn((n_tok, c.n_kv_heads, c.head_dim), generator=g,
+                    device="cuda") * 0.5
+    st.write_tokens(0, dev_u32(sb), dev_u32(so), k, k)
+    rng = np.random.default_rng(6)
+    blocks = np.unique(np.concatenate([
+        rng.choice(db.num_blocks, db.num_blocks // 50, replace=False),
+        db.tables[17]])).astype(np.uint32)
+    got = st.block_checksums(0, 0, dev_u32(blocks)).cpu().numpy().view(
+        np.uint64)
+    # token rows that landed in each sampled block, in slot order
+    tok_of = np.empty(db.num_blocks * bs, np.int64)
+    tok_of[sb.astype(np.int64) * bs + so] = np.arange(n_tok)
+    rows = tok_of[(blocks.astype(np.int64)[:, None] * bs +
+                   np.arange(bs)).reshape(-1)]
+    src = k[torch.from_numpy(rows).cuda()].cpu().numpy()
+    ref = orc.KvCache(len(blocks), bs, c.n_kv_heads, c.head_dim, orc.F16)
+    ref.k[:] = orc.f32_to_f16_bits(src).reshape(ref.k.shape)
+    want = ref.checksums(0, np.arange(len(blocks)))
+    assert np.array_equal(got, want)
+    v_sum = st.block_checksums(0, 1, dev_u32(blocks)).cpu().numpy()
+    assert np.array_equal(v_sum.view(np.uint64), want)  # k was used for v
