@@ -93,7 +93,9 @@ def measured_traffic(config, batch, unfused):
     known size) for this workload, from the committed summary, or None."""
     if batch:
         return None
-    name = "paged_decode_traffic.json" if unfused else "decode_step_traffic.json"
+    if unfused:
+        return None
+    name = "decode_step_traffic.json"
     path = os.path.join(ROOT, "profiles", name)
     try:
         with open(path) as f:
