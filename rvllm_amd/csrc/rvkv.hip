@@ -866,12 +866,13 @@ uint32_t partition_tokens(const rvkv_pool *p, uint32_t batch, uint32_t n_heads,
   return P;
 }
 
-// Wavefronts per decode workgroup: enough that the grid holds ~2048 waves
-// (8 per CU) when the batch is small; RVKV_DECODE_WAVES overrides.
+// Wavefronts per decode workgroup: four (the waves of a workgroup split its
+// context) unless the grid alone already has >= 2048 workgroups (8 per CU);
+// RVKV_DECODE_WAVES overrides.
 uint32_t decode_waves(uint64_t workgroups) {
   static const uint32_t forced = env_u32("RVKV_DECODE_WAVES");
   if (forced == 1 || forced == 2 || forced == 4) return forced;
-  return workgroups >= 2048 ? 1 : workgroups >= 1024 ? 2 : 4;
+  return workgroups >= 2048 ? 1 : 4;
 }
 
 struct WsLayout {

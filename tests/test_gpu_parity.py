@@ -684,3 +684,56 @@ def test_full_size_prefill_append_checksums():
     assert np.array_equal(got, want)
     v_sum = st.block_checksums(0, 1, dev_u32(blocks)).cpu().numpy()
     assert np.array_equal(v_sum.view(np.uint64), want)  # k was used for v
+
+
+# ---- HIP graph capture (serving loops) -------------------------------------
+def test_graph_capture_replays_match_eager():
+    """rvkv_decode_step (uniform) and rvkv_paged_decode_planned captured in a
+    HIP graph: every replay, with eager work and new q values between
+    replays, equals the eager result (the kernels record no memset)."""
+    from rvllm_amd.kv_storage import HipDecodePlan
+    bs, nkv, hd, H = 16, 4, 128, 8
+    cfg = W.Config("gr", 9, 1, H, nkv, hd, bs, 6)
+    lens = np.array([3000, 17, 900, 2048, 64, 700], np.uint32)
+    db = W.ragged_batch(cfg, lens, seed=8)
+    st = HipKvStorage(1, db.num_blocks, bs, nkv, hd)
+    fill_layer(st, 0, seed=12)
+    g = torch.Generator("cuda").manual_seed(9)
+    nk = torch.randn(6, nkv, hd, device="cuda", generator=g)
+    nv = torch.randn(6, nkv, hd, device="cuda", generator=g)
+    q = torch.randn(6, H, hd, device="cuda", generator=g)
+    sb, so = dev_u32(db.slot_block), dev_u32(db.slot_off)
+    tables, ctx = dev_u32(db.padded_tables()), dev_u32(lens)
+    max_ctx = int(lens.max())
+    ws = st.alloc_workspace(6, H, max_ctx)
+    plan = HipDecodePlan(st, lens, H)
+    out_g1 = torch.empty_like(q)
+    out_g2 = torch.empty_like(q)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        st.set_stream(side)
+        st.decode_step(0, nk, nv, sb, so, q, tables, ctx, max_ctx,
+                       out=out_g1, ws=ws)  # warm-up outside the graph
+        st.paged_decode_planned(0, plan, q, tables, ctx, out=out_g2)
+    torch.cuda.current_stream().wait_stream(side)
+    with torch.cuda.graph(graph):
+        st.set_stream(torch.cuda.current_stream())
+        st.decode_step(0, nk, nv, sb, so, q, tables, ctx, max_ctx,
+                       out=out_g1, ws=ws)
+        st.paged_decode_planned(0, plan, q, tables, ctx, out=out_g2)
+    st.set_stream(torch.cuda.current_stream())
+    for rep in range(3):
+        q.copy_(torch.randn(6, H, hd, device="cuda", generator=g))
+        out_g1.zero_()
+        out_g2.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        e1 = st.decode_step(0, nk, nv, sb, so, q, tables, ctx, max_ctx,
+                            ws=st.alloc_workspace(6, H, max_ctx))
+        e2 = st.paged_decode_planned(0, plan, q, tables, ctx)
+        torch.cuda.synchronize()
+        assert torch.equal(out_g1, e1), rep
+        assert torch.equal(out_g2, e2), rep
