@@ -56,6 +56,9 @@ def parse():
                    help="time the prefill append instead (BASELINE configs[2]: "
                         "every sequence's whole context scattered into the "
                         "paged cache, all layers; source dtype f32 or f16)")
+    p.add_argument("--prep", action="store_true",
+                   help="time the fused attention prep + append over the "
+                   "prefill batch of --config instead")
     p.add_argument("--graph", action="store_true",
                    help="time the step as one HIP graph replay (all layers' "
                         "append + decode launches captured once)")
@@ -192,6 +195,109 @@ def cpu_baseline(orc, W, st, db, budget_s):
     }
 
 
+def prompt_slots(torch, db):
+    """Device slot lists (block id, offset) of every prompt token of the
+    batch, in sequence order, plus each token's position."""
+    bs = db.cfg.block_size
+    sb, so, ps = [], [], []
+    for t, n in zip(db.tables, db.ctx_lens):
+        pos = np.arange(int(n))
+        sb.append(np.asarray(t, np.uint32)[pos // bs])
+        so.append((pos % bs).astype(np.uint32))
+        ps.append(pos)
+    dev = lambda a: torch.from_numpy(np.concatenate(a).view(np.int32)).cuda()
+    return dev(sb), dev(so), np.concatenate(ps)
+
+
+def run_prep(args, torch, W):
+    """Fused attention prep over a prefill batch: per token, q/k/v rows
+    (f32, as the QKV projection leaves them) get the bias, the per-head
+    RMS norm (q and k) and RoPE, q is written back in f32 and k/v are
+    appended into the f16 cache at the token's slot; one rvkv_attn_prep per
+    layer. Bias and norm weights are used when the model has them
+    (Qwen2.5: bias, Qwen3: QK norm)."""
+    from rvllm_amd.kv_storage import HipKvStorage
+    from rvllm_amd.rope import rope_cos_sin
+    db = build_workload(W, args.config, args.batch)
+    c = db.cfg
+    st = HipKvStorage(c.n_layers, db.num_blocks, c.block_size, c.n_kv_heads,
+                      c.head_dim)
+    sb, so, pos = prompt_slots(torch, db)
+    n_tok = sb.numel()
+    H, KV, hd = c.n_heads, c.n_kv_heads, c.head_dim
+    g = torch.Generator(device="cuda")
+    g.manual_seed(c.seed)
+    rnd = lambda *shape: torch.randn(shape, generator=g, device="cuda")
+    q, k, v = rnd(n_tok, H, hd), rnd(n_tok, KV, hd), rnd(n_tok, KV, hd)
+    q_out = torch.empty_like(q)
+    cs, sn = rope_cos_sin(c.rope_theta, hd, pos)
+    cs, sn = torch.from_numpy(cs).cuda(), torch.from_numpy(sn).cuda()
+    opt = {}
+    if c.qkv_bias:
+        opt.update(q_bias=rnd(H * hd), k_bias=rnd(KV * hd),
+                   v_bias=rnd(KV * hd))
+    if c.qk_norm:
+        opt.update(q_norm=rnd(hd), k_norm=rnd(hd))
+
+    def step():
+        for layer in range(c.n_layers):
+            st.attn_prep(layer, q, k, v, cs, sn, sb, so, eps=1e-6,
+                         q_out=q_out, **opt)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    launch_ms = e0.elapsed_time(e1) / (args.steps * c.n_layers)
+    per_launch = W.prep_bytes(n_tok, c)
+    achieved = per_launch / (launch_ms * 1e-3) / 1e9
+    res = {
+        "metric": "attention prep + append HBM GB/s, 1 MI355X",
+        "value": round(per_launch * c.n_layers / dt / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32 q/k/v -> f32 q, f16 cache",
+        "data": "synthetic N(0,1) rows and weights, seeded permuted tables",
+        "config": {
+            "workload": f"{c.name} attn prep: {n_tok} tokens "
+                        f"({db.batch} seqs x {int(db.ctx_lens.max())}) x "
+                        f"{c.n_layers} layers, {H} q / {KV} kv heads, "
+                        f"head_dim {hd}, bias {c.qkv_bias}, "
+                        f"qk_norm {c.qk_norm}",
+            "global_batch": db.batch,
+            "seq_len": int(db.ctx_lens.max()),
+            "parallelism": "single GPU",
+        },
+        "tok_per_s": round(n_tok / dt, 1),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": f"attn_prep_kernel<{hd}>",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "algorithmic_bytes_per_launch": per_launch,
+            "avg_launch_ms": round(launch_ms, 5),
+        },
+    }
+    print(json.dumps(res), flush=True)
+
+
 def run_prefill(args, torch, W):
     """Scatter-only prefill append: every sequence's ctx tokens (K and V
     rows [tokens, n_kv, hd] of the source dtype) appended into its
@@ -205,13 +311,7 @@ def run_prefill(args, torch, W):
     st = HipKvStorage(c.n_layers, db.num_blocks, c.block_size, c.n_kv_heads,
                       c.head_dim)
     bs = c.block_size
-    sb, so = [], []
-    for t, n in zip(db.tables, db.ctx_lens):
-        pos = np.arange(int(n))
-        sb.append(np.asarray(t, np.uint32)[pos // bs])
-        so.append((pos % bs).astype(np.uint32))
-    sb = torch.from_numpy(np.concatenate(sb).view(np.int32)).cuda()
-    so = torch.from_numpy(np.concatenate(so).view(np.int32)).cuda()
+    sb, so, _ = prompt_slots(torch, db)
     n_tok = sb.numel()
     dt_src = torch.float32 if args.prefill == "f32" else torch.float16
     g = torch.Generator(device="cuda")
@@ -382,6 +482,9 @@ def main():
         return
     if args.prefill:
         run_prefill(args, torch, W)
+        return
+    if args.prep:
+        run_prep(args, torch, W)
         return
     db = build_workload(W, args.config, args.batch)
     c = db.cfg

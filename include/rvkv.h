@@ -200,6 +200,29 @@ int rvkv_decode_step(rvkv_pool *pool, const rvkv_decode_plan *plan,
                      uint32_t max_ctx_len, float scale, int32_t window,
                      float *out, void *ws, size_t ws_bytes);
 
+/* ---- next row (f)1: attention prep fused with the append -----------------
+ * Everything between the QKV projection and attention for `rows` tokens,
+ * as src/model.rs:600-639 computes it (the reference's own fused form is
+ * the Metal attn_prep, src/metal/kernels/attention.metal:8-88):
+ *   q, k: + bias (optional) -> per-head RMS norm (optional, q_norm/k_norm
+ *         [head_dim], eps) -> rotate-half RoPE with this row's cos/sin;
+ *   v:    + bias (optional).
+ * q_in [rows, n_heads, hd], k_in/v_in [rows, n_kv_heads, hd] f32 (device);
+ * biases [heads*hd] or NULL; cos/sin [rows, hd/2] f32 (rope_cos_sin of each
+ * row's position, src/model.rs:224-250, built once per forward).
+ * The rotated q goes to q_out [rows, n_heads, hd] f32; k and v are rounded
+ * to f16 (nearest-even) and written to (slot_block[i], slot_off[i]) of
+ * `layer`, as rvkv_append would. head_dim in {32, 64, 128, 256}; every
+ * float buffer 16-byte aligned (RVKV_EINVAL otherwise). Rows whose slot is
+ * out of range still produce q_out but write no k/v. */
+int rvkv_attn_prep(rvkv_pool *pool, uint32_t layer, const float *q_in,
+                   const float *k_in, const float *v_in, uint32_t rows,
+                   uint32_t n_heads, const float *q_bias, const float *k_bias,
+                   const float *v_bias, const float *q_norm,
+                   const float *k_norm, float eps, const float *cos_t,
+                   const float *sin_t, const uint32_t *slot_block,
+                   const uint32_t *slot_off, float *q_out);
+
 /* ---- a10: prefix-cache copy-on-write -------------------------------------
  * No counterpart in the reference (rvllm never mutates a shared block; its
  * only copy is the whole-cache KvStorage::clone, src/kv_storage.rs:15-33).

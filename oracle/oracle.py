@@ -80,6 +80,12 @@ def lib() -> ctypes.CDLL:
         L.orc_decode_step.restype = ctypes.c_int
         L.orc_decode_step.argtypes = [P, P, u32, u32, u32, u32, P, P, P, P, P,
                                       u32, P, u32, u32, P, P, u32]
+        L.orc_rope_cos_sin.argtypes = [f32, P, u32, P, u32, P, P]
+        L.orc_rms_norm.argtypes = [P, P, u32, u32, f32, P]
+        L.orc_rope_apply.argtypes = [P, P, P, u32, u32, P]
+        L.orc_attn_prep.restype = ctypes.c_int
+        L.orc_attn_prep.argtypes = [P, P, P, u32, u32, u32, u32, P, P, P, P,
+                                    P, f32, P, P, P, P, P, P, u32, u32, P]
         _lib = L
     return _lib
 
@@ -266,3 +272,59 @@ def decode_step(cache: KvCache, slot_block, slot_off, new_k, new_v,
     if rc:
         raise ValueError("decode_step: slot out of range")
     return out
+
+
+# ---- SURVEY (f)1: attention prep (bias, QK RMS norm, RoPE) + append ------
+def rope_cos_sin(rope_theta, head_dim, positions, factors=None):
+    """rope_cos_sin (src/model.rs:224-250): f32 cos, sin [n, hd/2]."""
+    pos = _u32(positions)
+    half = head_dim // 2
+    c = np.empty((pos.size, half), np.float32)
+    s = np.empty((pos.size, half), np.float32)
+    fac = _f32(factors) if factors is not None else None
+    lib().orc_rope_cos_sin(float(rope_theta), _p(fac) if fac is not None
+                           else None, head_dim, _p(pos), pos.size, _p(c),
+                           _p(s))
+    return c, s
+
+
+def rms_norm(x, w, eps):
+    """rms_norm over the last dim (src/model.rs:200-215)."""
+    x, w = _f32(x), _f32(w)
+    out = np.empty_like(x)
+    dim = x.shape[-1]
+    lib().orc_rms_norm(_p(x), _p(w), x.size // dim, dim, float(eps), _p(out))
+    return out
+
+
+def rope_apply(x, cos, sin):
+    """rope_apply, rotate-half (src/model.rs:252-264); x [rows, hd]."""
+    x, cos, sin = _f32(x), _f32(cos), _f32(sin)
+    out = np.empty_like(x)
+    lib().orc_rope_apply(_p(x), _p(cos), _p(sin), x.shape[0], x.shape[1],
+                         _p(out))
+    return out
+
+
+def attn_prep(cache: KvCache, q_in, k_in, v_in, cos, sin, slot_block,
+              slot_off, q_bias=None, k_bias=None, v_bias=None, q_norm=None,
+              k_norm=None, eps=1e-6):
+    """The prep segment of Attention::forward (src/model.rs:600-626) plus
+    write_tokens: returns q_out, mutates the f16 cache."""
+    assert cache.dtype == F16
+    q_in, k_in, v_in = _f32(q_in), _f32(k_in), _f32(v_in)
+    rows, n_heads, hd = q_in.shape
+    n_kv = k_in.shape[1]
+    opt = [None if a is None else _f32(a) for a in
+           (q_bias, k_bias, v_bias, q_norm, k_norm)]
+    cos, sin = _f32(cos), _f32(sin)
+    sb, so = _u32(slot_block), _u32(slot_off)
+    q_out = np.empty_like(q_in)
+    rc = lib().orc_attn_prep(
+        _p(q_in), _p(k_in), _p(v_in), rows, n_heads, n_kv, hd,
+        *[None if a is None else _p(a) for a in opt], float(eps), _p(cos),
+        _p(sin), _p(sb), _p(so), _p(cache.k), _p(cache.v), cache.num_blocks,
+        cache.bs, _p(q_out))
+    if rc:
+        raise ValueError("attn_prep: slot out of range")
+    return q_out

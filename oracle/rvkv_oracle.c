@@ -457,3 +457,109 @@ int orc_decode_step(uint16_t *cache_k, uint16_t *cache_v, uint32_t num_blocks,
   pthread_mutex_destroy(&J.mu);
   return 0;
 }
+
+/* ---- SURVEY (f)1: attention prep before the append -------------------------
+ * rope_cos_sin (src/model.rs:224-250): theta_j = rope_theta^(-2j/hd) (f32),
+ * divided by factors[j] when given (Llama 3); angle = pos * theta_j;
+ * cos/sin [n, hd/2] in f32. */
+void orc_rope_cos_sin(float rope_theta, const float *factors, uint32_t hd,
+                      const uint32_t *positions, uint32_t n, float *cos_out,
+                      float *sin_out) {
+  uint32_t half = hd / 2;
+  for (uint32_t j = 0; j < half; ++j) {
+    float theta = powf(rope_theta, -2.0f * (float)j / (float)hd);
+    if (factors) theta = theta / factors[j];
+    for (uint32_t i = 0; i < n; ++i) {
+      float a = (float)positions[i] * theta;
+      cos_out[(size_t)i * half + j] = cosf(a);
+      sin_out[(size_t)i * half + j] = sinf(a);
+    }
+  }
+}
+
+/* rms_norm over the last dim (src/model.rs:200-215): rms = sqrt(mean(x^2) +
+ * eps); out = x / rms * w. rows x dim, in place allowed. */
+void orc_rms_norm(const float *x, const float *w, uint32_t rows, uint32_t dim,
+                  float eps, float *out) {
+  for (uint32_t r = 0; r < rows; ++r) {
+    const float *xr = x + (size_t)r * dim;
+    float ss = 0.0f;
+    for (uint32_t d = 0; d < dim; ++d) ss += xr[d] * xr[d];
+    float rms = sqrtf(ss / (float)dim + eps);
+    for (uint32_t d = 0; d < dim; ++d)
+      out[(size_t)r * dim + d] = (xr[d] / rms) * w[d];
+  }
+}
+
+/* rope_apply, rotate-half (src/model.rs:252-264), rows x hd with one cos/sin
+ * row per input row. */
+void orc_rope_apply(const float *x, const float *cos_t, const float *sin_t,
+                    uint32_t rows, uint32_t hd, float *out) {
+  uint32_t half = hd / 2;
+  for (uint32_t r = 0; r < rows; ++r)
+    for (uint32_t j = 0; j < half; ++j) {
+      float first = x[(size_t)r * hd + j], second = x[(size_t)r * hd + half + j];
+      float c = cos_t[(size_t)r * half + j], s = sin_t[(size_t)r * half + j];
+      float a = first * c, b = second * s, e = first * s, f = second * c;
+      out[(size_t)r * hd + j] = a - b;
+      out[(size_t)r * hd + half + j] = e + f;
+    }
+}
+
+/* The prep segment of Attention::forward (src/model.rs:600-626) for `rows`
+ * tokens, then write_tokens of K/V (src/model.rs:628-639): q/k/v inputs are
+ * the projection outputs [rows, heads, hd] (bias not yet added); q_out gets
+ * the normed + rotated q; the f16 cache (logical layout) gets the normed +
+ * rotated k and the biased v at each row's slot. NULL bias/norm = absent. */
+int orc_attn_prep(const float *q_in, const float *k_in, const float *v_in,
+                  uint32_t rows, uint32_t n_heads, uint32_t n_kv, uint32_t hd,
+                  const float *q_bias, const float *k_bias, const float *v_bias,
+                  const float *q_norm, const float *k_norm, float eps,
+                  const float *cos_t, const float *sin_t,
+                  const uint32_t *slot_block, const uint32_t *slot_off,
+                  uint16_t *cache_k, uint16_t *cache_v, uint32_t num_blocks,
+                  uint32_t bs, float *q_out) {
+  uint32_t half = hd / 2;
+  float *buf = (float *)malloc((size_t)hd * 4 * 2);
+  float *nb = buf + hd;
+  for (uint32_t r = 0; r < rows; ++r) {
+    const float *cr = cos_t + (size_t)r * half, *sr = sin_t + (size_t)r * half;
+    for (uint32_t h = 0; h < n_heads + 2 * n_kv; ++h) {
+      int is_q = h < n_heads, is_v = h >= n_heads + n_kv;
+      uint32_t hh = is_q ? h : (is_v ? h - n_heads - n_kv : h - n_heads);
+      const float *src =
+          (is_q ? q_in + ((size_t)r * n_heads + hh) * hd
+                : (is_v ? v_in : k_in) + ((size_t)r * n_kv + hh) * hd);
+      const float *bias = is_q ? q_bias : (is_v ? v_bias : k_bias);
+      for (uint32_t d = 0; d < hd; ++d)
+        buf[d] = bias ? src[d] + bias[(size_t)hh * hd + d] : src[d];
+      if (is_v) {
+        if (slot_block[r] >= num_blocks || slot_off[r] >= bs) {
+          free(buf);
+          return -1;
+        }
+        size_t dst = (((size_t)slot_block[r] * bs + slot_off[r]) * n_kv + hh) * hd;
+        for (uint32_t d = 0; d < hd; ++d) cache_v[dst + d] = orc_f32_to_f16(buf[d]);
+        continue;
+      }
+      const float *w = is_q ? q_norm : k_norm;
+      if (w) {
+        orc_rms_norm(buf, w, 1, hd, eps, nb);
+        memcpy(buf, nb, (size_t)hd * 4);
+      }
+      orc_rope_apply(buf, cr, sr, 1, hd, nb);
+      if (is_q) {
+        memcpy(q_out + ((size_t)r * n_heads + hh) * hd, nb, (size_t)hd * 4);
+      } else {
+        if (slot_block[r] >= num_blocks || slot_off[r] >= bs) {
+          free(buf);
+          return -1;
+        }
+        size_t dst = (((size_t)slot_block[r] * bs + slot_off[r]) * n_kv + hh) * hd;
+        for (uint32_t d = 0; d < hd; ++d) cache_k[dst + d] = orc_f32_to_f16(nb[d]);
+      }
+    }
+  }
+  free(buf);
+  return 0;
+}

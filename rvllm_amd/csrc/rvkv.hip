@@ -191,6 +191,132 @@ __global__ void __launch_bounds__(256)
 }
 
 // ---------------------------------------------------------------------------
+// SURVEY (f)1: attention prep + append. Per (row, head slot) - slots are the
+// n_heads q heads, then the n_kv k heads, then the n_kv v heads - T threads
+// each hold PPT rotate-half pairs (j, j + HD/2): optional bias, optional
+// per-head RMS norm (q and k; sum of squares reduced over the T lanes), RoPE
+// with this row's cos/sin (q and k), then q to q_out (f32) and k/v rounded
+// to f16 into the row's slot. Mirrors src/model.rs:600-639; the Metal
+// attn_prep (attention.metal:8-88) is the reference's own fused version.
+// Products and sums are kept unfused (no FMA contraction), as the CPU path
+// computes them.
+struct PrepArgs {
+  const float *q_in, *k_in, *v_in;
+  const float *q_bias, *k_bias, *v_bias, *q_norm, *k_norm;
+  const float *cos_t, *sin_t;
+  const uint32_t *slot_block, *slot_off;
+  float *q_out;
+  uint16_t *kc, *vc;
+  uint32_t rows, n_heads, n_kv, num_blocks, bs;
+  float eps;
+};
+
+__device__ __forceinline__ void ld8(const float *p, float *x) {
+  const float4 a = *reinterpret_cast<const float4 *>(p);
+  const float4 b = *reinterpret_cast<const float4 *>(p + 4);
+  x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+  x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+}
+__device__ __forceinline__ void st8(float *p, const float *x) {
+  *reinterpret_cast<float4 *>(p) = make_float4(x[0], x[1], x[2], x[3]);
+  *reinterpret_cast<float4 *>(p + 4) = make_float4(x[4], x[5], x[6], x[7]);
+}
+__device__ __forceinline__ uint32_t h2bits(float lo, float hi) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)lo) |
+         ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hi) << 16);
+}
+__device__ __forceinline__ void st8h(uint16_t *p, const float *x) {
+  *reinterpret_cast<uint4 *>(p) = make_uint4(
+      h2bits(x[0], x[1]), h2bits(x[2], x[3]), h2bits(x[4], x[5]),
+      h2bits(x[6], x[7]));
+}
+
+// One item = one (row, head slot): slots [0, n_heads) are q heads, then the
+// n_kv k heads, then the n_kv v heads. Each lane owns 8 consecutive
+// rotate-half pairs (d, d + HD/2), so every access is 16 bytes wide; the
+// T = HD/16 lanes of an item reduce the RMS sum of squares by xor shuffles.
+// Element arithmetic is the reference's, unfused (contract off): bias add,
+// x / rms * w, then x0*c - x1*s and x0*s + x1*c.
+template <int HD>
+__global__ void __launch_bounds__(256) attn_prep_kernel(PrepArgs a) {
+#pragma clang fp contract(off)
+  constexpr int HALF = HD / 2;
+  constexpr int V = 8;
+  constexpr int T = HALF / V;  // lanes per item: 2, 4, 8, 16
+  const uint32_t n_slots = a.n_heads + 2 * a.n_kv;
+  const uint32_t item = blockIdx.x * (256 / T) + threadIdx.x / T;
+  if (item >= a.rows * n_slots) return;  // whole items exit together
+  const int j = (threadIdx.x % T) * V;
+  const uint32_t row = item / n_slots;
+  const uint32_t slot = item - row * n_slots;
+  const bool is_q = slot < a.n_heads;
+  const bool is_v = slot >= a.n_heads + a.n_kv;
+  const uint32_t hh = is_q ? slot : (is_v ? slot - a.n_heads - a.n_kv
+                                          : slot - a.n_heads);
+  const float *src =
+      is_q ? a.q_in + ((size_t)row * a.n_heads + hh) * HD
+           : (is_v ? a.v_in : a.k_in) + ((size_t)row * a.n_kv + hh) * HD;
+  float x0[V], x1[V];
+  ld8(src + j, x0);
+  ld8(src + j + HALF, x1);
+  const float *bias = is_q ? a.q_bias : (is_v ? a.v_bias : a.k_bias);
+  if (bias) {
+    float b0[V], b1[V];
+    ld8(bias + (size_t)hh * HD + j, b0);
+    ld8(bias + (size_t)hh * HD + j + HALF, b1);
+#pragma unroll
+    for (int p = 0; p < V; ++p) {
+      x0[p] = x0[p] + b0[p];
+      x1[p] = x1[p] + b1[p];
+    }
+  }
+  const uint32_t blk = a.slot_block[row], off = a.slot_off[row];
+  const bool slot_ok = blk < a.num_blocks && off < a.bs;
+  const size_t dst = (((size_t)blk * a.n_kv + hh) * a.bs + off) * HD;
+  if (is_v) {
+    if (slot_ok) {
+      st8h(a.vc + dst + j, x0);
+      st8h(a.vc + dst + j + HALF, x1);
+    }
+    return;
+  }
+  const float *w = is_q ? a.q_norm : a.k_norm;
+  if (w) {  // uniform over the T lanes of this item
+    float ss = 0.f;
+#pragma unroll
+    for (int p = 0; p < V; ++p) ss = ss + (x0[p] * x0[p] + x1[p] * x1[p]);
+#pragma unroll
+    for (int o = T / 2; o >= 1; o >>= 1) ss = ss + __shfl_xor(ss, o, T);
+    const float rms = sqrtf(ss / (float)HD + a.eps);
+    float w0[V], w1[V];
+    ld8(w + j, w0);
+    ld8(w + j + HALF, w1);
+#pragma unroll
+    for (int p = 0; p < V; ++p) {
+      x0[p] = (x0[p] / rms) * w0[p];
+      x1[p] = (x1[p] / rms) * w1[p];
+    }
+  }
+  float c[V], sn[V];
+  ld8(a.cos_t + (size_t)row * HALF + j, c);
+  ld8(a.sin_t + (size_t)row * HALF + j, sn);
+  float r0[V], r1[V];
+#pragma unroll
+  for (int p = 0; p < V; ++p) {
+    r0[p] = x0[p] * c[p] - x1[p] * sn[p];
+    r1[p] = x0[p] * sn[p] + x1[p] * c[p];
+  }
+  if (is_q) {
+    float *o = a.q_out + ((size_t)row * a.n_heads + hh) * HD;
+    st8(o + j, r0);
+    st8(o + j + HALF, r1);
+  } else if (slot_ok) {
+    st8h(a.kc + dst + j, r0);
+    st8h(a.kc + dst + j + HALF, r1);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // a10: copy-on-write block copy, every layer, K and V. grid.y = pair,
 // grid.z = tensor (2 * n_layers); threads stride over the block's 16-byte
 // (or 2-byte) words.
@@ -1496,6 +1622,74 @@ int rvkv_decode_step(rvkv_pool *pool, const rvkv_decode_plan *plan,
   const dim3 grid(w.n_parts, pool->n_kv * a.n_sub, batch);
   return launch_decode_pair(op, a, pool->head_dim, gt, grid,
                             dim3(n_heads, batch), w.n_parts > 1, pool->stream);
+}
+
+int rvkv_attn_prep(rvkv_pool *pool, uint32_t layer, const float *q_in,
+                   const float *k_in, const float *v_in, uint32_t rows,
+                   uint32_t n_heads, const float *q_bias, const float *k_bias,
+                   const float *v_bias, const float *q_norm,
+                   const float *k_norm, float eps, const float *cos_t,
+                   const float *sin_t, const uint32_t *slot_block,
+                   const uint32_t *slot_off, float *q_out) {
+  const char *op = "attn_prep";
+  if (!pool) return fail(RVKV_EINVAL, op, "pool is NULL");
+  if (layer >= pool->n_layers)
+    return fail(RVKV_EINVAL, op, "layer out of range");
+  if (rows == 0) return RVKV_OK;
+  if (n_heads == 0 || n_heads % pool->n_kv != 0)
+    return fail(RVKV_EINVAL, op,
+                "n_heads must be a positive multiple of n_kv_heads");
+  if (!q_in || !k_in || !v_in || !cos_t || !sin_t || !slot_block ||
+      !slot_off || !q_out)
+    return fail(RVKV_EINVAL, op,
+                "NULL q/k/v/cos/sin/block_ids/offsets/q_out");
+  const uint32_t hd = pool->head_dim;
+  if (!hd_supported(hd))
+    return fail(RVKV_EUNSUPPORTED, op,
+                "head_dim must be one of 32, 64, 128, 256");
+  PrepArgs a{};
+  a.q_in = q_in;
+  a.k_in = k_in;
+  a.v_in = v_in;
+  a.q_bias = q_bias;
+  a.k_bias = k_bias;
+  a.v_bias = v_bias;
+  a.q_norm = q_norm;
+  a.k_norm = k_norm;
+  a.cos_t = cos_t;
+  a.sin_t = sin_t;
+  a.slot_block = slot_block;
+  a.slot_off = slot_off;
+  a.q_out = q_out;
+  a.kc = pool->tensor(layer, 0);
+  a.vc = pool->tensor(layer, 1);
+  a.rows = rows;
+  a.n_heads = n_heads;
+  a.n_kv = pool->n_kv;
+  a.num_blocks = pool->num_blocks;
+  a.bs = pool->block_size;
+  a.eps = eps;
+  for (const void *p : {(const void *)q_in, (const void *)k_in,
+                        (const void *)v_in, (const void *)q_bias,
+                        (const void *)k_bias, (const void *)v_bias,
+                        (const void *)q_norm, (const void *)k_norm,
+                        (const void *)cos_t, (const void *)sin_t,
+                        (const void *)q_out})
+    if ((uintptr_t)p % 16)
+      return fail(RVKV_EINVAL, op, "float buffers must be 16-byte aligned");
+  const uint64_t items = (uint64_t)rows * (n_heads + 2 * pool->n_kv);
+  if (items > 0xffffffffull)
+    return fail(RVKV_EUNSUPPORTED, op, "too many rows for one launch");
+  const uint32_t per_block = 256 / (hd / 16);
+  const dim3 grid((uint32_t)((items + per_block - 1) / per_block));
+  switch (hd) {
+    case 32: hipLaunchKernelGGL(attn_prep_kernel<32>, grid, dim3(256), 0, pool->stream, a); break;
+    case 64: hipLaunchKernelGGL(attn_prep_kernel<64>, grid, dim3(256), 0, pool->stream, a); break;
+    case 128: hipLaunchKernelGGL(attn_prep_kernel<128>, grid, dim3(256), 0, pool->stream, a); break;
+    default: hipLaunchKernelGGL(attn_prep_kernel<256>, grid, dim3(256), 0, pool->stream, a); break;
+  }
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? RVKV_OK : hip_fail(op, e);
 }
 
 int rvkv_copy_blocks(rvkv_pool *pool, const uint32_t *src, const uint32_t *dst,

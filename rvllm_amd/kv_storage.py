@@ -344,6 +344,38 @@ class HipKvStorage:
             ws.numel() if ws is not None else 0))
         return out
 
+    # -- (f)1: attention prep + append ------------------------------------
+    def attn_prep(self, layer: int, q_in: torch.Tensor, k_in: torch.Tensor,
+                  v_in: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                  slot_block: torch.Tensor, slot_off: torch.Tensor,
+                  q_bias=None, k_bias=None, v_bias=None, q_norm=None,
+                  k_norm=None, eps: float = 1e-6,
+                  q_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """rvkv_attn_prep: bias, per-head RMS norm and RoPE for q and k
+        (src/model.rs:600-626), q returned, k/v appended at their slots."""
+        rows, n_heads, hd = q_in.shape
+        _need(hd == self.head_dim and k_in.shape == (rows, self.n_kv_heads,
+                                                      hd)
+              and v_in.shape == k_in.shape,
+              "attn_prep: q/k/v must be [rows, heads, head_dim]")
+        for t in (q_in, k_in, v_in, cos, sin, q_bias, k_bias, v_bias, q_norm,
+                  k_norm):
+            _need(t is None or (t.dtype == torch.float32 and
+                                t.is_contiguous()),
+                  "attn_prep: float tensors must be contiguous float32")
+        _need(cos.shape == (rows, hd // 2) and sin.shape == cos.shape,
+              "attn_prep: cos/sin must be [rows, head_dim / 2]")
+        _need(slot_block.numel() == rows and slot_off.numel() == rows,
+              "attn_prep: block_ids/offsets length must equal rows")
+        if q_out is None:
+            q_out = torch.empty_like(q_in)
+        check(self._L.rvkv_attn_prep(
+            self._pool, layer, _ptr(q_in), _ptr(k_in), _ptr(v_in), rows,
+            n_heads, _ptr(q_bias), _ptr(k_bias), _ptr(v_bias), _ptr(q_norm),
+            _ptr(k_norm), float(eps), _ptr(cos), _ptr(sin), _ptr(slot_block),
+            _ptr(slot_off), _ptr(q_out)))
+        return q_out
+
     # -- a10: copy-on-write -------------------------------------------------
     def copy_blocks(self, src: torch.Tensor, dst: torch.Tensor) -> None:
         """Copies src[i] -> dst[i] for all layers, K and V."""

@@ -78,6 +78,9 @@ class Config:
     value_scale: float = 1.0
     window: int = 0
     description: str = ""
+    rope_theta: float = 10000.0
+    qkv_bias: bool = False     # Qwen2-style q/k/v projection bias
+    qk_norm: bool = False      # Qwen3/Gemma-3 per-head RMS norm of q and k
 
     @property
     def group(self) -> int:
@@ -91,17 +94,22 @@ class Config:
 CONFIGS = {
     # CPU reference path (f32 cache in the reference).
     "smollm2-360m": Config("smollm2-360m", 0, 1, 15, 5, 64, 16, 8,
-                           description="SmolLM2-360M attention, CPU config"),
+                           description="SmolLM2-360M attention, CPU config",
+                           rope_theta=100000.0),
     # the headline bench workload.
     "llama-3.2-1b": Config("llama-3.2-1b", 1, 16, 32, 8, 64, 16, 64,
-                           description="Llama-3.2-1B shape, 64 x 2048"),
+                           description="Llama-3.2-1B shape, 64 x 2048",
+                           rope_theta=500000.0),
     "qwen3-0.6b": Config("qwen3-0.6b", 2, 28, 16, 8, 128, 16, 256,
                          value_scale=0.5,
-                         description="Qwen3-0.6B shape, 256 x 4096"),
+                         description="Qwen3-0.6B shape, 256 x 4096",
+                         rope_theta=1000000.0, qk_norm=True),
     "qwen2.5-0.5b": Config("qwen2.5-0.5b", 3, 24, 14, 2, 64, 32, 512,
-                           description="Qwen2.5-0.5B shape, ragged + prefix"),
+                           description="Qwen2.5-0.5B shape, ragged + prefix",
+                           rope_theta=1000000.0, qkv_bias=True),
     "gemma-3-270m": Config("gemma-3-270m", 4, 18, 4, 1, 256, 16, 1024,
-                           description="gemma-3-270m shape, 1024 x 1024"),
+                           description="gemma-3-270m shape, 1024 x 1024",
+                           rope_theta=1000000.0, qk_norm=True),
 }
 
 
@@ -277,3 +285,15 @@ def append_bytes(n_tokens: int, cfg: Config, src_bytes: int = 4) -> int:
     per element, written as f16, plus 8 bytes of slot per token."""
     return (n_tokens * cfg.n_kv_heads * cfg.head_dim * 2 * (src_bytes + 2)
             + 8 * n_tokens)
+
+
+def prep_bytes(n_tokens: int, cfg: Config) -> int:
+    """Algorithmic bytes of one attn_prep launch: per token the f32 q row
+    read and written, the f32 k and v rows read and written as f16, the
+    f32 cos/sin halves and 8 bytes of slot; per launch the bias and norm
+    weights."""
+    H, KV, hd = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim
+    per_tok = 8 * H * hd + KV * hd * 2 * (4 + 2) + 4 * hd + 8
+    weights = 4 * ((H + 2 * KV) * hd if cfg.qkv_bias else 0) \
+        + 4 * (2 * hd if cfg.qk_norm else 0)
+    return n_tokens * per_tok + weights

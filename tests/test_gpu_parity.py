@@ -737,3 +737,54 @@ def test_graph_capture_replays_match_eager():
         torch.cuda.synchronize()
         assert torch.equal(out_g1, e1), rep
         assert torch.equal(out_g2, e2), rep
+
+
+# ---- (f)1: attention prep + append -------------------------------------------
+@pytest.mark.parametrize("hd,H,KV", [(64, 32, 8), (128, 16, 8), (256, 4, 1),
+                                     (64, 14, 2), (32, 9, 1)])
+@pytest.mark.parametrize("bias,norm", [(False, False), (True, False),
+                                       (False, True), (True, True)])
+def test_attn_prep_matches_oracle(hd, H, KV, bias, norm):
+    """rvkv_attn_prep vs the oracle's restatement of src/model.rs:600-639.
+    Without the RMS norm every f32 q and every f16 cache bit is identical
+    (same unfused operations); with it the per-head sum of squares is
+    reduced in a different order, so q agrees to 2e-6 * (1 + |q|) and cache
+    values to one f16 ulp."""
+    rng = np.random.default_rng(hd + H + 2 * bias + norm)
+    rows, nb, bs = 37, 40, 16
+    q = rng.standard_normal((rows, H, hd)).astype(np.float32)
+    k = rng.standard_normal((rows, KV, hd)).astype(np.float32)
+    v = rng.standard_normal((rows, KV, hd)).astype(np.float32)
+    opt = {}
+    if bias:
+        opt.update(q_bias=rng.standard_normal(H * hd).astype(np.float32),
+                   k_bias=rng.standard_normal(KV * hd).astype(np.float32),
+                   v_bias=rng.standard_normal(KV * hd).astype(np.float32))
+    if norm:
+        opt.update(q_norm=rng.standard_normal(hd).astype(np.float32),
+                   k_norm=rng.standard_normal(hd).astype(np.float32))
+    pos = rng.integers(0, 8192, rows)
+    factors = (rng.uniform(1, 8, hd // 2).astype(np.float32)
+               if hd == 64 else None)
+    c, s = orc.rope_cos_sin(500000.0, hd, pos, factors=factors)
+    slots = rng.permutation(nb * bs)[:rows]
+    sb, so = slots // bs, slots % bs
+    cache = orc.KvCache(nb, bs, KV, hd, orc.F16)
+    want_q = orc.attn_prep(cache, q, k, v, c, s, sb, so, eps=1e-6, **opt)
+    st = HipKvStorage(1, nb, bs, KV, hd)
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    got_q = st.attn_prep(0, T(q), T(k), T(v), T(c), T(s), dev_u32(sb),
+                         dev_u32(so), eps=1e-6,
+                         **{n: T(a) for n, a in opt.items()}).cpu().numpy()
+    ids = dev_u32(np.arange(nb))
+    gk, gv = bits(st.read_blocks(0, 0, ids)), bits(st.read_blocks(0, 1, ids))
+    assert np.array_equal(gv, cache.v)  # v: bias + RNE only
+    if not norm:
+        assert np.array_equal(got_q, want_q)
+        assert np.array_equal(gk, cache.k)
+    else:
+        # RoPE's x0*c - x1*s cancels, so the bound is absolute, scaled by
+        # the output's magnitude rather than relative to it.
+        assert np.max(np.abs(got_q - want_q) / (1 + np.abs(want_q))) < 2e-6
+        ulp = np.abs(gk.astype(np.int32) - cache.k.astype(np.int32))
+        assert ulp.max() <= 1 and (ulp == 0).mean() > 0.99

@@ -6,6 +6,8 @@ import ctypes
 import os
 import re
 
+import numpy as np
+
 import pytest
 
 from rvllm_amd import _lib
@@ -183,3 +185,22 @@ def test_batch_slots_and_tables_match_single_calls():
         assert lens[i] == bm.num_tokens(s)
     with pytest.raises(RvkvError):
         bm.fill_tables(seqs, 1)  # a table longer than max_blocks
+
+
+def test_rope_table_matches_oracle():
+    """rvllm_amd.rope vs the oracle's powf/cosf/sinf restatement of
+    src/model.rs:224-250: one f32 ulp (6e-8 below 1) everywhere, positions
+    up to 2^17, with and without Llama-3 factors."""
+    from oracle import oracle as orc
+    from rvllm_amd.rope import rope_cos_sin
+    rng = np.random.default_rng(0)
+    pos = np.concatenate([np.arange(64), [4095, 8191, 32767, 131071],
+                          rng.integers(0, 1 << 17, 500)])
+    for hd, theta, fac in [(64, 5e5, None), (128, 1e6, None),
+                           (64, 5e5, np.linspace(1, 8, 32)),
+                           (256, 1e4, None)]:
+        c, s = rope_cos_sin(theta, hd, pos, fac)
+        oc, os_ = orc.rope_cos_sin(theta, hd, pos, factors=fac)
+        assert c.dtype == np.float32 and c.shape == (len(pos), hd // 2)
+        assert np.max(np.abs(c - oc)) <= 6e-8
+        assert np.max(np.abs(s - os_)) <= 6e-8

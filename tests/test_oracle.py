@@ -318,3 +318,76 @@ def test_block_checksums_match_independent_fnv():
     got = c.checksums(0, [5, 0, 3])
     for i, b in enumerate([5, 0, 3]):
         assert int(got[i]) == _fnv1a64(c.k[b].astype("<u2").tobytes())
+
+
+# ---- (f)1: RMS norm / RoPE / attention prep ---------------------------------
+def test_rms_norm_kat():
+    """src/model.rs:758-776: x = [1, 2, 3], w = 1, eps 1e-5."""
+    out = orc.rms_norm([[1.0, 2.0, 3.0]], [1.0, 1.0, 1.0], 1e-5)
+    assert np.max(np.abs(out - [0.46292, 0.92583, 1.38875])) < 1e-4
+
+
+def test_rope_kats():
+    """src/model.rs:778-823: position 0 is the identity; position 1 with
+    theta [1, 0.01] rotates the rotate-half pairs (x0, x2), (x1, x3);
+    Llama-3 factors divide each pair's frequency."""
+    c, s = orc.rope_cos_sin(10000.0, 4, [0, 1])
+    x = np.array([[1, 2, 3, 4], [1, 1, 0, 0]], np.float32)
+    out = orc.rope_apply(x, c, s)
+    assert np.max(np.abs(out[0] - [1, 2, 3, 4])) < 1e-4
+    want = [np.cos(1.0), np.cos(0.01), np.sin(1.0), np.sin(0.01)]
+    assert np.max(np.abs(out[1] - want)) < 1e-4
+    c, s = orc.rope_cos_sin(10000.0, 4, [1], factors=[2.0, 4.0])
+    assert np.max(np.abs(c[0] - np.cos([0.5, 0.0025]))) < 1e-6
+    assert np.max(np.abs(s[0] - np.sin([0.5, 0.0025]))) < 1e-6
+
+
+def test_rope_is_a_relative_position_rotation():
+    """RoPE invariants: every rotate-half pair keeps its length, and
+    <rope(q, m), rope(k, n)> depends only on m - n."""
+    rng = np.random.default_rng(12)
+    hd = 64
+    q = rng.standard_normal((1, hd)).astype(np.float32)
+    k = rng.standard_normal((1, hd)).astype(np.float32)
+    c, s = orc.rope_cos_sin(10000.0, hd, [5, 2, 105, 102])
+    rq = [orc.rope_apply(q, c[i:i + 1], s[i:i + 1]) for i in (0, 2)]
+    rk = [orc.rope_apply(k, c[i:i + 1], s[i:i + 1]) for i in (1, 3)]
+    half = hd // 2
+    for r in rq:
+        assert np.allclose(r[0, :half] ** 2 + r[0, half:] ** 2,
+                           q[0, :half] ** 2 + q[0, half:] ** 2, rtol=1e-5)
+    assert abs(float(rq[0] @ rk[0].T) - float(rq[1] @ rk[1].T)) < 1e-4
+
+
+def test_attn_prep_composes_the_pinned_parts():
+    """orc_attn_prep = bias add, then rms_norm (q, k only), then rope_apply
+    (q, k only), then the f16 write at each row's slot (v: bias only)."""
+    rng = np.random.default_rng(13)
+    rows, H, KV, hd, nb, bs = 5, 6, 2, 16, 8, 4
+    q = rng.standard_normal((rows, H, hd)).astype(np.float32)
+    k = rng.standard_normal((rows, KV, hd)).astype(np.float32)
+    v = rng.standard_normal((rows, KV, hd)).astype(np.float32)
+    qb = rng.standard_normal(H * hd).astype(np.float32)
+    kb = rng.standard_normal(KV * hd).astype(np.float32)
+    vb = rng.standard_normal(KV * hd).astype(np.float32)
+    qn = rng.standard_normal(hd).astype(np.float32)
+    kn = rng.standard_normal(hd).astype(np.float32)
+    c, s = orc.rope_cos_sin(1e4, hd, [3, 9, 0, 40, 7])
+    sb, so = [1, 4, 4, 7, 0], [2, 0, 3, 1, 3]
+    cache = orc.KvCache(nb, bs, KV, hd, orc.F16)
+    qo = orc.attn_prep(cache, q, k, v, c, s, sb, so, qb, kb, vb, qn, kn, 1e-6)
+    for r in range(rows):
+        for h in range(H):
+            x = q[r, h] + qb[h * hd:(h + 1) * hd]
+            x = orc.rope_apply(orc.rms_norm(x[None], qn, 1e-6), c[r:r + 1],
+                               s[r:r + 1])[0]
+            assert np.array_equal(qo[r, h], x)
+        for h in range(KV):
+            x = k[r, h] + kb[h * hd:(h + 1) * hd]
+            x = orc.rope_apply(orc.rms_norm(x[None], kn, 1e-6), c[r:r + 1],
+                               s[r:r + 1])[0]
+            assert np.array_equal(cache.k[sb[r], so[r], h],
+                                  orc.f32_to_f16_bits(x))
+            y = v[r, h] + vb[h * hd:(h + 1) * hd]
+            assert np.array_equal(cache.v[sb[r], so[r], h],
+                                  orc.f32_to_f16_bits(y))
