@@ -788,3 +788,60 @@ def test_attn_prep_matches_oracle(hd, H, KV, bias, norm):
         assert np.max(np.abs(got_q - want_q) / (1 + np.abs(want_q))) < 2e-6
         ulp = np.abs(gk.astype(np.int32) - cache.k.astype(np.int32))
         assert ulp.max() <= 1 and (ulp == 0).mean() > 0.99
+
+
+def _prep_then_decode(st, q, k, v, c, s, sb, so, tables, lens, opt):
+    """attn_prep over every prompt token, then one decode over the cache
+    with each sequence's last q row (the prefill -> decode hand-off)."""
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    qo = st.attn_prep(0, T(q), T(k), T(v), T(c), T(s), dev_u32(sb),
+                      dev_u32(so), eps=1e-6,
+                      **{n: T(a) for n, a in opt.items()})
+    last = torch.from_numpy(np.cumsum(lens.astype(np.int64)) - 1).cuda()
+    out = st.paged_decode(0, qo[last].contiguous(), dev_u32(tables),
+                          dev_u32(lens), int(lens.max()))
+    return qo.cpu().numpy(), out.cpu().numpy()
+
+
+@pytest.mark.parametrize("hd,H,KV", [(128, 16, 8), (64, 14, 2)])
+def test_attn_prep_then_decode_end_to_end(hd, H, KV):
+    """Prompt rows through rvkv_attn_prep, then rvkv_paged_decode, against
+    the oracle's attn_prep + float64 paged decode (2e-3 max-abs), and the
+    reference's qk_norm_cancels_the_scale_of_the_qk_projections
+    (src/model.rs:1132-1162): with QK norm, scaling the q and k rows by 7
+    leaves the attention output unchanged (1e-4 in the reference; here
+    the f16 cache may round the renormalised k differently, so 2e-3)."""
+    rng = np.random.default_rng(hd + H)
+    bs, lens = 16, np.array([1, 17, 64, 200, 33], np.uint32)
+    nseq, rows = len(lens), int(lens.sum())
+    max_blocks = -(-int(lens.max()) // bs)
+    nb = nseq * max_blocks + 3
+    perm = rng.permutation(nb).astype(np.uint32)
+    tables = perm[:nseq * max_blocks].reshape(nseq, max_blocks)
+    pos = np.concatenate([np.arange(n) for n in lens])
+    seq = np.repeat(np.arange(nseq), lens)
+    sb, so = tables[seq, pos // bs], (pos % bs).astype(np.uint32)
+    from rvllm_amd.rope import rope_cos_sin
+    c, s = rope_cos_sin(1e6, hd, pos)
+    q = rng.standard_normal((rows, H, hd)).astype(np.float32)
+    k = rng.standard_normal((rows, KV, hd)).astype(np.float32)
+    v = rng.standard_normal((rows, KV, hd)).astype(np.float32)
+    opt = dict(q_norm=rng.uniform(0.5, 2, hd).astype(np.float32),
+               k_norm=rng.uniform(0.5, 2, hd).astype(np.float32))
+    st = HipKvStorage(1, nb, bs, KV, hd)
+    qo, out = _prep_then_decode(st, q, k, v, c, s, sb, so, tables, lens, opt)
+    cache = orc.KvCache(nb, bs, KV, hd, orc.F16)
+    want_q = orc.attn_prep(cache, q, k, v, c, s, sb, so, eps=1e-6, **opt)
+    want = orc.paged_decode_f64(cache, want_q[np.cumsum(lens) - 1], tables,
+                                max_blocks, lens)
+    assert np.max(np.abs(out - want)) < 2e-3
+    st2 = HipKvStorage(1, nb, bs, KV, hd)
+    _, out7 = _prep_then_decode(st2, q * 7, k * 7, v, c, s, sb, so, tables,
+                                lens, opt)
+    assert np.max(np.abs(out7 - out)) < 2e-3
+    # Without the norms the same scaling sharpens attention.
+    st3 = HipKvStorage(1, nb, bs, KV, hd)
+    _, a = _prep_then_decode(st3, q, k, v, c, s, sb, so, tables, lens, {})
+    _, b = _prep_then_decode(st3, q * 7, k * 7, v, c, s, sb, so, tables,
+                             lens, {})
+    assert np.max(np.abs(a - b)) > 1e-2
