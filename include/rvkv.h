@@ -223,6 +223,27 @@ int rvkv_attn_prep(rvkv_pool *pool, uint32_t layer, const float *q_in,
                    const float *sin_t, const uint32_t *slot_block,
                    const uint32_t *slot_off, float *q_out);
 
+/* ---- next row (f)2: paged prefill / chunked-prefill attention ------------
+ * Attention for q_len >= 1 query rows per sequence straight over the paged
+ * cache: what rvllm's prefill computes with kv_gather + batch_mask +
+ * gqa_attention (src/model.rs:346-415 called at :628-644; CUDA:
+ * src/cuda/model.rs:528-569; the Metal attn_decode with q_len > 1,
+ * src/metal/ops.rs:680-685). Row i of sequence b is at position
+ * pos_offset[b] + i and sees key j iff j < read_num_tokens[b], j <= its
+ * position and, with window > 0, j + window > its position. q and out are
+ * token-major [batch * q_len, n_heads, head_dim] f32, 16-byte aligned;
+ * block_tables [batch, max_blocks] u32; pos_offset, read_num_tokens [batch]
+ * u32 (all device). Table entries >= num_blocks mark keys unreadable (they
+ * get probability 0); a row that sees no key gets zeros. head_dim in {32,
+ * 64, 128}; block_size a power of two >= 8. Computed on the matrix cores in
+ * f16 with f32 accumulation. Allocates nothing. */
+int rvkv_paged_prefill(rvkv_pool *pool, uint32_t layer, const float *q,
+                       const uint32_t *block_tables,
+                       const uint32_t *pos_offset,
+                       const uint32_t *read_num_tokens, uint32_t batch,
+                       uint32_t q_len, uint32_t max_blocks, uint32_t n_heads,
+                       float scale, int32_t window, float *out);
+
 /* ---- a10: prefix-cache copy-on-write -------------------------------------
  * No counterpart in the reference (rvllm never mutates a shared block; its
  * only copy is the whole-cache KvStorage::clone, src/kv_storage.rs:15-33).

@@ -74,6 +74,9 @@ def lib() -> ctypes.CDLL:
                                         u32, P]
         L.orc_paged_decode_f64.argtypes = [P, P, ctypes.c_int, u32, u32, u32,
                                            P, P, u32, P, u32, u32, f64, i32, P]
+        L.orc_paged_prefill_f64.argtypes = [P, P, ctypes.c_int, u32, u32,
+                                            u32, P, P, u32, P, P, u32, u32,
+                                            u32, f64, i32, P]
         L.orc_copy_blocks.argtypes = [P, ctypes.c_int, u32, u32, u32, P, P,
                                       u32]
         L.orc_block_checksums.argtypes = [P, u32, u32, u32, P, u32, P]
@@ -250,6 +253,27 @@ def paged_decode_f64(cache: KvCache, q, tables, max_blocks, ctx_lens,
                                _p(tables), max_blocks, _p(ctx_lens), batch,
                                n_heads, float(scale), int(window or 0),
                                _p(out))
+    return out
+
+
+def paged_prefill_f64(cache: KvCache, q, tables, max_blocks, pos_offset,
+                      read_num, scale=None, window=0):
+    """Float64 paged attention for q_len >= 1 rows per sequence with
+    batch_mask's causal/window rule (src/model.rs:346-369; the Metal test
+    reference src/metal/ops.rs:719-745). q [batch, q_len, n_heads, hd]
+    token-major f32 -> out of the same shape."""
+    q = _f32(q)
+    batch, q_len, n_heads, hd = q.shape
+    tables, pos_offset, read_num = _u32(tables), _u32(pos_offset), \
+        _u32(read_num)
+    if scale is None:
+        scale = 1.0 / np.sqrt(hd)
+    out = np.empty_like(q)
+    lib().orc_paged_prefill_f64(_p(cache.k), _p(cache.v), cache.dtype,
+                                cache.bs, cache.n_kv, cache.hd, _p(q),
+                                _p(tables), max_blocks, _p(pos_offset),
+                                _p(read_num), batch, q_len, n_heads,
+                                float(scale), int(window or 0), _p(out))
     return out
 
 

@@ -329,6 +329,69 @@ void orc_paged_decode_f64(const void *cache_k, const void *cache_v, int dtype,
   free(acc);
 }
 
+/* ---- next row (f)2: paged prefill / chunked attention, q_len >= 1 ---------
+ * Float64 attention straight over the paged cache for q_len query rows per
+ * sequence, with batch_mask's rule (src/model.rs:346-369): row i of
+ * sequence b sits at position p = pos_offset[b] + i and sees key j iff
+ * j < read_num[b], j <= p and, with a window w > 0, j + w > p. This is
+ * src/metal/ops.rs:719-745 (the Metal attn_decode test reference, which
+ * takes q_len > 1 with that causal mask) with the mask written as
+ * batch_mask's. q and out are token-major: [batch * q_len, n_heads, hd].
+ * A row that sees no key gets zeros (as a decode with ctx_len 0). */
+void orc_paged_prefill_f64(const void *cache_k, const void *cache_v,
+                           int dtype, uint32_t bs, uint32_t n_kv, uint32_t hd,
+                           const float *q, const uint32_t *tables,
+                           uint32_t max_blocks, const uint32_t *pos_offset,
+                           const uint32_t *read_num, uint32_t batch,
+                           uint32_t q_len, uint32_t n_heads, double scale,
+                           int32_t window, float *out) {
+  uint32_t group = n_heads / n_kv;
+  uint32_t cap = max_blocks * bs;
+  double *sc = (double *)malloc((size_t)(cap ? cap : 1) * 8);
+  double *acc = (double *)malloc((size_t)hd * 8);
+  for (uint32_t b = 0; b < batch; ++b)
+    for (uint32_t i = 0; i < q_len; ++i) {
+      uint64_t p = (uint64_t)pos_offset[b] + i;
+      uint64_t hi = read_num[b] < p + 1 ? read_num[b] : p + 1;
+      if (hi > cap) hi = cap;
+      uint64_t lo = (window > 0 && p + 1 > (uint64_t)window)
+                        ? p + 1 - (uint64_t)window : 0;
+      size_t row = (size_t)b * q_len + i;
+      for (uint32_t h = 0; h < n_heads; ++h) {
+        uint32_t kvh = h / group;
+        const float *qh = q + (row * n_heads + h) * hd;
+        float *oh = out + (row * n_heads + h) * hd;
+        if (lo >= hi) {
+          memset(oh, 0, (size_t)hd * 4);
+          continue;
+        }
+        double mx = -INFINITY;
+        for (uint64_t j = lo; j < hi; ++j) {
+          size_t blk = tables[(size_t)b * max_blocks + j / bs];
+          size_t at = ((blk * bs + j % bs) * n_kv + kvh) * hd;
+          double dot = 0.0;
+          for (uint32_t d = 0; d < hd; ++d)
+            dot += (double)qh[d] * (double)cell_get(cache_k, dtype, at + d);
+          sc[j] = dot * scale;
+          if (sc[j] > mx) mx = sc[j];
+        }
+        double total = 0.0;
+        for (uint32_t d = 0; d < hd; ++d) acc[d] = 0.0;
+        for (uint64_t j = lo; j < hi; ++j) {
+          size_t blk = tables[(size_t)b * max_blocks + j / bs];
+          size_t at = ((blk * bs + j % bs) * n_kv + kvh) * hd;
+          double e = exp(sc[j] - mx);
+          total += e;
+          for (uint32_t d = 0; d < hd; ++d)
+            acc[d] += e * (double)cell_get(cache_v, dtype, at + d);
+        }
+        for (uint32_t d = 0; d < hd; ++d) oh[d] = (float)(acc[d] / total);
+      }
+    }
+  free(sc);
+  free(acc);
+}
+
 /* ---- a10: copy-on-write block copy (new behaviour; invariants only) -------
  * dst block := src block, every cell, for one layer's K or V tensor. */
 void orc_copy_blocks(void *cache, int dtype, uint32_t bs, uint32_t n_kv,

@@ -44,6 +44,8 @@ SIGNATURES = {
     "rvkv_decode_step": (_int, [_P, _P, _u32, _P, _P, _int, _P, _P, _P, _P,
                                 _P, _u32, _u32, _u32, _u32, _f32, _i32, _P,
                                 _P, _sz]),
+    "rvkv_paged_prefill": (_int, [_P, _u32, _P, _P, _P, _P, _u32, _u32, _u32,
+                                  _u32, _f32, _i32, _P]),
     "rvkv_attn_prep": (_int, [_P, _u32, _P, _P, _P, _u32, _u32, _P, _P, _P,
                               _P, _P, _f32, _P, _P, _P, _P, _P]),
     "rvkv_copy_blocks": (_int, [_P, _P, _P, _u32]),

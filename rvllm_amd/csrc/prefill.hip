@@ -1,0 +1,368 @@
+// prefill.hip - paged prefill / chunked-prefill attention (q_len >= 1 query
+// rows per sequence, causal, optional sliding window) straight over the
+// paged f16 cache, on the gfx950 matrix cores.
+//
+// What it computes is rvllm's prefill attention: gather the sequence's keys
+// through its block table, add batch_mask and run gqa_attention
+// (src/model.rs:346-415, called at src/model.rs:628-644; the CUDA backend's
+// kv_gather + cuBLAS scores + mask + softmax + apply, src/cuda/model.rs:
+// 528-569). Row i of sequence b sits at position p = pos_offset[b] + i and
+// sees key j iff j < read_num_tokens[b], j <= p and (window > 0) j + window
+// > p. A row that sees no key gets zeros.
+//
+// Work split: one workgroup = (sequence, KV head, tile of 128 query rows),
+// four wave64s of 32 rows each. The rows of a KV head are the GQA group
+// folded into the query axis, row r = (query qi = r / G, head g = r % G), so
+// every key/value tile read from HBM serves G heads * 128/G positions.
+// Keys stream in tiles of 64 through LDS; the next tile's global loads are
+// in flight while the current one is computed.
+//
+// Matrix layout (v_mfma_f32_32x32x16_f16, f32 accumulate):
+//   S^T = K . Q^T   (M = 32 keys, N = 32 query rows, K = 16 of head_dim)
+//   O^T = V^T . P^T (M = 32 of head_dim, N = 32 query rows, K = 16 keys)
+// With S transposed every lane holds ONE query row (lane % 32) and 16 keys
+// of each 32-key sub-tile, so the online-softmax max/sum is in-lane plus one
+// exchange with lane ^ 32, and the probabilities feed the P.V product from
+// registers. The K rows are fed to the S product in a permuted order
+// sigma(m) chosen so that accumulator register j of lane-half h holds key
+// 16*(j/8) + 8*h + j%8: that is exactly the k-slot order the P^T operand
+// needs (8 consecutive keys per lane-half), so no lane shuffles are needed.
+// V is the one operand read across its rows (8 keys of one d column); it is
+// staged transposed in LDS, Vt[d][key], so that read is one 16-byte load.
+//
+// q is pre-scaled by scale*log2(e) and rounded to f16; probabilities are
+// rounded to f16 and the row sum adds the rounded values, so numerator and
+// denominator see the same weights. Products are exact in f32; sums are f32.
+#include "pool.h"
+
+#include <cmath>
+
+using rvkv_detail::fail;
+using rvkv_detail::hip_fail;
+
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kBN = 64;   // keys per tile
+constexpr int kWaveRows = 32;
+constexpr int kWaves = 4;
+constexpr int kBM = kWaveRows * kWaves;  // query rows per workgroup
+constexpr float kNegBig = -1.0e30f;      // finite start value of the row max
+
+struct PrefillArgs {
+  const float *q;  // [batch * q_len, n_heads, hd]
+  float *out;      // same shape
+  const uint16_t *kc, *vc;
+  const uint32_t *tables;  // [batch, max_blocks]
+  const uint32_t *pos_offset, *read_num;
+  uint64_t block_stride;  // elements per block (all heads)
+  uint32_t head_stride;   // elements per (block, head) tile
+  uint32_t q_len, max_blocks, num_blocks, n_heads, group, bs_log2;
+  uint32_t rows;     // group * q_len rows per (sequence, KV head)
+  uint32_t n_tiles;  // ceil(rows / kBM)
+  float qscale;      // scale * log2(e)
+  int32_t window;
+};
+
+template <int HD>
+struct Lds {
+  static constexpr int KS = HD + 8;   // K row stride in halves (16 B pad)
+  static constexpr int VS = kBN + 8;  // Vt row stride in halves
+  static constexpr size_t k_bytes = (size_t)kBN * KS * 2;
+  static constexpr size_t v_bytes = (size_t)HD * VS * 2;
+  static constexpr size_t bytes = k_bytes + v_bytes + kBN;  // + key flags
+};
+
+__device__ __forceinline__ uint32_t lo_bound(uint32_t p, int32_t window) {
+  return (window > 0 && p + 1 > (uint32_t)window) ? p + 1 - (uint32_t)window
+                                                  : 0u;
+}
+
+template <int HD>
+__global__ void __launch_bounds__(256) prefill_kernel(PrefillArgs a) {
+  constexpr int KS = Lds<HD>::KS, VS = Lds<HD>::VS;
+  constexpr int KC = HD / 16;                 // MFMA k-steps of S
+  constexpr int DT = HD / 32;                 // 32-row tiles of O^T
+  constexpr int CPR = HD / 8;                 // 16-byte chunks per key row
+  constexpr int CH = kBN * CPR / 256;         // chunks per thread per tile
+  static_assert(CH >= 1 && kBN * CPR % 256 == 0, "tile/thread mismatch");
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint16_t *ks = reinterpret_cast<uint16_t *>(smem);
+  uint16_t *vt = reinterpret_cast<uint16_t *>(smem + Lds<HD>::k_bytes);
+  uint8_t *kok = smem + Lds<HD>::k_bytes + Lds<HD>::v_bytes;
+
+  const uint32_t b = blockIdx.z, kvh = blockIdx.y;
+  const uint32_t tile = a.n_tiles - 1 - blockIdx.x;  // long rows first
+  const int tid = threadIdx.x;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63, hl = lane >> 5, ln = lane & 31;
+  const uint32_t bs_mask = (1u << a.bs_log2) - 1u;
+
+  const uint32_t off = a.pos_offset[b];
+  const uint32_t cap = a.max_blocks << a.bs_log2;
+  const uint32_t ctx = min(a.read_num[b], cap);
+  const uint32_t *table = a.tables + (size_t)b * a.max_blocks;
+
+  // Key range any row of the workgroup sees, in whole tiles.
+  const uint32_t r_first = tile * kBM;
+  const uint32_t r_last = min(r_first + kBM, a.rows) - 1u;
+  const uint32_t k_end = min(ctx, off + r_last / a.group + 1u);
+  const uint32_t k_begin =
+      lo_bound(off + r_first / a.group, a.window) & ~(uint32_t)(kBN - 1);
+
+  // The same for this wave's 32 rows (wave-uniform).
+  const uint32_t rw0 = r_first + wave * kWaveRows;
+  const bool wave_live = rw0 < a.rows;
+  const uint32_t rw1 = min(rw0 + kWaveRows, a.rows) - 1u;
+  const uint32_t w_end = wave_live ? min(ctx, off + rw1 / a.group + 1u) : 0u;
+  const uint32_t w_begin = lo_bound(off + rw0 / a.group, a.window);
+
+  // This lane's query row.
+  const uint32_t r = rw0 + ln;
+  const bool row_ok = r < a.rows;
+  const uint32_t qi = row_ok ? r / a.group : 0u;
+  const uint32_t head = kvh * a.group + (row_ok ? r - qi * a.group : 0u);
+  const uint32_t p = off + qi;
+  const uint32_t row_hi = row_ok ? min(ctx, p + 1u) : 0u;
+  const uint32_t row_lo = lo_bound(p, a.window);
+  const size_t qrow = ((size_t)b * a.q_len + qi) * a.n_heads + head;
+
+  half8 qf[KC];
+  {
+    const float *qp = a.q + qrow * HD;
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) {
+      const int d0 = kc * 16 + hl * 8;
+      float4 x = make_float4(0.f, 0.f, 0.f, 0.f), y = x;
+      if (row_ok) {
+        x = *reinterpret_cast<const float4 *>(qp + d0);
+        y = *reinterpret_cast<const float4 *>(qp + d0 + 4);
+      }
+      qf[kc] = half8{(_Float16)(x.x * a.qscale), (_Float16)(x.y * a.qscale),
+                     (_Float16)(x.z * a.qscale), (_Float16)(x.w * a.qscale),
+                     (_Float16)(y.x * a.qscale), (_Float16)(y.y * a.qscale),
+                     (_Float16)(y.z * a.qscale), (_Float16)(y.w * a.qscale)};
+    }
+  }
+
+  f32x16 o[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) o[t][j] = 0.f;
+  float m = kNegBig, l = 0.f;
+
+  // K row this lane feeds to the S product: sigma(ln), see the header.
+  const int sig = 16 * (ln >> 4) + 8 * ((ln >> 2) & 1) + 4 * ((ln >> 3) & 1) +
+                  (ln & 3);
+
+  const char *kbase = reinterpret_cast<const char *>(a.kc) +
+                      (size_t)kvh * a.head_stride * 2;
+  const char *vbase = reinterpret_cast<const char *>(a.vc) +
+                      (size_t)kvh * a.head_stride * 2;
+  uint4 kr[CH], vr[CH];
+  uint32_t okbits = 0;
+
+  auto load = [&](uint32_t kt) {
+    okbits = 0;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int c = tid + 256 * i;
+      const uint32_t tok = kt + (uint32_t)(c / CPR);
+      const int dc = c % CPR;
+      const uint32_t bi = min(tok >> a.bs_log2, a.max_blocks - 1u);
+      const uint32_t blk = table[bi];
+      const bool ok = tok < k_end && blk < a.num_blocks;
+      okbits |= (uint32_t)ok << i;
+      const uint64_t at = ((uint64_t)(ok ? blk : 0u) * a.block_stride +
+                           (uint64_t)(tok & bs_mask) * HD + dc * 8) * 2;
+      kr[i] = ok ? *reinterpret_cast<const uint4 *>(kbase + at)
+                 : make_uint4(0, 0, 0, 0);
+      vr[i] = ok ? *reinterpret_cast<const uint4 *>(vbase + at)
+                 : make_uint4(0, 0, 0, 0);
+    }
+  };
+
+  if (k_begin < k_end) load(k_begin);
+  for (uint32_t kt = k_begin; kt < k_end; kt += kBN) {
+    __syncthreads();  // the previous tile is no longer read
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int c = tid + 256 * i;
+      const int key = c / CPR, dc = c % CPR;
+      *reinterpret_cast<uint4 *>(ks + key * KS + dc * 8) = kr[i];
+      const uint32_t w[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        vt[(dc * 8 + 2 * e) * VS + key] = (uint16_t)(w[e] & 0xffffu);
+        vt[(dc * 8 + 2 * e + 1) * VS + key] = (uint16_t)(w[e] >> 16);
+      }
+      if (dc == 0) kok[key] = (uint8_t)((okbits >> i) & 1u);
+    }
+    __syncthreads();
+    if (kt + kBN < k_end) load(kt + kBN);
+    if (!(kt < w_end && kt + kBN > w_begin)) continue;  // nothing for this wave
+
+    f32x16 s[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) s[t][j] = 0.f;
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) {
+        const half8 kf = *reinterpret_cast<const half8 *>(
+            ks + (32 * t + sig) * KS + kc * 16 + hl * 8);
+        s[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[kc], s[t], 0, 0,
+                                                      0);
+      }
+    }
+
+    // Mask, online softmax; register j of sub-tile t is key
+    // kt + 32t + 16(j/8) + 8hl + j%8.
+    float mx = kNegBig;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int g8 = 0; g8 < 2; ++g8) {
+        const uint32_t k0 = 32 * t + 16 * g8 + 8 * hl;
+        const uint64_t okw = *reinterpret_cast<const uint64_t *>(kok + k0);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t key = kt + k0 + e;
+          const bool valid = ((okw >> (8 * e)) & 1u) && key >= row_lo &&
+                             key < row_hi;
+          const float x = valid ? s[t][8 * g8 + e] : -__builtin_inff();
+          s[t][8 * g8 + e] = x;
+          mx = fmaxf(mx, x);
+        }
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m, mx);
+    const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+    m = m_new;
+    half8 pb[2][2];
+    float psum = 0.f;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const _Float16 ph =
+              (_Float16)__builtin_amdgcn_exp2f(s[t][8 * c + e] - m_new);
+          pb[t][c][e] = ph;
+          psum += (float)ph;
+        }
+    l = l * alpha + psum;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) o[dt][j] *= alpha;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const half8 vf = *reinterpret_cast<const half8 *>(
+              vt + (dt * 32 + ln) * VS + 32 * t + 16 * c + 8 * hl);
+          o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pb[t][c], o[dt],
+                                                         0, 0, 0);
+        }
+  }
+
+  const float lt = l + __shfl_xor(l, 32);
+  const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+  if (row_ok) {
+    float *op = a.out + qrow * HD;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4)
+        *reinterpret_cast<float4 *>(op + dt * 32 + 8 * q4 + 4 * hl) =
+            make_float4(o[dt][4 * q4] * inv, o[dt][4 * q4 + 1] * inv,
+                        o[dt][4 * q4 + 2] * inv, o[dt][4 * q4 + 3] * inv);
+  }
+}
+
+template <int HD>
+void launch_prefill(const PrefillArgs &a, dim3 grid, hipStream_t st) {
+  hipLaunchKernelGGL(prefill_kernel<HD>, grid, dim3(256), Lds<HD>::bytes, st,
+                     a);
+}
+
+}  // namespace
+
+extern "C" {
+
+int rvkv_paged_prefill(rvkv_pool *pool, uint32_t layer, const float *q,
+                       const uint32_t *block_tables,
+                       const uint32_t *pos_offset,
+                       const uint32_t *read_num_tokens, uint32_t batch,
+                       uint32_t q_len, uint32_t max_blocks, uint32_t n_heads,
+                       float scale, int32_t window, float *out) {
+  const char *op = "paged_prefill";
+  if (!pool) return fail(RVKV_EINVAL, op, "pool is NULL");
+  if (layer >= pool->n_layers)
+    return fail(RVKV_EINVAL, op, "layer out of range");
+  if (batch == 0 || q_len == 0) return RVKV_OK;
+  if (!q || !block_tables || !pos_offset || !read_num_tokens || !out)
+    return fail(RVKV_EINVAL, op,
+                "NULL q/block_tables/pos_offset/read_num_tokens/out");
+  if (max_blocks == 0) return fail(RVKV_EINVAL, op, "max_blocks is 0");
+  if (n_heads == 0 || n_heads % pool->n_kv != 0)
+    return fail(RVKV_EINVAL, op,
+                "n_heads must be a positive multiple of n_kv_heads");
+  const uint32_t hd = pool->head_dim, bs = pool->block_size;
+  if (hd != 32 && hd != 64 && hd != 128)
+    return fail(RVKV_EUNSUPPORTED, op, "head_dim must be 32, 64 or 128");
+  if (bs < 8 || (bs & (bs - 1)) != 0)
+    return fail(RVKV_EUNSUPPORTED, op,
+                "block_size must be a power of two >= 8");
+  if (batch > 65535 || pool->n_kv > 65535)
+    return fail(RVKV_EUNSUPPORTED, op, "batch and n_kv_heads must be <= 65535");
+  if ((uintptr_t)q % 16 || (uintptr_t)out % 16)
+    return fail(RVKV_EINVAL, op, "q and out must be 16-byte aligned");
+  if ((uint64_t)max_blocks * bs > 0x80000000ull)
+    return fail(RVKV_EUNSUPPORTED, op, "max_blocks * block_size too large");
+  const uint64_t rows = (uint64_t)(n_heads / pool->n_kv) * q_len;
+  if (rows > 0x7fffffffull)
+    return fail(RVKV_EUNSUPPORTED, op, "q_len too large for one launch");
+  if (!(scale > 0.f) || !std::isfinite(scale))
+    return fail(RVKV_EINVAL, op, "scale must be positive and finite");
+
+  PrefillArgs a{};
+  a.q = q;
+  a.out = out;
+  a.kc = pool->tensor(layer, 0);
+  a.vc = pool->tensor(layer, 1);
+  a.tables = block_tables;
+  a.pos_offset = pos_offset;
+  a.read_num = read_num_tokens;
+  a.block_stride = pool->block_elems;
+  a.head_stride = bs * hd;
+  a.q_len = q_len;
+  a.max_blocks = max_blocks;
+  a.num_blocks = pool->num_blocks;
+  a.n_heads = n_heads;
+  a.group = n_heads / pool->n_kv;
+  uint32_t lg = 0;
+  while ((1u << lg) < bs) ++lg;
+  a.bs_log2 = lg;
+  a.rows = (uint32_t)rows;
+  a.n_tiles = (uint32_t)((rows + kBM - 1) / kBM);
+  a.qscale = scale * 1.4426950408889634f;
+  a.window = window;
+  const dim3 grid(a.n_tiles, pool->n_kv, batch);
+  switch (hd) {
+    case 32: launch_prefill<32>(a, grid, pool->stream); break;
+    case 64: launch_prefill<64>(a, grid, pool->stream); break;
+    default: launch_prefill<128>(a, grid, pool->stream); break;
+  }
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? RVKV_OK : hip_fail(op, e);
+}
+
+}  // extern "C"

@@ -19,12 +19,13 @@
 #include <string>
 #include <vector>
 
-#include "../../include/rvkv.h"
+#include "pool.h"
 
 namespace {
-
 thread_local std::string g_last_error;
+}  // namespace
 
+namespace rvkv_detail {
 int fail(int code, const char *op, const char *reason) {
   g_last_error = std::string(op) + ": " + reason;
   return code;
@@ -34,6 +35,12 @@ int hip_fail(const char *op, hipError_t e) {
   g_last_error = std::string(op) + ": " + hipGetErrorString(e);
   return RVKV_EHIP;
 }
+}  // namespace rvkv_detail
+
+using rvkv_detail::fail;
+using rvkv_detail::hip_fail;
+
+namespace {
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
@@ -46,18 +53,6 @@ __device__ __forceinline__ uint32_t as_u32(h2 x) {
 
 }  // namespace
 
-struct rvkv_pool {
-  uint32_t n_layers, num_blocks, block_size, n_kv, head_dim;
-  hipStream_t stream;
-  int device;
-  uint16_t *base;        // 2 * n_layers tensors
-  size_t tensor_elems;   // num_blocks * n_kv * block_size * head_dim
-  size_t block_elems;    // n_kv * block_size * head_dim
-
-  uint16_t *tensor(uint32_t layer, uint32_t which) const {
-    return base + ((size_t)layer * 2 + which) * tensor_elems;
-  }
-};
 
 // ---------------------------------------------------------------------------
 // a2: KV append. One thread per VW contiguous elements of one (token, head)

@@ -267,6 +267,40 @@ class HipKvStorage:
             ws.numel() if ws is not None else 0))
         return out
 
+    def paged_prefill(self, layer: int, q: torch.Tensor,
+                      block_tables: torch.Tensor, pos_offset: torch.Tensor,
+                      read_num_tokens: torch.Tensor,
+                      out: Optional[torch.Tensor] = None,
+                      scale: Optional[float] = None,
+                      window: int = 0) -> torch.Tensor:
+        """Prefill / chunked-prefill attention (q_len >= 1 rows per
+        sequence, batch_mask's causal and window rule) straight over the
+        paged cache: the replacement of kv_gather + batch_mask +
+        gqa_attention (src/model.rs:346-415, 628-644). q: [batch, q_len,
+        n_heads, hd] f32 token-major; block_tables [batch, max_blocks],
+        pos_offset and read_num_tokens [batch] u32."""
+        _need(q.dim() == 4 and q.shape[3] == self.head_dim,
+              "paged_prefill: q must be [batch, q_len, n_heads, head_dim]")
+        _need(q.dtype == torch.float32 and q.is_contiguous(),
+              "paged_prefill: q must be contiguous float32")
+        batch, q_len, n_heads, hd = q.shape
+        _need(block_tables.dim() == 2 and block_tables.shape[0] == batch,
+              "paged_prefill: block_tables must be [batch, max_blocks]")
+        _need(pos_offset.numel() == batch and read_num_tokens.numel() == batch,
+              "paged_prefill: pos_offset/read_num_tokens length must equal "
+              "batch")
+        if out is None:
+            out = torch.empty_like(q)
+        _need(out.shape == q.shape and out.dtype == torch.float32 and
+              out.is_contiguous(), "paged_prefill: out must match q")
+        if scale is None:
+            scale = 1.0 / math.sqrt(hd)
+        check(self._L.rvkv_paged_prefill(
+            self._pool, layer, _ptr(q), _ptr(block_tables), _ptr(pos_offset),
+            _ptr(read_num_tokens), batch, q_len, block_tables.shape[1],
+            n_heads, float(scale), int(window or 0), _ptr(out)))
+        return out
+
     def paged_decode_planned(self, layer: int, plan: HipDecodePlan,
                              q: torch.Tensor, block_tables: torch.Tensor,
                              ctx_lens: torch.Tensor,

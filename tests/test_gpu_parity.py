@@ -845,3 +845,144 @@ def test_attn_prep_then_decode_end_to_end(hd, H, KV):
     _, b = _prep_then_decode(st3, q * 7, k * 7, v, c, s, sb, so, tables,
                              lens, {})
     assert np.max(np.abs(a - b)) > 1e-2
+
+
+# ---- (f)2: paged prefill / chunked-prefill attention -------------------------
+@pytest.mark.parametrize("case", [0, 1, 2, 4])
+def test_prefill_metal_cases(golden, case):
+    """The attn_decode cases of src/metal/ops.rs:676-766 with their own
+    q_len (1, 1, 2, 3) through rvkv_paged_prefill: the Metal mask is
+    batch_mask with pos_offset = valid - q_len, read_num = valid. Against
+    the oracle over the same f16 cache and against the f32-cache golden."""
+    c = metal_case_inputs(case)
+    B, Q, H, D, bs = c["batch"], c["q_len"], c["n_heads"], c["hd"], c["bs"]
+    st = HipKvStorage(1, c["num_blocks"], bs, c["n_kv"], D)
+    nslot = c["num_blocks"] * bs
+    slots = np.arange(nslot)
+    kk = c["cache_k"].reshape(nslot, c["n_kv"], D)
+    vv = c["cache_v"].reshape(nslot, c["n_kv"], D)
+    st.write_tokens(0, dev_u32(slots // bs), dev_u32(slots % bs),
+                    torch.from_numpy(kk).cuda(), torch.from_numpy(vv).cuda())
+    valid = np.array([c["ctx"] - 2 * b for b in range(B)], np.uint32)
+    q = c["q"].reshape(B, Q, H, D)
+    tables = c["block_idx"].reshape(B, c["max_blocks"])
+    out = st.paged_prefill(0, torch.from_numpy(q).cuda(), dev_u32(tables),
+                           dev_u32(valid - Q), dev_u32(valid)).cpu().numpy()
+    ref = orc.KvCache(c["num_blocks"], bs, c["n_kv"], D, orc.F16)
+    ref.write_tokens(slots // bs, slots % bs, kk, vv)
+    want = orc.paged_prefill_f64(ref, q, c["block_idx"], c["max_blocks"],
+                                 valid - Q, valid)
+    assert np.abs(out - want).max() < ATOL
+    exp = np.array(golden["metal_attn_decode"][case]["expected"],
+                   np.float32).reshape(B, Q, H, D)
+    assert np.abs(out - exp).max() < ATOL
+
+
+def _prefill_case(seed, B, Q, nkv, G, hd, bs, window, ragged=True,
+                  prior=None):
+    """A chunked-prefill batch over a random pool: sequence b already holds
+    prior[b] tokens and appends a chunk of Q (pos_offset = prior[b]);
+    read_num is prior + Q, or a little less/more when ragged (padding past
+    read_num, rows that see fewer keys). Returns the GPU result and the
+    oracle's."""
+    rng = np.random.default_rng(seed)
+    if prior is None:
+        prior = rng.integers(0, 3 * Q + 1, B)
+    prior = np.asarray(prior, np.int64)
+    read = prior + Q
+    if ragged:
+        read = np.maximum(read + rng.integers(-3, 2, B), 0)
+    mb = max(1, -(-int(max(read.max(), (prior + Q).max())) // bs))
+    nb = B * mb + 5
+    st = HipKvStorage(1, nb, bs, nkv, hd)
+    fill_layer(st, 0, seed=seed)
+    perm = rng.permutation(nb).astype(np.uint32)
+    tables = perm[:B * mb].reshape(B, mb)
+    q = rng.standard_normal((B, Q, nkv * G, hd)).astype(np.float32)
+    out = st.paged_prefill(0, torch.from_numpy(q).cuda(), dev_u32(tables),
+                           dev_u32(prior), dev_u32(read),
+                           window=window).cpu().numpy()
+    cache, padded, mbo = oracle_subset(st, 0, list(tables), read)
+    want = orc.paged_prefill_f64(cache, q, padded, mbo, prior, read,
+                                 window=window)
+    return out, want
+
+
+@pytest.mark.parametrize("G,hd,bs", [(1, 64, 16), (2, 128, 16), (4, 64, 32),
+                                     (7, 64, 32), (8, 128, 8), (3, 32, 16),
+                                     (16, 64, 16)])
+def test_prefill_chunked_vs_oracle(G, hd, bs):
+    """Several query-row tiles per (sequence, KV head) (G * Q > 128),
+    chunk offsets that are not tile or block aligned, ragged read counts."""
+    out, want = _prefill_case(G * 100 + hd, 3, 97, 2, G, hd, bs, 0)
+    err = np.abs(out - want).max()
+    assert np.isfinite(out).all() and err < ATOL, err
+
+
+@pytest.mark.parametrize("window", [1, 37, 300])
+def test_prefill_window(window):
+    out, want = _prefill_case(window, 2, 200, 2, 4, 64, 16, window,
+                              prior=[0, 333])
+    assert np.abs(out - want).max() < ATOL
+
+
+def test_prefill_full_prompt_from_empty():
+    """Whole-prompt prefill (pos_offset 0, read_num = q_len), the
+    reference's first forward of a sequence, at 1000 tokens."""
+    out, want = _prefill_case(5, 2, 1000, 2, 2, 128, 16, 0, ragged=False,
+                              prior=[0, 0])
+    assert np.abs(out - want).max() < ATOL
+
+
+def test_prefill_edges():
+    """Rows that see no key (read_num <= pos_offset) are zero; q_len 1
+    agrees with the decode kernel; an out-of-range table entry is read as
+    masked, never faults, and leaves rows that do not reach it unchanged."""
+    nb, bs, nkv, hd, H = 40, 16, 2, 64, 8
+    st = HipKvStorage(1, nb, bs, nkv, hd)
+    fill_layer(st, 0, seed=4)
+    rng = np.random.default_rng(4)
+    tables = rng.permutation(nb).astype(np.uint32)[:36].reshape(3, 12)
+    q = torch.randn(3, 5, H, hd, device="cuda")
+    off = dev_u32([10, 50, 0])
+    read = dev_u32([0, 53, 0])  # seq 0 and 2 see nothing
+    out = st.paged_prefill(0, q, dev_u32(tables), off, read)
+    assert out[0].eq(0).all() and out[2].eq(0).all()
+    assert (out[1].abs().sum(-1) > 0).all()  # rows past read_num see < 53
+    # window 1: a row sees only its own position, absent past read_num
+    w1 = st.paged_prefill(0, q, dev_u32(tables), off, read, window=1)
+    assert (w1[1, :3].abs().sum(-1) > 0).all() and w1[1, 3:].eq(0).all()
+    # q_len 1 == decode
+    lens = np.array([1, 150, 192], np.uint32)
+    q1 = torch.randn(3, 1, H, hd, device="cuda")
+    a = st.paged_prefill(0, q1, dev_u32(tables), dev_u32(lens - 1),
+                         dev_u32(lens))
+    b = st.paged_decode(0, q1[:, 0].contiguous(), dev_u32(tables),
+                        dev_u32(lens), 192)
+    assert (a[:, 0] - b).abs().max().item() < 1e-3
+    # a bad block id in the last block of sequence 2
+    bad = tables.copy()
+    bad[2, 11] = 10_000
+    qq = torch.randn(3, 192, H, hd, device="cuda")
+    z = dev_u32([0, 0, 0])
+    full = dev_u32([192, 192, 192])
+    good = st.paged_prefill(0, qq, dev_u32(tables), z, full)
+    got = st.paged_prefill(0, qq, dev_u32(bad), z, full)
+    assert torch.isfinite(got).all()
+    assert torch.equal(got[:2], good[:2])
+    assert torch.equal(got[2, :176], good[2, :176])
+
+
+def test_prefill_rejections():
+    st = HipKvStorage(1, 4, 16, 1, 256)
+    with pytest.raises(RvkvError, match="paged_prefill: head_dim"):
+        st.paged_prefill(0, torch.zeros(1, 2, 2, 256, device="cuda"),
+                         dev_u32([[0]]), dev_u32([0]), dev_u32([2]))
+    st = HipKvStorage(1, 4, 4, 1, 64)
+    with pytest.raises(RvkvError, match="paged_prefill: block_size"):
+        st.paged_prefill(0, torch.zeros(1, 2, 2, 64, device="cuda"),
+                         dev_u32([[0]]), dev_u32([0]), dev_u32([2]))
+    st = HipKvStorage(1, 4, 16, 2, 64)
+    with pytest.raises(RvkvError, match="paged_prefill: n_heads"):
+        st.paged_prefill(0, torch.zeros(1, 2, 3, 64, device="cuda"),
+                         dev_u32([[0]]), dev_u32([0]), dev_u32([2]))

@@ -391,3 +391,69 @@ def test_attn_prep_composes_the_pinned_parts():
             y = v[r, h] + vb[h * hd:(h + 1) * hd]
             assert np.array_equal(cache.v[sb[r], so[r], h],
                                   orc.f32_to_f16_bits(y))
+
+
+# ---- (f)2: paged prefill / chunked attention ----------------------------------
+@pytest.mark.parametrize("case", range(6))
+def test_paged_prefill_f64_matches_metal_golden(golden, case):
+    """orc_paged_prefill_f64 on all six attn_decode cases of
+    src/metal/ops.rs:676-766, q_len 2 and 3 included: the Metal mask
+    (j >= valid or j + q_len > valid + qi) is batch_mask with
+    pos_offset = valid - q_len and read_num = valid."""
+    c = metal_case_inputs(case)
+    exp = np.array(golden["metal_attn_decode"][case]["expected"], np.float32)
+    cache = orc.KvCache(c["num_blocks"], c["bs"], c["n_kv"], c["hd"], orc.F32)
+    cache.k[:] = c["cache_k"]
+    cache.v[:] = c["cache_v"]
+    B, Q, H, D = c["batch"], c["q_len"], c["n_heads"], c["hd"]
+    valid = np.array([c["ctx"] - 2 * b for b in range(B)], np.uint32)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    out = orc.paged_prefill_f64(cache, c["q"].reshape(B, Q, H, D),
+                                c["block_idx"], c["max_blocks"], valid - Q,
+                                valid, scale=scale)
+    assert np.max(np.abs(out.reshape(-1) - exp)) < 1e-6
+
+
+def test_paged_prefill_f64_matches_reference_composition():
+    """Against the reference's own prefill composition, gather +
+    batch_mask + gqa_attention (src/model.rs:628-644, each pinned above),
+    over chunked offsets, ragged read counts, padding past read_num,
+    windows and GQA groups 1/3/4."""
+    rng = np.random.default_rng(21)
+    for (nkv, G, hd, B, Q, window) in [(2, 3, 16, 3, 5, 0), (1, 4, 8, 2, 9, 4),
+                                       (2, 1, 32, 2, 1, 0), (3, 2, 16, 4, 7, 3)]:
+        bs, mb = 4, 8
+        nb = B * mb
+        cache = orc.KvCache(nb, bs, nkv, hd, orc.F16)
+        cache.k[:] = orc.f32_to_f16_bits(rng.standard_normal(cache.k.shape))
+        cache.v[:] = orc.f32_to_f16_bits(rng.standard_normal(cache.v.shape))
+        tables = rng.permutation(nb).astype(np.uint32)
+        off = rng.integers(0, bs * mb - Q, B).astype(np.uint32)
+        read = np.minimum(off + Q + rng.integers(-2, 3, B), bs * mb)
+        read = read.astype(np.uint32)
+        q = rng.standard_normal((B, Q, nkv * G, hd)).astype(np.float32)
+        out = orc.paged_prefill_f64(cache, q, tables, mb, off, read,
+                                    window=window)
+        ctx = int(read.max())
+        gk, gv = cache.gather(tables, B, mb, ctx)
+        m = orc.batch_mask(off, read, Q, ctx, window)
+        ref = orc.gqa_attention(q.transpose(0, 2, 1, 3).copy(), gk, gv, m)
+        ref = ref.transpose(0, 2, 1, 3)
+        seen = np.isfinite(m.reshape(B, Q, ctx)).any(-1)  # rows with keys
+        assert np.max(np.abs(out - ref)[seen]) < 1e-5
+        assert np.all(out[~seen] == 0)
+
+
+def test_paged_prefill_f64_q_len_one_is_decode():
+    rng = np.random.default_rng(22)
+    cache = orc.KvCache(30, 16, 2, 32, orc.F16)
+    cache.k[:] = orc.f32_to_f16_bits(rng.standard_normal(cache.k.shape))
+    cache.v[:] = orc.f32_to_f16_bits(rng.standard_normal(cache.v.shape))
+    tables = rng.permutation(30).astype(np.uint32)
+    ctx = np.array([1, 77, 160], np.uint32)
+    q = rng.standard_normal((3, 1, 6, 32)).astype(np.float32)
+    for w in (0, 20):
+        a = orc.paged_prefill_f64(cache, q, tables, 10, ctx - 1, ctx,
+                                  window=w)
+        b = orc.paged_decode_f64(cache, q[:, 0], tables, 10, ctx, window=w)
+        assert np.array_equal(a[:, 0], b)
