@@ -24,6 +24,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0  # dense f16/bf16, no sparsity
 METRIC = "paged-decode attn HBM GB/s (% of peak) + decode tok/s, 1 MI355X"
 
 
@@ -56,6 +57,9 @@ def parse():
                    help="time the prefill append instead (BASELINE configs[2]: "
                         "every sequence's whole context scattered into the "
                         "paged cache, all layers; source dtype f32 or f16)")
+    p.add_argument("--prefill-attn", action="store_true",
+                   help="time whole-prompt paged prefill attention over the "
+                   "uniform batch of --config (default batch 16)")
     p.add_argument("--prep", action="store_true",
                    help="time the fused attention prep + append over the "
                    "prefill batch of --config instead")
@@ -207,6 +211,97 @@ def prompt_slots(torch, db):
         ps.append(pos)
     dev = lambda a: torch.from_numpy(np.concatenate(a).view(np.int32)).cuda()
     return dev(sb), dev(so), np.concatenate(ps)
+
+
+def run_prefill_attn(args, torch, W):
+    """Whole-prompt prefill attention over the paged cache: every sequence
+    of the config's uniform batch (its prompt already in the cache, as
+    after the prefill append) attends causally from all ctx positions,
+    pos_offset 0 and read_num = ctx, one rvkv_paged_prefill per layer.
+    Matrix-core bound: priced in flops against the f16 dense MFMA peak."""
+    from rvllm_amd.kv_storage import HipKvStorage
+    batch = args.batch or 16
+    db = build_workload(W, args.config, batch)
+    c = db.cfg
+    if len(set(int(x) for x in db.ctx_lens)) != 1:
+        raise SystemExit("--prefill-attn needs a uniform-length config")
+    L = int(db.ctx_lens[0])
+    st = HipKvStorage(c.n_layers, db.num_blocks, c.block_size, c.n_kv_heads,
+                      c.head_dim)
+    fill_pool(torch, st, c.seed, c.value_scale)
+    tables = torch.from_numpy(db.padded_tables().view(np.int32)).cuda()
+    zero = torch.zeros(db.batch, dtype=torch.int32, device="cuda")
+    read = torch.full((db.batch,), L, dtype=torch.int32, device="cuda")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(c.seed + 1)
+    q = torch.randn((db.batch, L, c.n_heads, c.head_dim), generator=g,
+                    device="cuda")
+    out = torch.empty_like(q)
+    window = c.window
+
+    def step():
+        for layer in range(c.n_layers):
+            st.paged_prefill(layer, q, tables, zero, read, out=out,
+                             window=window)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    launch_ms = e0.elapsed_time(e1) / (args.steps * c.n_layers)
+    pairs = W.prefill_visible_pairs(np.zeros(db.batch), db.ctx_lens, L,
+                                    window)
+    flops = W.prefill_attn_flops(pairs, c)
+    achieved = flops / (launch_ms * 1e-3) / 1e12
+    kv_bytes = int(db.ctx_lens.astype(np.int64).sum()) * c.n_kv_heads * \
+        c.head_dim * 4
+    qo_bytes = db.batch * L * c.n_heads * c.head_dim * 8
+    res = {
+        "metric": "paged prefill attention TFLOP/s, 1 MI355X",
+        "value": round(flops * c.n_layers / dt / 1e12, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 MFMA, f32 accumulate (f32 q/out, f16 cache)",
+        "data": "synthetic N(0,1)*scale KV and q, seeded permuted tables",
+        "config": {
+            "workload": f"{c.name} whole-prompt prefill attention: "
+                        f"{db.batch} seqs x {L} tokens, causal, "
+                        f"{c.n_layers} layers, {c.n_heads} q / "
+                        f"{c.n_kv_heads} kv heads, head_dim {c.head_dim}, "
+                        f"block_size {c.block_size}",
+            "global_batch": db.batch,
+            "seq_len": L,
+            "parallelism": "single GPU",
+        },
+        "tok_per_s": round(db.batch * L / dt, 1),
+        "roofline": {
+            "bound": "mfma",
+            "kernel": f"prefill_kernel<{c.head_dim}>",
+            "achieved": round(achieved, 2),
+            "peak": MFMA_F16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4),
+            "traffic": None,
+            "algorithmic_flops_per_launch": flops,
+            "min_hbm_bytes_per_launch": kv_bytes + qo_bytes,
+            "avg_launch_ms": round(launch_ms, 5),
+        },
+    }
+    print(json.dumps(res), flush=True)
 
 
 def run_prep(args, torch, W):
@@ -485,6 +580,9 @@ def main():
         return
     if args.prep:
         run_prep(args, torch, W)
+        return
+    if args.prefill_attn:
+        run_prefill_attn(args, torch, W)
         return
     db = build_workload(W, args.config, args.batch)
     c = db.cfg

@@ -44,6 +44,8 @@ namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
 constexpr int kBN = 64;   // keys per tile
 constexpr int kWaveRows = 32;
@@ -86,8 +88,8 @@ __global__ void __launch_bounds__(256) prefill_kernel(PrefillArgs a) {
   constexpr int KC = HD / 16;                 // MFMA k-steps of S
   constexpr int DT = HD / 32;                 // 32-row tiles of O^T
   constexpr int CPR = HD / 8;                 // 16-byte chunks per key row
-  constexpr int CH = kBN * CPR / 256;         // chunks per thread per tile
-  static_assert(CH >= 1 && kBN * CPR % 256 == 0, "tile/thread mismatch");
+  constexpr int CHK = kBN * CPR / 256;        // K chunks per thread per tile
+  static_assert(CHK >= 1 && kBN * CPR % 256 == 0, "tile/thread mismatch");
   extern __shared__ __align__(16) unsigned char smem[];
   uint16_t *ks = reinterpret_cast<uint16_t *>(smem);
   uint16_t *vt = reinterpret_cast<uint16_t *>(smem + Lds<HD>::k_bytes);
@@ -118,6 +120,9 @@ __global__ void __launch_bounds__(256) prefill_kernel(PrefillArgs a) {
   const uint32_t rw1 = min(rw0 + kWaveRows, a.rows) - 1u;
   const uint32_t w_end = wave_live ? min(ctx, off + rw1 / a.group + 1u) : 0u;
   const uint32_t w_begin = lo_bound(off + rw0 / a.group, a.window);
+  // Keys every row of the wave sees: [w_lo_max, w_hi_min).
+  const uint32_t w_hi_min = wave_live ? min(ctx, off + rw0 / a.group + 1u) : 0u;
+  const uint32_t w_lo_max = lo_bound(off + rw1 / a.group, a.window);
 
   // This lane's query row.
   const uint32_t r = rw0 + ln;
@@ -162,47 +167,107 @@ __global__ void __launch_bounds__(256) prefill_kernel(PrefillArgs a) {
                       (size_t)kvh * a.head_stride * 2;
   const char *vbase = reinterpret_cast<const char *>(a.vc) +
                       (size_t)kvh * a.head_stride * 2;
-  uint4 kr[CH], vr[CH];
-  uint32_t okbits = 0;
+  // Tile loads. K goes to LDS row-major, so its 16-byte chunks are taken in
+  // row order (chunk c: key c / CPR, column chunk c % CPR: whole rows per
+  // lane group, coalesced). V goes to LDS transposed, so its chunks are
+  // taken in key-pair order (pair c % 32, column chunk c / 32): a lane loads
+  // keys 2p and 2p+1 of one column chunk and writes 8 dwords Vt[d][2p..2p+1];
+  // the 32 lanes of a half-wave write 32 consecutive dwords of one Vt row,
+  // one per bank. Block ids are fetched one tile ahead so a tile's loads
+  // issue back to back; loads are unconditional (invalid ones read block 0)
+  // and invalid V is zeroed at the LDS store, because masked keys get
+  // probability 0 and 0 * (stale V) must stay 0.
+  constexpr int VP = kBN / 2 * CPR;               // V chunk pairs per tile
+  constexpr int CHV = VP >= 256 ? VP / 256 : 1;   // per thread
+  const bool v_lane = VP >= 256 || tid < VP;      // all but hd 32
+  uint32_t kid[CHK], vid[CHV];
+  u32x4 kr[CHK], vr0[CHV], vr1[CHV];
+  uint32_t kbits = 0, vbits = 0;
 
-  auto load = [&](uint32_t kt) {
-    okbits = 0;
+  auto fetch_ids = [&](uint32_t kt) {
 #pragma unroll
-    for (int i = 0; i < CH; ++i) {
+    for (int i = 0; i < CHK; ++i) {
+      const uint32_t tok = kt + (uint32_t)((tid + 256 * i) / CPR);
+      kid[i] = table[min(tok >> a.bs_log2, a.max_blocks - 1u)];
+    }
+#pragma unroll
+    for (int j = 0; j < CHV; ++j) {
+      const uint32_t tok = kt + 2u * (uint32_t)((tid + 256 * j) % 32);
+      vid[j] = table[min(tok >> a.bs_log2, a.max_blocks - 1u)];
+    }
+  };
+  auto load = [&](uint32_t kt) {
+    kbits = 0;
+    vbits = 0;
+#pragma unroll
+    for (int i = 0; i < CHK; ++i) {
       const int c = tid + 256 * i;
       const uint32_t tok = kt + (uint32_t)(c / CPR);
-      const int dc = c % CPR;
-      const uint32_t bi = min(tok >> a.bs_log2, a.max_blocks - 1u);
-      const uint32_t blk = table[bi];
-      const bool ok = tok < k_end && blk < a.num_blocks;
-      okbits |= (uint32_t)ok << i;
-      const uint64_t at = ((uint64_t)(ok ? blk : 0u) * a.block_stride +
-                           (uint64_t)(tok & bs_mask) * HD + dc * 8) * 2;
-      kr[i] = ok ? *reinterpret_cast<const uint4 *>(kbase + at)
-                 : make_uint4(0, 0, 0, 0);
-      vr[i] = ok ? *reinterpret_cast<const uint4 *>(vbase + at)
-                 : make_uint4(0, 0, 0, 0);
+      const bool ok = tok < k_end && kid[i] < a.num_blocks;
+      kbits |= (uint32_t)ok << i;
+      const uint64_t at = ((uint64_t)(ok ? kid[i] : 0u) * a.block_stride +
+                           (uint64_t)(tok & bs_mask) * HD + (c % CPR) * 8) * 2;
+      kr[i] = *reinterpret_cast<const u32x4 *>(kbase + at);
+    }
+#pragma unroll
+    for (int j = 0; j < CHV; ++j) {
+      const int c = tid + 256 * j;
+      const uint32_t tok = kt + 2u * (uint32_t)(c % 32);
+      const bool okb = vid[j] < a.num_blocks;
+      vbits |= (uint32_t)(okb && tok < k_end) << (2 * j);
+      vbits |= (uint32_t)(okb && tok + 1 < k_end) << (2 * j + 1);
+      const uint64_t at = ((uint64_t)(okb ? vid[j] : 0u) * a.block_stride +
+                           (uint64_t)(tok & bs_mask) * HD + (c / 32) * 8) * 2;
+      if (v_lane) {
+        vr0[j] = *reinterpret_cast<const u32x4 *>(vbase + at);
+        vr1[j] = *reinterpret_cast<const u32x4 *>(vbase + at + HD * 2);
+      }
     }
   };
 
-  if (k_begin < k_end) load(k_begin);
+  if (k_begin < k_end) {
+    fetch_ids(k_begin);
+    load(k_begin);
+    fetch_ids(k_begin + kBN);
+  }
   for (uint32_t kt = k_begin; kt < k_end; kt += kBN) {
     __syncthreads();  // the previous tile is no longer read
 #pragma unroll
-    for (int i = 0; i < CH; ++i) {
+    for (int i = 0; i < CHK; ++i) {
       const int c = tid + 256 * i;
       const int key = c / CPR, dc = c % CPR;
-      *reinterpret_cast<uint4 *>(ks + key * KS + dc * 8) = kr[i];
-      const uint32_t w[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        vt[(dc * 8 + 2 * e) * VS + key] = (uint16_t)(w[e] & 0xffffu);
-        vt[(dc * 8 + 2 * e + 1) * VS + key] = (uint16_t)(w[e] >> 16);
-      }
-      if (dc == 0) kok[key] = (uint8_t)((okbits >> i) & 1u);
+      *reinterpret_cast<u32x4 *>(ks + key * KS + dc * 8) = kr[i];
+      // Every loader of this key writes the same flag (no branch, which
+      // would keep kr[] out of registers).
+      kok[key] = (uint8_t)((kbits >> i) & 1u);
     }
-    __syncthreads();
-    if (kt + kBN < k_end) load(kt + kBN);
+    if (v_lane) {
+#pragma unroll
+      for (int j = 0; j < CHV; ++j) {
+        const int c = tid + 256 * j;
+        const int pr = c % 32, dc = c / 32;
+        const uint32_t m0 = (vbits >> (2 * j)) & 1u ? 0xffffu : 0u;
+        const uint32_t m1 = (vbits >> (2 * j + 1)) & 1u ? 0xffff0000u : 0u;
+        uint32_t *row = reinterpret_cast<uint32_t *>(vt + dc * 8 * VS) + pr;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          // d = 8dc + 2e: low halves of both keys; d + 1: high halves.
+          row[(2 * e) * (VS / 2)] =
+              (__builtin_amdgcn_perm(vr1[j][e], vr0[j][e], 0x05040100u)) &
+              (m0 | m1);
+          row[(2 * e + 1) * (VS / 2)] =
+              (__builtin_amdgcn_perm(vr1[j][e], vr0[j][e], 0x07060302u)) &
+              (m0 | m1);
+        }
+      }
+    }
+    // Every key of the tile readable (in range, valid block)?
+    const bool tile_ok = __syncthreads_and(
+        (int)(kbits == (1u << CHK) - 1u));
+    if (kt + kBN < k_end) {
+      load(kt + kBN);
+      fetch_ids(kt + 2 * kBN);
+    }
     if (!(kt < w_end && kt + kBN > w_begin)) continue;  // nothing for this wave
 
     f32x16 s[2];
@@ -219,47 +284,66 @@ __global__ void __launch_bounds__(256) prefill_kernel(PrefillArgs a) {
       }
     }
 
-    // Mask, online softmax; register j of sub-tile t is key
+    // Mask (only where some row of the wave does not see the whole tile),
+    // then the online softmax; register j of sub-tile t is key
     // kt + 32t + 16(j/8) + 8hl + j%8.
     float mx = kNegBig;
+    if (tile_ok && kt >= w_lo_max && kt + kBN <= w_hi_min) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int g8 = 0; g8 < 2; ++g8) {
-        const uint32_t k0 = 32 * t + 16 * g8 + 8 * hl;
-        const uint64_t okw = *reinterpret_cast<const uint64_t *>(kok + k0);
+        for (int j = 0; j < 16; j += 2)
+          mx = fmaxf(mx, fmaxf(s[t][j], s[t][j + 1]));
+    } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const uint32_t key = kt + k0 + e;
-          const bool valid = ((okw >> (8 * e)) & 1u) && key >= row_lo &&
-                             key < row_hi;
-          const float x = valid ? s[t][8 * g8 + e] : -__builtin_inff();
-          s[t][8 * g8 + e] = x;
-          mx = fmaxf(mx, x);
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int g8 = 0; g8 < 2; ++g8) {
+          const uint32_t k0 = 32 * t + 16 * g8 + 8 * hl;
+          const uint64_t okw = *reinterpret_cast<const uint64_t *>(kok + k0);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const uint32_t key = kt + k0 + e;
+            const bool valid = ((okw >> (8 * e)) & 1u) && key >= row_lo &&
+                               key < row_hi;
+            const float x = valid ? s[t][8 * g8 + e] : -__builtin_inff();
+            s[t][8 * g8 + e] = x;
+            mx = fmaxf(mx, x);
+          }
         }
-      }
+    }
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m, mx);
-    const float alpha = __builtin_amdgcn_exp2f(m - m_new);
-    m = m_new;
+    // Lazy rescale: the reference max m moves only when the tile's max
+    // exceeds it by more than 2^8, so probabilities stay <= 256 (exact
+    // in f16's range) and O and l are rescaled on few tiles; the final
+    // division by l cancels whichever m was used.
+    const bool grow = mx > m + 8.0f;
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+      const float m_new = grow ? mx : m;
+      const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+      m = m_new;
+      l *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) o[dt][j] *= alpha;
+    }
     half8 pb[2][2];
     float psum = 0.f;
+    const h2 ones = h2{(_Float16)1.0f, (_Float16)1.0f};
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int c = 0; c < 2; ++c)
+      for (int c = 0; c < 2; ++c) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const _Float16 ph =
-              (_Float16)__builtin_amdgcn_exp2f(s[t][8 * c + e] - m_new);
-          pb[t][c][e] = ph;
-          psum += (float)ph;
-        }
-    l = l * alpha + psum;
+        for (int e = 0; e < 8; ++e)
+          pb[t][c][e] = (_Float16)__builtin_amdgcn_exp2f(s[t][8 * c + e] - m);
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) o[dt][j] *= alpha;
+        for (int e = 0; e < 8; e += 2)
+          psum = __builtin_amdgcn_fdot2(h2{pb[t][c][e], pb[t][c][e + 1]},
+                                        ones, psum, false);
+      }
+    l += psum;
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll

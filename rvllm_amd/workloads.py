@@ -297,3 +297,25 @@ def prep_bytes(n_tokens: int, cfg: Config) -> int:
     weights = 4 * ((H + 2 * KV) * hd if cfg.qkv_bias else 0) \
         + 4 * (2 * hd if cfg.qk_norm else 0)
     return n_tokens * per_tok + weights
+
+
+def prefill_visible_pairs(pos_offset, read_num, q_len: int,
+                          window: int = 0) -> int:
+    """Number of (query row, key) pairs batch_mask leaves visible
+    (src/model.rs:346-369), summed over the batch: row i of sequence b at
+    p = pos_offset[b] + i sees keys [max(0, p + 1 - window), min(read_num,
+    p + 1))."""
+    total = 0
+    for off, rd in zip(np.asarray(pos_offset, np.int64),
+                       np.asarray(read_num, np.int64)):
+        p = off + np.arange(q_len, dtype=np.int64)
+        hi = np.minimum(rd, p + 1)
+        lo = np.maximum(0, p + 1 - window) if window > 0 else 0
+        total += int(np.maximum(hi - lo, 0).sum())
+    return total
+
+
+def prefill_attn_flops(pairs: int, cfg: Config) -> int:
+    """Algorithmic flops of paged prefill attention: per visible pair and
+    query head, q.k (2 hd) and p.v (2 hd)."""
+    return pairs * cfg.n_heads * 4 * cfg.head_dim
