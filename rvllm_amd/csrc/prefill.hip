@@ -82,8 +82,12 @@ __device__ __forceinline__ uint32_t lo_bound(uint32_t p, int32_t window) {
                                                   : 0u;
 }
 
+// Two workgroups per CU at head_dim 128 (<= 256 registers a lane, so the
+// O accumulators stay in arch VGPRs), three below; a second resident
+// workgroup overlaps its softmax with the other's matrix work.
 template <int HD>
-__global__ void __launch_bounds__(256) prefill_kernel(PrefillArgs a) {
+__global__ void __launch_bounds__(256, HD <= 64 ? 3 : 2)
+    prefill_kernel(PrefillArgs a) {
   constexpr int KS = Lds<HD>::KS, VS = Lds<HD>::VS;
   constexpr int KC = HD / 16;                 // MFMA k-steps of S
   constexpr int DT = HD / 32;                 // 32-row tiles of O^T
