@@ -36,6 +36,9 @@ def parse():
     p.add_argument("--config", default="llama-3.2-1b")
     p.add_argument("--batch", type=int, default=0,
                    help="override the number of sequences (uniform configs)")
+    p.add_argument("--ctx", type=int, default=0,
+                   help="context length of the uniform configs (llama, "
+                   "qwen3, gemma); 0 = the config's own")
     p.add_argument("--no-cpu", action="store_true",
                    help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -94,11 +97,11 @@ def copy_calibration(torch, steps):
         "GB/s": round(2 * n * 4 / (ms * 1e-3) / 1e9, 1)}}), flush=True)
 
 
-def measured_traffic(config, batch, unfused):
+def measured_traffic(config, batch, unfused, ctx=0):
     """HBM bytes per decode launch measured by rocprofv3 --pmc (FETCH_SIZE +
     WRITE_SIZE, each scaled by the same counter's reading for a copy of
     known size) for this workload, from the committed summary, or None."""
-    if batch:
+    if batch or ctx:
         return None
     if unfused:
         return None
@@ -112,17 +115,17 @@ def measured_traffic(config, batch, unfused):
     return rec.get("traffic_bytes_per_launch") if rec else None
 
 
-def build_workload(W, name, batch=0):
+def build_workload(W, name, batch=0, ctx=0):
     c = W.CONFIGS[name]
     if batch:
         import dataclasses
         c = dataclasses.replace(c, batch=batch)
     if name == "llama-3.2-1b":
-        return W.uniform_batch(c, 2048)
+        return W.uniform_batch(c, ctx or 2048)
     if name == "qwen3-0.6b":
-        return W.uniform_batch(c, 4096)
+        return W.uniform_batch(c, ctx or 4096)
     if name == "gemma-3-270m":
-        return W.uniform_batch(c, 1024)
+        return W.uniform_batch(c, ctx or 1024)
     if name == "qwen2.5-0.5b":
         return W.qwen25_batch(batch=c.batch)
     if name == "smollm2-360m":
@@ -221,7 +224,7 @@ def run_prefill_attn(args, torch, W):
     Matrix-core bound: priced in flops against the f16 dense MFMA peak."""
     from rvllm_amd.kv_storage import HipKvStorage
     batch = args.batch or 16
-    db = build_workload(W, args.config, batch)
+    db = build_workload(W, args.config, batch, args.ctx)
     c = db.cfg
     if len(set(int(x) for x in db.ctx_lens)) != 1:
         raise SystemExit("--prefill-attn needs a uniform-length config")
@@ -313,7 +316,7 @@ def run_prep(args, torch, W):
     (Qwen2.5: bias, Qwen3: QK norm)."""
     from rvllm_amd.kv_storage import HipKvStorage
     from rvllm_amd.rope import rope_cos_sin
-    db = build_workload(W, args.config, args.batch)
+    db = build_workload(W, args.config, args.batch, args.ctx)
     c = db.cfg
     st = HipKvStorage(c.n_layers, db.num_blocks, c.block_size, c.n_kv_heads,
                       c.head_dim)
@@ -401,7 +404,7 @@ def run_prefill(args, torch, W):
     device buffer reused by every layer (each layer's write goes to its own
     pool, and the source is far larger than the 256 MB MALL)."""
     from rvllm_amd.kv_storage import HipKvStorage
-    db = build_workload(W, args.config, args.batch)
+    db = build_workload(W, args.config, args.batch, args.ctx)
     c = db.cfg
     st = HipKvStorage(c.n_layers, db.num_blocks, c.block_size, c.n_kv_heads,
                       c.head_dim)
@@ -584,7 +587,7 @@ def main():
     if args.prefill_attn:
         run_prefill_attn(args, torch, W)
         return
-    db = build_workload(W, args.config, args.batch)
+    db = build_workload(W, args.config, args.batch, args.ctx)
     c = db.cfg
     st = HipKvStorage(c.n_layers, db.num_blocks, c.block_size, c.n_kv_heads,
                       c.head_dim)
@@ -683,7 +686,8 @@ def main():
     torch.cuda.synchronize()
     dec_ms = e0.elapsed_time(e1) / (args.steps * L)
 
-    traffic = measured_traffic(args.config, args.batch, args.unfused)
+    traffic = measured_traffic(args.config, args.batch, args.unfused,
+                               args.ctx)
     app_bytes = W.append_bytes(B, c)
     # The fused launch also moves the appended rows (f32 in, f16 out).
     dec_bytes = W.decode_bytes(db) + (0 if args.unfused else app_bytes)

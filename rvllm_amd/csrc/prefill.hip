@@ -62,6 +62,7 @@ struct PrefillArgs {
   uint64_t block_stride;  // elements per block (all heads)
   uint32_t head_stride;   // elements per (block, head) tile
   uint32_t q_len, max_blocks, num_blocks, n_heads, group, bs_log2;
+  uint32_t batch, n_kv;
   uint32_t rows;     // group * q_len rows per (sequence, KV head)
   uint32_t n_tiles;  // ceil(rows / kBM)
   float qscale;      // scale * log2(e)
@@ -99,8 +100,20 @@ __global__ void __launch_bounds__(256, HD <= 64 ? 3 : 2)
   uint16_t *vt = reinterpret_cast<uint16_t *>(smem + Lds<HD>::k_bytes);
   uint8_t *kok = smem + Lds<HD>::k_bytes + Lds<HD>::v_bytes;
 
-  const uint32_t b = blockIdx.z, kvh = blockIdx.y;
-  const uint32_t tile = a.n_tiles - 1 - blockIdx.x;  // long rows first
+  // XCD-aware order: workgroups are dispatched round-robin over the 8 XCDs
+  // (each with its own L2), so workgroup w runs on XCD w % 8. Renumber so
+  // each XCD gets a contiguous range of logical ids, in which the query
+  // tiles of one (sequence, KV head) are adjacent: they re-read the same
+  // K/V, which then stays in that XCD's L2. Within a head, long (late)
+  // rows go first.
+  const uint32_t n_wg = a.n_tiles * a.n_kv * a.batch;
+  const uint32_t w = blockIdx.x, xcd = w % 8, idx = w / 8;
+  const uint32_t per = n_wg / 8, rem = n_wg % 8;
+  const uint32_t logical = xcd < rem ? xcd * (per + 1) + idx
+                                     : rem * (per + 1) + (xcd - rem) * per + idx;
+  const uint32_t tile = a.n_tiles - 1 - logical % a.n_tiles;
+  const uint32_t kvh = (logical / a.n_tiles) % a.n_kv;
+  const uint32_t b = logical / a.n_tiles / a.n_kv;
   const int tid = threadIdx.x;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63, hl = lane >> 5, ln = lane & 31;
@@ -184,47 +197,74 @@ __global__ void __launch_bounds__(256, HD <= 64 ? 3 : 2)
   constexpr int VP = kBN / 2 * CPR;               // V chunk pairs per tile
   constexpr int CHV = VP >= 256 ? VP / 256 : 1;   // per thread
   const bool v_lane = VP >= 256 || tid < VP;      // all but hd 32
+
+  // Are all the blocks this workgroup reads valid? One scan of its table
+  // range; then the per-tile work needs no per-key flags (key < row_hi
+  // already implies key < k_end).
+  bool all_ok = true;
+  if (k_begin < k_end) {
+    int bad = 0;
+    for (uint32_t i = (k_begin >> a.bs_log2) + tid;
+         i <= ((k_end - 1u) >> a.bs_log2); i += 256)
+      bad |= table[i] >= a.num_blocks;
+    all_ok = !__syncthreads_or(bad);
+  }
+
+  // Per-lane constants: tiles start at multiples of 64, so a chunk's byte
+  // offset inside its (block, head) tile and its block index relative to
+  // the tile's first block are the same for every tile (for block_size >
+  // 64 the tile's own offset inside the block is added per tile).
+  uint32_t k_key[CHK], k_off[CHK], k_db[CHK];
+#pragma unroll
+  for (int i = 0; i < CHK; ++i) {
+    const int c = tid + 256 * i;
+    k_key[i] = (uint32_t)(c / CPR);
+    k_off[i] = ((k_key[i] & bs_mask) * HD + (c % CPR) * 8) * 2;
+    k_db[i] = k_key[i] >> a.bs_log2;
+  }
+  uint32_t v_key[CHV], v_off[CHV], v_db[CHV];
+#pragma unroll
+  for (int j = 0; j < CHV; ++j) {
+    const int c = tid + 256 * j;
+    v_key[j] = 2u * (uint32_t)(c % 32);
+    v_off[j] = ((v_key[j] & bs_mask) * HD + (c / 32) * 8) * 2;
+    v_db[j] = v_key[j] >> a.bs_log2;
+  }
+  const uint64_t blk_bytes = a.block_stride * 2;
   uint32_t kid[CHK], vid[CHV];
   u32x4 kr[CHK], vr0[CHV], vr1[CHV];
   uint32_t kbits = 0, vbits = 0;
 
   auto fetch_ids = [&](uint32_t kt) {
+    const uint32_t b0 = kt >> a.bs_log2, last = a.max_blocks - 1u;
 #pragma unroll
-    for (int i = 0; i < CHK; ++i) {
-      const uint32_t tok = kt + (uint32_t)((tid + 256 * i) / CPR);
-      kid[i] = table[min(tok >> a.bs_log2, a.max_blocks - 1u)];
-    }
+    for (int i = 0; i < CHK; ++i) kid[i] = table[min(b0 + k_db[i], last)];
 #pragma unroll
-    for (int j = 0; j < CHV; ++j) {
-      const uint32_t tok = kt + 2u * (uint32_t)((tid + 256 * j) % 32);
-      vid[j] = table[min(tok >> a.bs_log2, a.max_blocks - 1u)];
-    }
+    for (int j = 0; j < CHV; ++j) vid[j] = table[min(b0 + v_db[j], last)];
   };
   auto load = [&](uint32_t kt) {
+    const uint32_t t_off = (kt & bs_mask) * HD * 2;  // 0 unless bs > 64
     kbits = 0;
     vbits = 0;
 #pragma unroll
     for (int i = 0; i < CHK; ++i) {
-      const int c = tid + 256 * i;
-      const uint32_t tok = kt + (uint32_t)(c / CPR);
-      const bool ok = tok < k_end && kid[i] < a.num_blocks;
-      kbits |= (uint32_t)ok << i;
-      const uint64_t at = ((uint64_t)(ok ? kid[i] : 0u) * a.block_stride +
-                           (uint64_t)(tok & bs_mask) * HD + (c % CPR) * 8) * 2;
-      kr[i] = *reinterpret_cast<const u32x4 *>(kbase + at);
+      const bool okb = all_ok || kid[i] < a.num_blocks;
+      kbits |= (uint32_t)(okb && kt + k_key[i] < k_end) << i;
+      kr[i] = *reinterpret_cast<const u32x4 *>(
+          kbase + (uint64_t)(okb ? kid[i] : 0u) * blk_bytes + t_off +
+          k_off[i]);
     }
 #pragma unroll
     for (int j = 0; j < CHV; ++j) {
-      const int c = tid + 256 * j;
-      const uint32_t tok = kt + 2u * (uint32_t)(c % 32);
-      const bool okb = vid[j] < a.num_blocks;
+      const bool okb = all_ok || vid[j] < a.num_blocks;
+      const uint32_t tok = kt + v_key[j];
       vbits |= (uint32_t)(okb && tok < k_end) << (2 * j);
       vbits |= (uint32_t)(okb && tok + 1 < k_end) << (2 * j + 1);
-      const uint64_t at = ((uint64_t)(okb ? vid[j] : 0u) * a.block_stride +
-                           (uint64_t)(tok & bs_mask) * HD + (c / 32) * 8) * 2;
+      const char *vp = vbase + (uint64_t)(okb ? vid[j] : 0u) * blk_bytes +
+                       t_off + v_off[j];
       if (v_lane) {
-        vr0[j] = *reinterpret_cast<const u32x4 *>(vbase + at);
-        vr1[j] = *reinterpret_cast<const u32x4 *>(vbase + at + HD * 2);
+        vr0[j] = *reinterpret_cast<const u32x4 *>(vp);
+        vr1[j] = *reinterpret_cast<const u32x4 *>(vp + HD * 2);
       }
     }
   };
@@ -235,39 +275,38 @@ __global__ void __launch_bounds__(256, HD <= 64 ? 3 : 2)
     fetch_ids(k_begin + kBN);
   }
   for (uint32_t kt = k_begin; kt < k_end; kt += kBN) {
+    // Every key of the tile readable: all blocks valid, tile inside k_end.
+    const bool tile_ok = all_ok && kt + kBN <= k_end;
     __syncthreads();  // the previous tile is no longer read
 #pragma unroll
     for (int i = 0; i < CHK; ++i) {
       const int c = tid + 256 * i;
       const int key = c / CPR, dc = c % CPR;
       *reinterpret_cast<u32x4 *>(ks + key * KS + dc * 8) = kr[i];
-      // Every loader of this key writes the same flag (no branch, which
-      // would keep kr[] out of registers).
-      kok[key] = (uint8_t)((kbits >> i) & 1u);
+      // Every loader of a key writes the same flag.
+      if (!all_ok) kok[key] = (uint8_t)((kbits >> i) & 1u);
     }
     if (v_lane) {
 #pragma unroll
       for (int j = 0; j < CHV; ++j) {
         const int c = tid + 256 * j;
         const int pr = c % 32, dc = c / 32;
-        const uint32_t m0 = (vbits >> (2 * j)) & 1u ? 0xffffu : 0u;
-        const uint32_t m1 = (vbits >> (2 * j + 1)) & 1u ? 0xffff0000u : 0u;
+        const uint32_t mask = tile_ok ? 0xffffffffu
+                              : (((vbits >> (2 * j)) & 1u ? 0xffffu : 0u) |
+                                 ((vbits >> (2 * j + 1)) & 1u ? 0xffff0000u
+                                                              : 0u));
         uint32_t *row = reinterpret_cast<uint32_t *>(vt + dc * 8 * VS) + pr;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           // d = 8dc + 2e: low halves of both keys; d + 1: high halves.
           row[(2 * e) * (VS / 2)] =
-              (__builtin_amdgcn_perm(vr1[j][e], vr0[j][e], 0x05040100u)) &
-              (m0 | m1);
+              __builtin_amdgcn_perm(vr1[j][e], vr0[j][e], 0x05040100u) & mask;
           row[(2 * e + 1) * (VS / 2)] =
-              (__builtin_amdgcn_perm(vr1[j][e], vr0[j][e], 0x07060302u)) &
-              (m0 | m1);
+              __builtin_amdgcn_perm(vr1[j][e], vr0[j][e], 0x07060302u) & mask;
         }
       }
     }
-    // Every key of the tile readable (in range, valid block)?
-    const bool tile_ok = __syncthreads_and(
-        (int)(kbits == (1u << CHK) - 1u));
+    __syncthreads();
     if (kt + kBN < k_end) {
       load(kt + kBN);
       fetch_ids(kt + 2 * kBN);
@@ -276,17 +315,20 @@ __global__ void __launch_bounds__(256, HD <= 64 ? 3 : 2)
 
     f32x16 s[2];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int j = 0; j < 16; ++j) s[t][j] = 0.f;
+    // The two sub-tiles' accumulation chains alternate, so each MFMA's
+    // dependency on the previous one of its chain is hidden.
 #pragma unroll
-      for (int kc = 0; kc < KC; ++kc) {
+    for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
         const half8 kf = *reinterpret_cast<const half8 *>(
             ks + (32 * t + sig) * KS + kc * 16 + hl * 8);
         s[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[kc], s[t], 0, 0,
                                                       0);
       }
-    }
 
     // Mask (only where some row of the wave does not see the whole tile),
     // then the online softmax; register j of sub-tile t is key
@@ -304,12 +346,13 @@ __global__ void __launch_bounds__(256, HD <= 64 ? 3 : 2)
 #pragma unroll
         for (int g8 = 0; g8 < 2; ++g8) {
           const uint32_t k0 = 32 * t + 16 * g8 + 8 * hl;
-          const uint64_t okw = *reinterpret_cast<const uint64_t *>(kok + k0);
+          const uint64_t okw =
+              all_ok ? ~0ull : *reinterpret_cast<const uint64_t *>(kok + k0);
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
             const uint32_t key = kt + k0 + e;
-            const bool valid = ((okw >> (8 * e)) & 1u) && key >= row_lo &&
-                               key < row_hi;
+            const bool valid = (all_ok || ((okw >> (8 * e)) & 1u)) &&
+                               key >= row_lo && key < row_hi;
             const float x = valid ? s[t][8 * g8 + e] : -__builtin_inff();
             s[t][8 * g8 + e] = x;
             mx = fmaxf(mx, x);
@@ -409,8 +452,6 @@ int rvkv_paged_prefill(rvkv_pool *pool, uint32_t layer, const float *q,
   if (bs < 8 || (bs & (bs - 1)) != 0)
     return fail(RVKV_EUNSUPPORTED, op,
                 "block_size must be a power of two >= 8");
-  if (batch > 65535 || pool->n_kv > 65535)
-    return fail(RVKV_EUNSUPPORTED, op, "batch and n_kv_heads must be <= 65535");
   if ((uintptr_t)q % 16 || (uintptr_t)out % 16)
     return fail(RVKV_EINVAL, op, "q and out must be 16-byte aligned");
   if ((uint64_t)max_blocks * bs > 0x80000000ull)
@@ -443,7 +484,12 @@ int rvkv_paged_prefill(rvkv_pool *pool, uint32_t layer, const float *q,
   a.n_tiles = (uint32_t)((rows + kBM - 1) / kBM);
   a.qscale = scale * 1.4426950408889634f;
   a.window = window;
-  const dim3 grid(a.n_tiles, pool->n_kv, batch);
+  a.batch = batch;
+  a.n_kv = pool->n_kv;
+  const uint64_t n_wg = (uint64_t)a.n_tiles * pool->n_kv * batch;
+  if (n_wg > 0x7fffffffull)
+    return fail(RVKV_EUNSUPPORTED, op, "too many query tiles for one launch");
+  const dim3 grid((uint32_t)n_wg);
   switch (hd) {
     case 32: launch_prefill<32>(a, grid, pool->stream); break;
     case 64: launch_prefill<64>(a, grid, pool->stream); break;
