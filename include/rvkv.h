@@ -331,6 +331,86 @@ uint32_t rvkv_bm_refcount(const rvkv_bm *bm, uint32_t block);
 int rvkv_bm_table(const rvkv_bm *bm, int64_t seq, uint32_t *table,
                   uint32_t cap);
 
+/* ---- next row (f)3: continuous-batching scheduler with prefix cache -----
+ * The contract rvllm's engine uses from the kv-cache-scheduler crate (0.2.0,
+ * not vendored; used at src/engine.rs:351-539): a refcounted block pool
+ * (pool.available(), pool.total_allocs), FIFO `waiting` and `running`
+ * lists, sequences holding token_ids and a block table, prefix_cache.
+ * match_prefix, prefill(seq), step() (one more slot for every running
+ * sequence, preempting from the back of `running` when the pool is empty),
+ * finish_sequence(seq) and the prefix_hits / prefix_total metrics. Host
+ * only; ids are int64, blocks u32. Full blocks whose tokens are final are
+ * kept matchable in a prefix cache (also after release, until evicted, LRU);
+ * the block of a sequence's last prompt token is never matched. Errors: -1
+ * (RVKV_EINVAL) or RVKV_ENOMEM, message in rvkv_sched_last_error(). */
+typedef struct rvkv_sched rvkv_sched;
+
+const char *rvkv_sched_last_error(void);
+/* Scheduler::new(num_blocks, block_size), src/engine.rs:226 */
+rvkv_sched *rvkv_sched_create(uint32_t num_blocks, uint32_t block_size);
+void rvkv_sched_destroy(rvkv_sched *s);
+/* scheduler.add_request(tokens), src/engine.rs:314-316: queued at the back
+ * of waiting; returns the sequence id. */
+int64_t rvkv_sched_add_request(rvkv_sched *s, const int32_t *tokens,
+                               uint32_t n);
+/* pool.available() / pool.total_allocs, src/engine.rs:361, 626 */
+uint32_t rvkv_sched_available(const rvkv_sched *s);
+uint64_t rvkv_sched_total_allocs(const rvkv_sched *s);
+/* metrics.prefix_hits / prefix_total (src/engine.rs:624-625) and the
+ * number of preemptions so far; any pointer may be NULL. */
+void rvkv_sched_metrics(const rvkv_sched *s, uint64_t *prefix_hits,
+                        uint64_t *prefix_total, uint64_t *preemptions);
+/* waiting.len() / running.len() and their contents in order (copies at
+ * most cap ids, returns the length), src/engine.rs:272-282, 353-357 */
+uint32_t rvkv_sched_num_waiting(const rvkv_sched *s);
+uint32_t rvkv_sched_num_running(const rvkv_sched *s);
+uint32_t rvkv_sched_waiting(const rvkv_sched *s, int64_t *out, uint32_t cap);
+uint32_t rvkv_sched_running(const rvkv_sched *s, int64_t *out, uint32_t cap);
+int rvkv_sched_has_seq(const rvkv_sched *s, int64_t id);
+/* prefix_cache.match_prefix(tokens).1, src/engine.rs:365-367: the cached
+ * blocks of the longest matching run of full leading blocks (copies at most
+ * cap, returns the count); no side effects. */
+uint32_t rvkv_sched_match_prefix(const rvkv_sched *s, const int32_t *tokens,
+                                 uint32_t n, uint32_t *blocks, uint32_t cap);
+/* scheduler.prefill(seq), src/engine.rs:371: gives the sequence's token_ids
+ * a block table (matched prefix blocks shared, the rest allocated) and moves
+ * it from waiting to running; all-or-nothing (RVKV_ENOMEM). */
+int rvkv_sched_prefill(rvkv_sched *s, int64_t id, uint32_t *matched_blocks);
+/* scheduler.step(), src/engine.rs:418: every running sequence gets one more
+ * slot and a placeholder token; sequences are preempted from the back of
+ * running (blocks released, back to the front of waiting) while the pool is
+ * empty. */
+int rvkv_sched_step(rvkv_sched *s, uint32_t *n_preempted);
+/* Copy-on-write pairs created by step() since the last call (no
+ * counterpart in the reference, which never shares a written block): if n
+ * > cap nothing is copied and n is returned; run rvkv_copy_blocks on them
+ * before the forward that writes the new slots. */
+uint32_t rvkv_sched_take_cow(rvkv_sched *s, uint32_t *src, uint32_t *dst,
+                             uint32_t cap);
+/* scheduler.finish_sequence(seq) (src/engine.rs:510) and
+ * sequences.remove(seq) (src/engine.rs:513); remove also finishes. */
+int rvkv_sched_finish(rvkv_sched *s, int64_t id);
+int rvkv_sched_remove(rvkv_sched *s, int64_t id);
+/* A sequence sharing all of `parent`'s blocks (parallel sampling); a write
+ * into a shared last block copies it first (see take_cow). No counterpart
+ * in the reference engine. */
+int64_t rvkv_sched_fork(rvkv_sched *s, int64_t parent);
+/* block_table.num_tokens() / blocks() / logical_to_physical(pos) and
+ * token_ids, src/engine.rs:372-382, 426-447 */
+uint32_t rvkv_sched_num_tokens(const rvkv_sched *s, int64_t id);
+uint32_t rvkv_sched_num_blocks(const rvkv_sched *s, int64_t id);
+uint32_t rvkv_sched_table(const rvkv_sched *s, int64_t id, uint32_t *out,
+                          uint32_t cap);
+int rvkv_sched_slot(const rvkv_sched *s, int64_t id, uint32_t pos,
+                    uint32_t *block, uint32_t *offset);
+uint32_t rvkv_sched_tokens(const rvkv_sched *s, int64_t id, int32_t *out,
+                           uint32_t cap);
+/* Replaces token_ids (the engine's fix-ups, src/engine.rs:424-437); tokens
+ * that already hold K/V must stay as they are. */
+int rvkv_sched_set_tokens(rvkv_sched *s, int64_t id, const int32_t *tokens,
+                          uint32_t n);
+uint32_t rvkv_sched_refcount(const rvkv_sched *s, uint32_t block);
+
 #ifdef __cplusplus
 }
 #endif

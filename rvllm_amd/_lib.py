@@ -68,6 +68,32 @@ SIGNATURES = {
     "rvkv_bm_num_blocks": (_u32, [_P, _i64]),
     "rvkv_bm_refcount": (_u32, [_P, _u32]),
     "rvkv_bm_table": (_int, [_P, _i64, _pu32, _u32]),
+    "rvkv_sched_last_error": (ctypes.c_char_p, []),
+    "rvkv_sched_create": (_P, [_u32, _u32]),
+    "rvkv_sched_destroy": (None, [_P]),
+    "rvkv_sched_add_request": (_i64, [_P, _P, _u32]),
+    "rvkv_sched_available": (_u32, [_P]),
+    "rvkv_sched_total_allocs": (_u64, [_P]),
+    "rvkv_sched_metrics": (None, [_P, _P, _P, _P]),
+    "rvkv_sched_num_waiting": (_u32, [_P]),
+    "rvkv_sched_num_running": (_u32, [_P]),
+    "rvkv_sched_waiting": (_u32, [_P, _P, _u32]),
+    "rvkv_sched_running": (_u32, [_P, _P, _u32]),
+    "rvkv_sched_has_seq": (_int, [_P, _i64]),
+    "rvkv_sched_match_prefix": (_u32, [_P, _P, _u32, _P, _u32]),
+    "rvkv_sched_prefill": (_int, [_P, _i64, _pu32]),
+    "rvkv_sched_step": (_int, [_P, _pu32]),
+    "rvkv_sched_take_cow": (_u32, [_P, _P, _P, _u32]),
+    "rvkv_sched_finish": (_int, [_P, _i64]),
+    "rvkv_sched_remove": (_int, [_P, _i64]),
+    "rvkv_sched_fork": (_i64, [_P, _i64]),
+    "rvkv_sched_num_tokens": (_u32, [_P, _i64]),
+    "rvkv_sched_num_blocks": (_u32, [_P, _i64]),
+    "rvkv_sched_table": (_u32, [_P, _i64, _P, _u32]),
+    "rvkv_sched_slot": (_int, [_P, _i64, _u32, _pu32, _pu32]),
+    "rvkv_sched_tokens": (_u32, [_P, _i64, _P, _u32]),
+    "rvkv_sched_set_tokens": (_int, [_P, _i64, _P, _u32]),
+    "rvkv_sched_refcount": (_u32, [_P, _u32]),
 }
 
 

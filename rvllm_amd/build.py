@@ -18,6 +18,7 @@ SOURCES = [
     os.path.join(HERE, "csrc", "rvkv.hip"),
     os.path.join(HERE, "csrc", "prefill.hip"),
     os.path.join(HERE, "csrc", "block_manager.cpp"),
+    os.path.join(HERE, "csrc", "scheduler.cpp"),
 ]
 
 # Packed-FP32 instructions are kept out of generated code on purpose.
