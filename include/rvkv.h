@@ -331,6 +331,15 @@ uint32_t rvkv_bm_refcount(const rvkv_bm *bm, uint32_t block);
 int rvkv_bm_table(const rvkv_bm *bm, int64_t seq, uint32_t *table,
                   uint32_t cap);
 
+/* ---- next row (f)4: greedy token pick on the GPU --------------------------
+ * out[r] = index of the maximum of logits[r * row_len ...] (f32, device):
+ * ties go to the lowest index, NaN is ignored, a row with nothing above
+ * -inf gives 0 - the greedy scan of Sampler::sample_slice
+ * (src/sampler.rs:64-75) that rvllm's CUDA argmax kernel reproduces
+ * (argmax_wrapper, src/cuda/ops.rs:516-550). Asynchronous on `stream`. */
+int rvkv_argmax(const float *logits, uint32_t rows, uint32_t row_len,
+                uint32_t *out, rvkv_stream stream);
+
 /* ---- next row (f)3: continuous-batching scheduler with prefix cache -----
  * The contract rvllm's engine uses from the kv-cache-scheduler crate (0.2.0,
  * not vendored; used at src/engine.rs:351-539): a refcounted block pool

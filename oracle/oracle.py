@@ -352,3 +352,13 @@ def attn_prep(cache: KvCache, q_in, k_in, v_in, cos, sin, slot_block,
     if rc:
         raise ValueError("attn_prep: slot out of range")
     return q_out
+
+
+def argmax_rows(logits) -> np.ndarray:
+    """Greedy token per row as Sampler::sample_slice scans it
+    (src/sampler.rs:64-75): first maximum wins, NaN is never a maximum, a
+    row with nothing above -inf gives 0 (numpy's argmax returns the first
+    occurrence, and index 0 for an all -inf row)."""
+    x = np.asarray(logits, np.float32)
+    x = np.where(np.isnan(x), -np.inf, x)
+    return np.argmax(x, axis=-1).astype(np.uint32)

@@ -17,6 +17,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 SOURCES = [
     os.path.join(HERE, "csrc", "rvkv.hip"),
     os.path.join(HERE, "csrc", "prefill.hip"),
+    os.path.join(HERE, "csrc", "argmax.hip"),
     os.path.join(HERE, "csrc", "block_manager.cpp"),
     os.path.join(HERE, "csrc", "scheduler.cpp"),
 ]

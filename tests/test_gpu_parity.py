@@ -986,3 +986,90 @@ def test_prefill_rejections():
     with pytest.raises(RvkvError, match="paged_prefill: n_heads"):
         st.paged_prefill(0, torch.zeros(1, 2, 3, 64, device="cuda"),
                          dev_u32([[0]]), dev_u32([0]), dev_u32([2]))
+
+
+# ---- (f)4 argmax and the engine over the paged KV path -------------------------
+def test_argmax_kat_and_random():
+    """rvkv_argmax: the reference KAT (src/cuda/ops.rs:1447-1477) and random
+    rows with ties/NaN at vocab sizes that are and are not multiples of 4."""
+    from rvllm_amd import _lib
+    import ctypes
+    from tests.test_oracle import argmax_kat_rows
+    L = _lib.load()
+
+    def gpu_argmax(x):
+        t = torch.from_numpy(np.ascontiguousarray(x, np.float32)).cuda()
+        out = torch.empty(x.shape[0], dtype=torch.int32, device="cuda")
+        _lib.check(L.rvkv_argmax(ctypes.c_void_p(t.data_ptr()), x.shape[0],
+                                 x.shape[1], ctypes.c_void_p(out.data_ptr()),
+                                 ctypes.c_void_p(
+                                     torch.cuda.current_stream().cuda_stream)))
+        torch.cuda.synchronize()
+        return out.cpu().numpy().view(np.uint32).tolist()
+
+    assert gpu_argmax(argmax_kat_rows()) == [1, 1, 0, 599]
+    rng = np.random.default_rng(31)
+    for V in (1, 7, 1000, 32000, 151936):
+        x = rng.integers(-5, 6, (33, V)).astype(np.float32)
+        x[rng.random(x.shape) < 0.05] = np.nan
+        x[3] = -np.inf
+        assert gpu_argmax(x) == orc.argmax_rows(x).tolist(), V
+
+
+def _engine_pair(cfg, num_blocks, bs):
+    from rvllm_amd.attn_model import HipBackend, init_weights
+    from tests.engine_backends import LockstepBackend, OracleBackend
+    w = init_weights(cfg)
+    return LockstepBackend(HipBackend(cfg, w, num_blocks, bs),
+                           OracleBackend(cfg, w, num_blocks, bs))
+
+
+@pytest.mark.parametrize("variant", ["plain", "qwen3", "qwen25"])
+def test_engine_lockstep_with_oracle(variant):
+    """The engine over the native scheduler with the GPU backend: every
+    prefill and decode forward (attn_prep + append, paged prefill, paged
+    decode, argmax) agrees with the oracle's computation of the same model;
+    requests share prefixes (prefix-cache hits skip their tokens) and the
+    pool is small enough to force preemption and re-prefill."""
+    from rvllm_amd.attn_model import AttnModelConfig
+    from rvllm_amd.engine import Engine, EngineConfig, Request
+    cfg = AttnModelConfig(
+        vocab=512, hidden=128, n_layers=2, n_heads=8, n_kv_heads=2,
+        head_dim=64, qkv_bias=variant == "qwen25",
+        qk_norm=variant == "qwen3", context_length=512)
+    be = _engine_pair(cfg, num_blocks=14, bs=16)  # tight: preempts twice
+    eng = Engine(be, EngineConfig(block_size=16, num_blocks=14,
+                                  max_running=6))
+    rng = np.random.default_rng(5)
+    shared = rng.integers(0, 512, 40).tolist()
+    ids = []
+    for i in range(7):
+        prompt = (shared if i % 2 == 0 else []) + rng.integers(
+            0, 512, int(rng.integers(3, 30))).tolist()
+        ids.append(eng.add_request(Request(prompt, int(rng.integers(8, 40)))))
+    while eng.has_work():
+        eng.step()
+    hits, total, pre = eng.scheduler.metrics()
+    print(f"forwards {be.calls} worst/tol {be.worst:.3f} hits {hits}/{total} "
+          f"preemptions {pre} close {be.close_calls}")
+    assert hits > 0 and pre > 0 and be.calls > 20
+    assert eng.scheduler.available() == 14
+
+
+def test_engine_fork_copy_on_write_on_gpu():
+    """A forked sequence shares its parent's half-full tail block; the
+    first step copies it (rvkv_copy_blocks) before either writes, and both
+    continue to agree with the oracle."""
+    from rvllm_amd.attn_model import AttnModelConfig
+    from rvllm_amd.engine import Engine, EngineConfig, Request
+    cfg = AttnModelConfig(vocab=256, hidden=128, n_layers=2, n_heads=4,
+                          n_kv_heads=2, head_dim=64, context_length=256)
+    be = _engine_pair(cfg, num_blocks=16, bs=8)
+    eng = Engine(be, EngineConfig(block_size=8, num_blocks=16))
+    a = eng.add_request(Request(list(range(20, 33)), 6))
+    eng.step()  # prefill + one decode
+    b = eng.scheduler.fork(a)
+    eng.seqs[b] = type(eng.seqs[a])(**vars(eng.seqs[a]))
+    while eng.has_work():
+        eng.step()
+    assert be.calls > 5

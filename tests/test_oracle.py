@@ -457,3 +457,35 @@ def test_paged_prefill_f64_q_len_one_is_decode():
                                   window=w)
         b = orc.paged_decode_f64(cache, q[:, 0], tables, 10, ctx, window=w)
         assert np.array_equal(a[:, 0], b)
+
+
+# ---- (f)4: greedy argmax -------------------------------------------------------
+def argmax_kat_rows():
+    """The rows of argmax_matches_hand_computed (src/cuda/ops.rs:1447-1477):
+    unique max; tie between 1 and 3 with a NaN; all -inf; max at 599."""
+    n = 600
+    d = np.zeros((4, n), np.float32)
+    d[0, 0], d[0, 1], d[0, 2] = 1.0, 5.0, -2.0
+    d[1, 0], d[1, 1], d[1, 3] = np.nan, 3.0, 3.0
+    d[2, :] = -np.inf
+    d[3, 599] = 9.0
+    d[0, 4:] = -1.0
+    d[1, 4:] = -1.0
+    return d
+
+
+def test_argmax_kat():
+    assert orc.argmax_rows(argmax_kat_rows()).tolist() == [1, 1, 0, 599]
+
+
+def test_argmax_matches_a_python_scan():
+    rng = np.random.default_rng(30)
+    x = rng.integers(-3, 4, (50, 37)).astype(np.float32)  # many ties
+    x[rng.random(x.shape) < 0.1] = np.nan
+    x[7] = np.nan
+    for r, row in enumerate(x):
+        best, bv = 0, -np.inf
+        for i, v in enumerate(row):
+            if v > bv:
+                best, bv = i, v
+        assert orc.argmax_rows(x)[r] == best
