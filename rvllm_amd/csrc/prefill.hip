@@ -198,9 +198,9 @@ __global__ void __launch_bounds__(256, HD <= 64 ? 3 : 2)
   constexpr int CHV = VP >= 256 ? VP / 256 : 1;   // per thread
   const bool v_lane = VP >= 256 || tid < VP;      // all but hd 32
 
-  // Are all the blocks this workgroup reads valid? One scan of its table
-  // range; then the per-tile work needs no per-key flags (key < row_hi
-  // already implies key < k_end).
+  // Are all the blocks holding keys below k_end valid? One scan of its
+  // table range; then the masks need no per-key flags (key < row_hi already
+  // implies key < k_end). Loads still check every block id themselves.
   bool all_ok = true;
   if (k_begin < k_end) {
     int bad = 0;
@@ -248,7 +248,9 @@ __global__ void __launch_bounds__(256, HD <= 64 ? 3 : 2)
     vbits = 0;
 #pragma unroll
     for (int i = 0; i < CHK; ++i) {
-      const bool okb = all_ok || kid[i] < a.num_blocks;
+      // The address checks its own block id: all_ok covers only the blocks
+      // of keys below k_end, and the last tile may reach past them.
+      const bool okb = kid[i] < a.num_blocks;
       kbits |= (uint32_t)(okb && kt + k_key[i] < k_end) << i;
       kr[i] = *reinterpret_cast<const u32x4 *>(
           kbase + (uint64_t)(okb ? kid[i] : 0u) * blk_bytes + t_off +
@@ -256,7 +258,7 @@ __global__ void __launch_bounds__(256, HD <= 64 ? 3 : 2)
     }
 #pragma unroll
     for (int j = 0; j < CHV; ++j) {
-      const bool okb = all_ok || vid[j] < a.num_blocks;
+      const bool okb = vid[j] < a.num_blocks;
       const uint32_t tok = kt + v_key[j];
       vbits |= (uint32_t)(okb && tok < k_end) << (2 * j);
       vbits |= (uint32_t)(okb && tok + 1 < k_end) << (2 * j + 1);
