@@ -235,7 +235,7 @@ int rvkv_attn_prep(rvkv_pool *pool, uint32_t layer, const float *q_in,
  * block_tables [batch, max_blocks] u32; pos_offset, read_num_tokens [batch]
  * u32 (all device). Table entries >= num_blocks mark keys unreadable (they
  * get probability 0); a row that sees no key gets zeros. head_dim in {32,
- * 64, 128}; block_size a power of two >= 8. Computed on the matrix cores in
+ * 64, 128, 256}; block_size a power of two >= 8. Computed on the matrix cores in
  * f16 with f32 accumulation. Allocates nothing. */
 int rvkv_paged_prefill(rvkv_pool *pool, uint32_t layer, const float *q,
                        const uint32_t *block_tables,

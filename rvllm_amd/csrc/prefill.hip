@@ -47,7 +47,12 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
-constexpr int kBN = 64;   // keys per tile
+// Keys per tile: 64, or 32 at head_dim 256 (one 32-key sub-tile keeps the
+// S accumulators and the tile's load registers within the register file).
+template <int HD>
+constexpr int tile_keys() {
+  return HD >= 256 ? 32 : 64;
+}
 constexpr int kWaveRows = 32;
 constexpr int kWaves = 4;
 constexpr int kBM = kWaveRows * kWaves;  // query rows per workgroup
@@ -71,11 +76,12 @@ struct PrefillArgs {
 
 template <int HD>
 struct Lds {
-  static constexpr int KS = HD + 8;   // K row stride in halves (16 B pad)
-  static constexpr int VS = kBN + 8;  // Vt row stride in halves
-  static constexpr size_t k_bytes = (size_t)kBN * KS * 2;
+  static constexpr int BN = tile_keys<HD>();
+  static constexpr int KS = HD + 8;  // K row stride in halves (16 B pad)
+  static constexpr int VS = BN + 8;  // Vt row stride in halves
+  static constexpr size_t k_bytes = (size_t)BN * KS * 2;
   static constexpr size_t v_bytes = (size_t)HD * VS * 2;
-  static constexpr size_t bytes = k_bytes + v_bytes + kBN;  // + key flags
+  static constexpr size_t bytes = k_bytes + v_bytes + BN;  // + key flags
 };
 
 __device__ __forceinline__ uint32_t lo_bound(uint32_t p, int32_t window) {
@@ -87,14 +93,16 @@ __device__ __forceinline__ uint32_t lo_bound(uint32_t p, int32_t window) {
 // O accumulators stay in arch VGPRs), three below; a second resident
 // workgroup overlaps its softmax with the other's matrix work.
 template <int HD>
-__global__ void __launch_bounds__(256, HD <= 64 ? 3 : 2)
+__global__ void __launch_bounds__(256, HD <= 64 ? 3 : (HD <= 128 ? 2 : 1))
     prefill_kernel(PrefillArgs a) {
-  constexpr int KS = Lds<HD>::KS, VS = Lds<HD>::VS;
+  constexpr int KS = Lds<HD>::KS, VS = Lds<HD>::VS, BN = Lds<HD>::BN;
+  constexpr int NT = BN / 32;                 // 32-key sub-tiles per tile
+  constexpr int NPR = BN / 2;                 // key pairs per tile
   constexpr int KC = HD / 16;                 // MFMA k-steps of S
   constexpr int DT = HD / 32;                 // 32-row tiles of O^T
   constexpr int CPR = HD / 8;                 // 16-byte chunks per key row
-  constexpr int CHK = kBN * CPR / 256;        // K chunks per thread per tile
-  static_assert(CHK >= 1 && kBN * CPR % 256 == 0, "tile/thread mismatch");
+  constexpr int CHK = BN * CPR / 256;         // K chunks per thread per tile
+  static_assert(CHK >= 1 && BN * CPR % 256 == 0, "tile/thread mismatch");
   extern __shared__ __align__(16) unsigned char smem[];
   uint16_t *ks = reinterpret_cast<uint16_t *>(smem);
   uint16_t *vt = reinterpret_cast<uint16_t *>(smem + Lds<HD>::k_bytes);
@@ -129,7 +137,7 @@ __global__ void __launch_bounds__(256, HD <= 64 ? 3 : 2)
   const uint32_t r_last = min(r_first + kBM, a.rows) - 1u;
   const uint32_t k_end = min(ctx, off + r_last / a.group + 1u);
   const uint32_t k_begin =
-      lo_bound(off + r_first / a.group, a.window) & ~(uint32_t)(kBN - 1);
+      lo_bound(off + r_first / a.group, a.window) & ~(uint32_t)(BN - 1);
 
   // The same for this wave's 32 rows (wave-uniform).
   const uint32_t rw0 = r_first + wave * kWaveRows;
@@ -187,14 +195,14 @@ __global__ void __launch_bounds__(256, HD <= 64 ? 3 : 2)
   // Tile loads. K goes to LDS row-major, so its 16-byte chunks are taken in
   // row order (chunk c: key c / CPR, column chunk c % CPR: whole rows per
   // lane group, coalesced). V goes to LDS transposed, so its chunks are
-  // taken in key-pair order (pair c % 32, column chunk c / 32): a lane loads
-  // keys 2p and 2p+1 of one column chunk and writes 8 dwords Vt[d][2p..2p+1];
-  // the 32 lanes of a half-wave write 32 consecutive dwords of one Vt row,
-  // one per bank. Block ids are fetched one tile ahead so a tile's loads
+  // taken in key-pair order (pair c % (BN/2), column chunk c / (BN/2)): a
+  // lane loads keys 2p and 2p+1 of one column chunk and writes 8 dwords
+  // Vt[d][2p..2p+1]; consecutive lanes write consecutive dwords of one Vt
+  // row (with BN 64, a half-wave covers the 32 banks once). Block ids are fetched one tile ahead so a tile's loads
   // issue back to back; loads are unconditional (invalid ones read block 0)
   // and invalid V is zeroed at the LDS store, because masked keys get
   // probability 0 and 0 * (stale V) must stay 0.
-  constexpr int VP = kBN / 2 * CPR;               // V chunk pairs per tile
+  constexpr int VP = NPR * CPR;                   // V chunk pairs per tile
   constexpr int CHV = VP >= 256 ? VP / 256 : 1;   // per thread
   const bool v_lane = VP >= 256 || tid < VP;      // all but hd 32
 
@@ -210,10 +218,11 @@ __global__ void __launch_bounds__(256, HD <= 64 ? 3 : 2)
     all_ok = !__syncthreads_or(bad);
   }
 
-  // Per-lane constants: tiles start at multiples of 64, so a chunk's byte
-  // offset inside its (block, head) tile and its block index relative to
-  // the tile's first block are the same for every tile (for block_size >
-  // 64 the tile's own offset inside the block is added per tile).
+  // Per-lane constants: tiles start at multiples of the tile width BN, so
+  // a chunk's byte offset inside its (block, head) tile and its block index
+  // relative to the tile's first block are the same for every tile (for
+  // block_size > BN the tile's own offset inside the block is added per
+  // tile).
   uint32_t k_key[CHK], k_off[CHK], k_db[CHK];
 #pragma unroll
   for (int i = 0; i < CHK; ++i) {
@@ -226,8 +235,8 @@ __global__ void __launch_bounds__(256, HD <= 64 ? 3 : 2)
 #pragma unroll
   for (int j = 0; j < CHV; ++j) {
     const int c = tid + 256 * j;
-    v_key[j] = 2u * (uint32_t)(c % 32);
-    v_off[j] = ((v_key[j] & bs_mask) * HD + (c / 32) * 8) * 2;
+    v_key[j] = 2u * (uint32_t)(c % NPR);
+    v_off[j] = ((v_key[j] & bs_mask) * HD + (c / NPR) * 8) * 2;
     v_db[j] = v_key[j] >> a.bs_log2;
   }
   const uint64_t blk_bytes = a.block_stride * 2;
@@ -274,11 +283,11 @@ __global__ void __launch_bounds__(256, HD <= 64 ? 3 : 2)
   if (k_begin < k_end) {
     fetch_ids(k_begin);
     load(k_begin);
-    fetch_ids(k_begin + kBN);
+    fetch_ids(k_begin + BN);
   }
-  for (uint32_t kt = k_begin; kt < k_end; kt += kBN) {
+  for (uint32_t kt = k_begin; kt < k_end; kt += BN) {
     // Every key of the tile readable: all blocks valid, tile inside k_end.
-    const bool tile_ok = all_ok && kt + kBN <= k_end;
+    const bool tile_ok = all_ok && kt + BN <= k_end;
     __syncthreads();  // the previous tile is no longer read
 #pragma unroll
     for (int i = 0; i < CHK; ++i) {
@@ -292,7 +301,7 @@ __global__ void __launch_bounds__(256, HD <= 64 ? 3 : 2)
 #pragma unroll
       for (int j = 0; j < CHV; ++j) {
         const int c = tid + 256 * j;
-        const int pr = c % 32, dc = c / 32;
+        const int pr = c % NPR, dc = c / NPR;
         const uint32_t mask = tile_ok ? 0xffffffffu
                               : (((vbits >> (2 * j)) & 1u ? 0xffffu : 0u) |
                                  ((vbits >> (2 * j + 1)) & 1u ? 0xffff0000u
@@ -309,15 +318,15 @@ __global__ void __launch_bounds__(256, HD <= 64 ? 3 : 2)
       }
     }
     __syncthreads();
-    if (kt + kBN < k_end) {
-      load(kt + kBN);
-      fetch_ids(kt + 2 * kBN);
+    if (kt + BN < k_end) {
+      load(kt + BN);
+      fetch_ids(kt + 2 * BN);
     }
-    if (!(kt < w_end && kt + kBN > w_begin)) continue;  // nothing for this wave
+    if (!(kt < w_end && kt + BN > w_begin)) continue;  // nothing for this wave
 
-    f32x16 s[2];
+    f32x16 s[NT];
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < NT; ++t)
 #pragma unroll
       for (int j = 0; j < 16; ++j) s[t][j] = 0.f;
     // The two sub-tiles' accumulation chains alternate, so each MFMA's
@@ -325,7 +334,7 @@ __global__ void __launch_bounds__(256, HD <= 64 ? 3 : 2)
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc)
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
+      for (int t = 0; t < NT; ++t) {
         const half8 kf = *reinterpret_cast<const half8 *>(
             ks + (32 * t + sig) * KS + kc * 16 + hl * 8);
         s[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[kc], s[t], 0, 0,
@@ -336,15 +345,15 @@ __global__ void __launch_bounds__(256, HD <= 64 ? 3 : 2)
     // then the online softmax; register j of sub-tile t is key
     // kt + 32t + 16(j/8) + 8hl + j%8.
     float mx = kNegBig;
-    if (tile_ok && kt >= w_lo_max && kt + kBN <= w_hi_min) {
+    if (tile_ok && kt >= w_lo_max && kt + BN <= w_hi_min) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < NT; ++t)
 #pragma unroll
         for (int j = 0; j < 16; j += 2)
           mx = fmaxf(mx, fmaxf(s[t][j], s[t][j + 1]));
     } else {
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < NT; ++t)
 #pragma unroll
         for (int g8 = 0; g8 < 2; ++g8) {
           const uint32_t k0 = 32 * t + 16 * g8 + 8 * hl;
@@ -377,11 +386,11 @@ __global__ void __launch_bounds__(256, HD <= 64 ? 3 : 2)
 #pragma unroll
         for (int j = 0; j < 16; ++j) o[dt][j] *= alpha;
     }
-    half8 pb[2][2];
+    half8 pb[NT][2];
     float psum = 0.f;
     const h2 ones = h2{(_Float16)1.0f, (_Float16)1.0f};
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < NT; ++t)
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
 #pragma unroll
@@ -394,7 +403,7 @@ __global__ void __launch_bounds__(256, HD <= 64 ? 3 : 2)
       }
     l += psum;
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < NT; ++t)
 #pragma unroll
       for (int c = 0; c < 2; ++c)
 #pragma unroll
@@ -449,8 +458,8 @@ int rvkv_paged_prefill(rvkv_pool *pool, uint32_t layer, const float *q,
     return fail(RVKV_EINVAL, op,
                 "n_heads must be a positive multiple of n_kv_heads");
   const uint32_t hd = pool->head_dim, bs = pool->block_size;
-  if (hd != 32 && hd != 64 && hd != 128)
-    return fail(RVKV_EUNSUPPORTED, op, "head_dim must be 32, 64 or 128");
+  if (hd != 32 && hd != 64 && hd != 128 && hd != 256)
+    return fail(RVKV_EUNSUPPORTED, op, "head_dim must be 32, 64, 128 or 256");
   if (bs < 8 || (bs & (bs - 1)) != 0)
     return fail(RVKV_EUNSUPPORTED, op,
                 "block_size must be a power of two >= 8");
@@ -495,7 +504,8 @@ int rvkv_paged_prefill(rvkv_pool *pool, uint32_t layer, const float *q,
   switch (hd) {
     case 32: launch_prefill<32>(a, grid, pool->stream); break;
     case 64: launch_prefill<64>(a, grid, pool->stream); break;
-    default: launch_prefill<128>(a, grid, pool->stream); break;
+    case 128: launch_prefill<128>(a, grid, pool->stream); break;
+    default: launch_prefill<256>(a, grid, pool->stream); break;
   }
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? RVKV_OK : hip_fail(op, e);

@@ -910,7 +910,8 @@ def _prefill_case(seed, B, Q, nkv, G, hd, bs, window, ragged=True,
 
 @pytest.mark.parametrize("G,hd,bs", [(1, 64, 16), (2, 128, 16), (4, 64, 32),
                                      (7, 64, 32), (8, 128, 8), (3, 32, 16),
-                                     (16, 64, 16)])
+                                     (16, 64, 16), (4, 256, 16), (1, 256, 8),
+                                     (2, 256, 64)])
 def test_prefill_chunked_vs_oracle(G, hd, bs):
     """Several query-row tiles per (sequence, KV head) (G * Q > 128),
     chunk offsets that are not tile or block aligned, ragged read counts."""
@@ -974,9 +975,9 @@ def test_prefill_edges():
 
 
 def test_prefill_rejections():
-    st = HipKvStorage(1, 4, 16, 1, 256)
+    st = HipKvStorage(1, 4, 16, 1, 48)
     with pytest.raises(RvkvError, match="paged_prefill: head_dim"):
-        st.paged_prefill(0, torch.zeros(1, 2, 2, 256, device="cuda"),
+        st.paged_prefill(0, torch.zeros(1, 2, 2, 48, device="cuda"),
                          dev_u32([[0]]), dev_u32([0]), dev_u32([2]))
     st = HipKvStorage(1, 4, 4, 1, 64)
     with pytest.raises(RvkvError, match="paged_prefill: block_size"):
