@@ -186,6 +186,15 @@ def cpu_baseline(orc, W, st, db, budget_s):
         t_total += time.perf_counter() - t0
         reps += 1
     per_layer = t_total / reps
+    # The same work on one thread (a short sample).
+    reps1, t1 = 0, 0.0
+    while reps1 < 1 or (t1 < min(3.0, budget_s / 4) and reps1 < 100):
+        t0 = time.perf_counter()
+        orc.decode_step(cache, db.slot_block, db.slot_off, nk, nv, idx,
+                        db.max_blocks, db.ctx_lens, q, n_threads=1)
+        t1 += time.perf_counter() - t0
+        reps1 += 1
+    per_layer1 = t1 / reps1
     layer_bytes = W.decode_bytes(db) + W.append_bytes(db.batch, c)
     return {
         "value": round(layer_bytes / per_layer / 1e9, 3),
@@ -199,6 +208,11 @@ def cpu_baseline(orc, W, st, db, budget_s):
                    f"tok/s extrapolated to {c.n_layers} layers"),
         "tok_per_s": round(db.batch / (per_layer * c.n_layers), 2),
         "ms_per_layer": round(per_layer * 1e3, 3),
+        "single_thread": {
+            "value": round(layer_bytes / per_layer1 / 1e9, 3),
+            "ms_per_layer": round(per_layer1 * 1e3, 3),
+            "repetitions": reps1,
+        },
     }
 
 
@@ -524,6 +538,7 @@ def run_churn(args, torch, W):
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(dt * 1e3, 4),
+        "ms_per_step_median": round(step_median_ms, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -664,12 +679,19 @@ def main():
 
     for _ in range(args.warmup):
         run()
+    # Step events (recording does not synchronise) give the median step.
+    evs = [torch.cuda.Event(enable_timing=True)
+           for _ in range(args.steps + 1)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    evs[0].record()
+    for i in range(args.steps):
         run()
+        evs[i + 1].record()
     torch.cuda.synchronize()
     dt = (time.perf_counter() - t0) / args.steps
+    step_median_ms = float(np.median([evs[i].elapsed_time(evs[i + 1])
+                                      for i in range(args.steps)]))
 
     # Per-launch decode duration: HIP events on the pool's stream (torch's
     # current stream) around `steps` rounds of back-to-back decode launches
@@ -701,6 +723,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(dt * 1e3, 4),
+        "ms_per_step_median": round(step_median_ms, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

@@ -36,6 +36,7 @@
 #include "pool.h"
 
 #include <cmath>
+#include <cstdlib>
 
 using rvkv_detail::fail;
 using rvkv_detail::hip_fail;
@@ -53,9 +54,7 @@ template <int HD>
 constexpr int tile_keys() {
   return HD >= 256 ? 32 : 64;
 }
-constexpr int kWaveRows = 32;
-constexpr int kWaves = 4;
-constexpr int kBM = kWaveRows * kWaves;  // query rows per workgroup
+constexpr int kWaveRows = 32;  // query rows per wave
 constexpr float kNegBig = -1.0e30f;      // finite start value of the row max
 
 struct PrefillArgs {
@@ -69,7 +68,7 @@ struct PrefillArgs {
   uint32_t q_len, max_blocks, num_blocks, n_heads, group, bs_log2;
   uint32_t batch, n_kv;
   uint32_t rows;     // group * q_len rows per (sequence, KV head)
-  uint32_t n_tiles;  // ceil(rows / kBM)
+  uint32_t n_tiles;  // ceil(rows / (32 * waves per workgroup))
   float qscale;      // scale * log2(e)
   int32_t window;
 };
@@ -84,25 +83,41 @@ struct Lds {
   static constexpr size_t bytes = k_bytes + v_bytes + BN;  // + key flags
 };
 
+// max(a, b, c) in one v_max3_f32. Written as an instruction because the
+// IEEE-mode fmaxf would first quiet each (never NaN here) MFMA result with
+// an extra v_max x, x.
+__device__ __forceinline__ float vmax3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
 __device__ __forceinline__ uint32_t lo_bound(uint32_t p, int32_t window) {
   return (window > 0 && p + 1 > (uint32_t)window) ? p + 1 - (uint32_t)window
                                                   : 0u;
 }
 
-// Two workgroups per CU at head_dim 128 (<= 256 registers a lane, so the
-// O accumulators stay in arch VGPRs), three below; a second resident
-// workgroup overlaps its softmax with the other's matrix work.
-template <int HD>
-__global__ void __launch_bounds__(256, HD <= 64 ? 3 : (HD <= 128 ? 2 : 1))
+// WAVES wave64s per workgroup (4 or 8, 32 query rows each); the K/V tile
+// loads and LDS stores are shared among them, so more waves halve each
+// wave's share of that work. Registers are bounded for 8 resident waves per
+// CU at head_dim 128 (<= 256 a lane, so the O accumulators stay in arch
+// VGPRs), 12 below and 4 at 256: two or more waves per SIMD overlap one's
+// softmax with another's matrix work.
+template <int HD, int WAVES>
+__global__ void __launch_bounds__(64 * WAVES,
+                                  (HD <= 64 ? 12 : (HD <= 128 ? 8 : 4)) /
+                                      WAVES)
     prefill_kernel(PrefillArgs a) {
+  constexpr int NTH = 64 * WAVES;  // threads per workgroup
+  constexpr int kBM = kWaveRows * WAVES;
   constexpr int KS = Lds<HD>::KS, VS = Lds<HD>::VS, BN = Lds<HD>::BN;
   constexpr int NT = BN / 32;                 // 32-key sub-tiles per tile
   constexpr int NPR = BN / 2;                 // key pairs per tile
   constexpr int KC = HD / 16;                 // MFMA k-steps of S
   constexpr int DT = HD / 32;                 // 32-row tiles of O^T
   constexpr int CPR = HD / 8;                 // 16-byte chunks per key row
-  constexpr int CHK = BN * CPR / 256;         // K chunks per thread per tile
-  static_assert(CHK >= 1 && BN * CPR % 256 == 0, "tile/thread mismatch");
+  constexpr int CHK = BN * CPR / NTH;         // K chunks per thread per tile
+  static_assert(CHK >= 1 && BN * CPR % NTH == 0, "tile/thread mismatch");
   extern __shared__ __align__(16) unsigned char smem[];
   uint16_t *ks = reinterpret_cast<uint16_t *>(smem);
   uint16_t *vt = reinterpret_cast<uint16_t *>(smem + Lds<HD>::k_bytes);
@@ -203,8 +218,8 @@ __global__ void __launch_bounds__(256, HD <= 64 ? 3 : (HD <= 128 ? 2 : 1))
   // and invalid V is zeroed at the LDS store, because masked keys get
   // probability 0 and 0 * (stale V) must stay 0.
   constexpr int VP = NPR * CPR;                   // V chunk pairs per tile
-  constexpr int CHV = VP >= 256 ? VP / 256 : 1;   // per thread
-  const bool v_lane = VP >= 256 || tid < VP;      // all but hd 32
+  constexpr int CHV = VP >= NTH ? VP / NTH : 1;   // per thread
+  const bool v_lane = VP >= NTH || tid < VP;
 
   // Are all the blocks holding keys below k_end valid? One scan of its
   // table range; then the masks need no per-key flags (key < row_hi already
@@ -213,7 +228,7 @@ __global__ void __launch_bounds__(256, HD <= 64 ? 3 : (HD <= 128 ? 2 : 1))
   if (k_begin < k_end) {
     int bad = 0;
     for (uint32_t i = (k_begin >> a.bs_log2) + tid;
-         i <= ((k_end - 1u) >> a.bs_log2); i += 256)
+         i <= ((k_end - 1u) >> a.bs_log2); i += NTH)
       bad |= table[i] >= a.num_blocks;
     all_ok = !__syncthreads_or(bad);
   }
@@ -226,7 +241,7 @@ __global__ void __launch_bounds__(256, HD <= 64 ? 3 : (HD <= 128 ? 2 : 1))
   uint32_t k_key[CHK], k_off[CHK], k_db[CHK];
 #pragma unroll
   for (int i = 0; i < CHK; ++i) {
-    const int c = tid + 256 * i;
+    const int c = tid + NTH * i;
     k_key[i] = (uint32_t)(c / CPR);
     k_off[i] = ((k_key[i] & bs_mask) * HD + (c % CPR) * 8) * 2;
     k_db[i] = k_key[i] >> a.bs_log2;
@@ -234,7 +249,7 @@ __global__ void __launch_bounds__(256, HD <= 64 ? 3 : (HD <= 128 ? 2 : 1))
   uint32_t v_key[CHV], v_off[CHV], v_db[CHV];
 #pragma unroll
   for (int j = 0; j < CHV; ++j) {
-    const int c = tid + 256 * j;
+    const int c = tid + NTH * j;
     v_key[j] = 2u * (uint32_t)(c % NPR);
     v_off[j] = ((v_key[j] & bs_mask) * HD + (c / NPR) * 8) * 2;
     v_db[j] = v_key[j] >> a.bs_log2;
@@ -291,7 +306,7 @@ __global__ void __launch_bounds__(256, HD <= 64 ? 3 : (HD <= 128 ? 2 : 1))
     __syncthreads();  // the previous tile is no longer read
 #pragma unroll
     for (int i = 0; i < CHK; ++i) {
-      const int c = tid + 256 * i;
+      const int c = tid + NTH * i;
       const int key = c / CPR, dc = c % CPR;
       *reinterpret_cast<u32x4 *>(ks + key * KS + dc * 8) = kr[i];
       // Every loader of a key writes the same flag.
@@ -300,20 +315,31 @@ __global__ void __launch_bounds__(256, HD <= 64 ? 3 : (HD <= 128 ? 2 : 1))
     if (v_lane) {
 #pragma unroll
       for (int j = 0; j < CHV; ++j) {
-        const int c = tid + 256 * j;
+        const int c = tid + NTH * j;
         const int pr = c % NPR, dc = c / NPR;
-        const uint32_t mask = tile_ok ? 0xffffffffu
-                              : (((vbits >> (2 * j)) & 1u ? 0xffffu : 0u) |
-                                 ((vbits >> (2 * j + 1)) & 1u ? 0xffff0000u
-                                                              : 0u));
         uint32_t *row = reinterpret_cast<uint32_t *>(vt + dc * 8 * VS) + pr;
+        if (tile_ok) {  // uniform: every key of the tile is readable
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          // d = 8dc + 2e: low halves of both keys; d + 1: high halves.
-          row[(2 * e) * (VS / 2)] =
-              __builtin_amdgcn_perm(vr1[j][e], vr0[j][e], 0x05040100u) & mask;
-          row[(2 * e + 1) * (VS / 2)] =
-              __builtin_amdgcn_perm(vr1[j][e], vr0[j][e], 0x07060302u) & mask;
+          for (int e = 0; e < 4; ++e) {
+            // d = 8dc + 2e: low halves of both keys; d + 1: high halves.
+            row[(2 * e) * (VS / 2)] =
+                __builtin_amdgcn_perm(vr1[j][e], vr0[j][e], 0x05040100u);
+            row[(2 * e + 1) * (VS / 2)] =
+                __builtin_amdgcn_perm(vr1[j][e], vr0[j][e], 0x07060302u);
+          }
+        } else {
+          const uint32_t mask =
+              ((vbits >> (2 * j)) & 1u ? 0xffffu : 0u) |
+              ((vbits >> (2 * j + 1)) & 1u ? 0xffff0000u : 0u);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            row[(2 * e) * (VS / 2)] =
+                __builtin_amdgcn_perm(vr1[j][e], vr0[j][e], 0x05040100u) &
+                mask;
+            row[(2 * e + 1) * (VS / 2)] =
+                __builtin_amdgcn_perm(vr1[j][e], vr0[j][e], 0x07060302u) &
+                mask;
+          }
         }
       }
     }
@@ -349,8 +375,7 @@ __global__ void __launch_bounds__(256, HD <= 64 ? 3 : (HD <= 128 ? 2 : 1))
 #pragma unroll
       for (int t = 0; t < NT; ++t)
 #pragma unroll
-        for (int j = 0; j < 16; j += 2)
-          mx = fmaxf(mx, fmaxf(s[t][j], s[t][j + 1]));
+        for (int j = 0; j < 16; j += 2) mx = vmax3(mx, s[t][j], s[t][j + 1]);
     } else {
 #pragma unroll
       for (int t = 0; t < NT; ++t)
@@ -429,10 +454,22 @@ __global__ void __launch_bounds__(256, HD <= 64 ? 3 : (HD <= 128 ? 2 : 1))
   }
 }
 
-template <int HD>
+template <int HD, int WAVES>
 void launch_prefill(const PrefillArgs &a, dim3 grid, hipStream_t st) {
-  hipLaunchKernelGGL(prefill_kernel<HD>, grid, dim3(256), Lds<HD>::bytes, st,
-                     a);
+  hipLaunchKernelGGL((prefill_kernel<HD, WAVES>), grid, dim3(64 * WAVES),
+                     Lds<HD>::bytes, st, a);
+}
+
+// Waves per workgroup: 8 at head_dim 128 (measured ~5 % faster than 4);
+// 4 at 64, where 8-wave workgroups would cost the third resident wave per
+// SIMD (measured ~7 % slower), and at 32 and 256. RVKV_PREFILL_WAVES=4|8
+// overrides (8 only where a K/V tile fills 512 threads: 64, 128).
+uint32_t prefill_waves(uint32_t hd) {
+  static const char *env = getenv("RVKV_PREFILL_WAVES");
+  static const uint32_t forced = env ? (uint32_t)atoi(env) : 0u;
+  const bool can8 = hd == 64 || hd == 128;
+  if (forced == 4 || (forced == 8 && can8)) return forced;
+  return hd == 128 ? 8u : 4u;
 }
 
 }  // namespace
@@ -492,7 +529,9 @@ int rvkv_paged_prefill(rvkv_pool *pool, uint32_t layer, const float *q,
   while ((1u << lg) < bs) ++lg;
   a.bs_log2 = lg;
   a.rows = (uint32_t)rows;
-  a.n_tiles = (uint32_t)((rows + kBM - 1) / kBM);
+  const uint32_t waves = prefill_waves(hd);
+  const uint32_t bm = kWaveRows * waves;
+  a.n_tiles = (uint32_t)((rows + bm - 1) / bm);
   a.qscale = scale * 1.4426950408889634f;
   a.window = window;
   a.batch = batch;
@@ -502,10 +541,16 @@ int rvkv_paged_prefill(rvkv_pool *pool, uint32_t layer, const float *q,
     return fail(RVKV_EUNSUPPORTED, op, "too many query tiles for one launch");
   const dim3 grid((uint32_t)n_wg);
   switch (hd) {
-    case 32: launch_prefill<32>(a, grid, pool->stream); break;
-    case 64: launch_prefill<64>(a, grid, pool->stream); break;
-    case 128: launch_prefill<128>(a, grid, pool->stream); break;
-    default: launch_prefill<256>(a, grid, pool->stream); break;
+    case 32: launch_prefill<32, 4>(a, grid, pool->stream); break;
+    case 64:
+      if (waves == 8) launch_prefill<64, 8>(a, grid, pool->stream);
+      else launch_prefill<64, 4>(a, grid, pool->stream);
+      break;
+    case 128:
+      if (waves == 8) launch_prefill<128, 8>(a, grid, pool->stream);
+      else launch_prefill<128, 4>(a, grid, pool->stream);
+      break;
+    default: launch_prefill<256, 4>(a, grid, pool->stream); break;
   }
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? RVKV_OK : hip_fail(op, e);
