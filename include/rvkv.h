@@ -244,6 +244,18 @@ int rvkv_paged_prefill(rvkv_pool *pool, uint32_t layer, const float *q,
                        uint32_t q_len, uint32_t max_blocks, uint32_t n_heads,
                        float scale, int32_t window, float *out);
 
+/* The same step over one fused [rows, (n_heads + 2 n_kv_heads) * head_dim]
+ * QKV buffer (Q heads, then K, then V) with one fused bias [that width] or
+ * NULL: the interface of the reference's fused attn_prep (Metal,
+ * src/metal/ops.rs:357-420, kernel src/metal/kernels/attention.metal:8-88),
+ * so the projection's output is consumed in place. Same rules otherwise. */
+int rvkv_attn_prep_qkv(rvkv_pool *pool, uint32_t layer, const float *qkv,
+                       uint32_t rows, uint32_t n_heads, const float *bias,
+                       const float *q_norm, const float *k_norm, float eps,
+                       const float *cos_t, const float *sin_t,
+                       const uint32_t *block_ids, const uint32_t *offsets,
+                       float *q_out);
+
 /* ---- a10: prefix-cache copy-on-write -------------------------------------
  * No counterpart in the reference (rvllm never mutates a shared block; its
  * only copy is the whole-cache KvStorage::clone, src/kv_storage.rs:15-33).

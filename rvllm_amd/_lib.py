@@ -48,6 +48,8 @@ SIGNATURES = {
                                   _u32, _f32, _i32, _P]),
     "rvkv_attn_prep": (_int, [_P, _u32, _P, _P, _P, _u32, _u32, _P, _P, _P,
                               _P, _P, _f32, _P, _P, _P, _P, _P]),
+    "rvkv_attn_prep_qkv": (_int, [_P, _u32, _P, _u32, _u32, _P, _P, _P, _f32,
+                                  _P, _P, _P, _P, _P]),
     "rvkv_copy_blocks": (_int, [_P, _P, _P, _u32]),
     "rvkv_read_blocks": (_int, [_P, _u32, _u32, _P, _u32, _P]),
     "rvkv_block_checksums": (_int, [_P, _u32, _u32, _P, _u32, _P]),

@@ -3,7 +3,8 @@
 This is the harness that drives the paged KV path the way rvllm's forward
 does (src/model.rs:600-644 per layer; the CUDA backend's forward_sample,
 src/cuda/engine.rs:339-404): token embedding, then per layer the Q/K/V
-projections, attention prep with the K/V append (rvkv_attn_prep),
+projection (one fused QKV GEMM), attention prep with the K/V append
+(rvkv_attn_prep_qkv),
 attention straight over the paged cache (rvkv_paged_prefill for a prefill
 item, rvkv_paged_decode for a decode batch) and the output projection with
 a residual add; then tied-embedding logits and the greedy pick on the GPU
@@ -98,6 +99,15 @@ class HipBackend:
         self.dev = torch.device(device)
         self.w = {k: torch.from_numpy(v).to(self.dev) for k, v in
                   weights.items()}
+        # One fused QKV projection per layer (Q heads, then K, then V),
+        # consumed in place by rvkv_attn_prep_qkv.
+        for l in range(cfg.n_layers):
+            self.w[f"wqkv{l}"] = torch.cat(
+                [self.w[f"wq{l}"], self.w[f"wk{l}"], self.w[f"wv{l}"]],
+                dim=1).contiguous()
+            if cfg.qkv_bias:
+                self.w[f"bqkv{l}"] = torch.cat(
+                    [self.w[f"bq{l}"], self.w[f"bk{l}"], self.w[f"bv{l}"]])
         self.st = HipKvStorage(cfg.n_layers, num_blocks, block_size,
                                cfg.n_kv_heads, cfg.head_dim)
         self._L = _lib.load()
@@ -134,13 +144,11 @@ class HipBackend:
         scale = 1.0 / math.sqrt(hd)
         decode = not last_only and all(len(it.tokens) == 1 for it in items)
         for l in range(c.n_layers):
-            q = (x @ w[f"wq{l}"]).view(rows, H, hd)
-            k = (x @ w[f"wk{l}"]).view(rows, KV, hd)
-            v = (x @ w[f"wv{l}"]).view(rows, KV, hd)
-            qr = st.attn_prep(l, q, k, v, cos, sin, sb, so,
-                              q_bias=w.get(f"bq{l}"), k_bias=w.get(f"bk{l}"),
-                              v_bias=w.get(f"bv{l}"), q_norm=w.get(f"qn{l}"),
-                              k_norm=w.get(f"kn{l}"), eps=c.eps)
+            qkv = x @ w[f"wqkv{l}"]
+            qr = st.attn_prep_qkv(l, qkv, H, cos, sin, sb, so,
+                                  bias=w.get(f"bqkv{l}"),
+                                  q_norm=w.get(f"qn{l}"),
+                                  k_norm=w.get(f"kn{l}"), eps=c.eps)
             if decode:
                 att = st.paged_decode(
                     l, qr, tables, reads,

@@ -203,6 +203,7 @@ struct PrepArgs {
   float *q_out;
   uint16_t *kc, *vc;
   uint32_t rows, n_heads, n_kv, num_blocks, bs;
+  uint32_t q_stride, kv_stride;  // elements between consecutive input rows
   float eps;
 };
 
@@ -248,9 +249,9 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(PrepArgs a) {
   const bool is_v = slot >= a.n_heads + a.n_kv;
   const uint32_t hh = is_q ? slot : (is_v ? slot - a.n_heads - a.n_kv
                                           : slot - a.n_heads);
-  const float *src =
-      is_q ? a.q_in + ((size_t)row * a.n_heads + hh) * HD
-           : (is_v ? a.v_in : a.k_in) + ((size_t)row * a.n_kv + hh) * HD;
+  const float *src = is_q ? a.q_in + (size_t)row * a.q_stride + hh * HD
+                          : (is_v ? a.v_in : a.k_in) +
+                                (size_t)row * a.kv_stride + hh * HD;
   float x0[V], x1[V];
   ld8(src + j, x0);
   ld8(src + j + HALF, x1);
@@ -1619,29 +1620,22 @@ int rvkv_decode_step(rvkv_pool *pool, const rvkv_decode_plan *plan,
                             dim3(n_heads, batch), w.n_parts > 1, pool->stream);
 }
 
-int rvkv_attn_prep(rvkv_pool *pool, uint32_t layer, const float *q_in,
-                   const float *k_in, const float *v_in, uint32_t rows,
-                   uint32_t n_heads, const float *q_bias, const float *k_bias,
+}  // extern "C"
+
+namespace {
+
+// Shared by the split (q, k, v) and the fused (qkv) entry points; q and
+// k/v rows are q_stride / kv_stride floats apart.
+int attn_prep_impl(rvkv_pool *pool, uint32_t layer, const float *q_in,
+                   const float *k_in, const float *v_in, uint32_t q_stride,
+                   uint32_t kv_stride, uint32_t rows, uint32_t n_heads,
+                   const float *q_bias, const float *k_bias,
                    const float *v_bias, const float *q_norm,
                    const float *k_norm, float eps, const float *cos_t,
                    const float *sin_t, const uint32_t *slot_block,
                    const uint32_t *slot_off, float *q_out) {
   const char *op = "attn_prep";
-  if (!pool) return fail(RVKV_EINVAL, op, "pool is NULL");
-  if (layer >= pool->n_layers)
-    return fail(RVKV_EINVAL, op, "layer out of range");
-  if (rows == 0) return RVKV_OK;
-  if (n_heads == 0 || n_heads % pool->n_kv != 0)
-    return fail(RVKV_EINVAL, op,
-                "n_heads must be a positive multiple of n_kv_heads");
-  if (!q_in || !k_in || !v_in || !cos_t || !sin_t || !slot_block ||
-      !slot_off || !q_out)
-    return fail(RVKV_EINVAL, op,
-                "NULL q/k/v/cos/sin/block_ids/offsets/q_out");
   const uint32_t hd = pool->head_dim;
-  if (!hd_supported(hd))
-    return fail(RVKV_EUNSUPPORTED, op,
-                "head_dim must be one of 32, 64, 128, 256");
   PrepArgs a{};
   a.q_in = q_in;
   a.k_in = k_in;
@@ -1663,6 +1657,8 @@ int rvkv_attn_prep(rvkv_pool *pool, uint32_t layer, const float *q_in,
   a.n_kv = pool->n_kv;
   a.num_blocks = pool->num_blocks;
   a.bs = pool->block_size;
+  a.q_stride = q_stride;
+  a.kv_stride = kv_stride;
   a.eps = eps;
   for (const void *p : {(const void *)q_in, (const void *)k_in,
                         (const void *)v_in, (const void *)q_bias,
@@ -1685,6 +1681,69 @@ int rvkv_attn_prep(rvkv_pool *pool, uint32_t layer, const float *q_in,
   }
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? RVKV_OK : hip_fail(op, e);
+}
+
+// Validation common to both entry points; 1 = proceed, 0 = nothing to do,
+// < 0 = error code.
+int attn_prep_check(rvkv_pool *pool, uint32_t layer, uint32_t rows,
+                    uint32_t n_heads) {
+  const char *op = "attn_prep";
+  if (!pool) return fail(RVKV_EINVAL, op, "pool is NULL");
+  if (layer >= pool->n_layers)
+    return fail(RVKV_EINVAL, op, "layer out of range");
+  if (rows == 0) return 0;
+  if (n_heads == 0 || n_heads % pool->n_kv != 0)
+    return fail(RVKV_EINVAL, op,
+                "n_heads must be a positive multiple of n_kv_heads");
+  if (!hd_supported(pool->head_dim))
+    return fail(RVKV_EUNSUPPORTED, op,
+                "head_dim must be one of 32, 64, 128, 256");
+  return 1;
+}
+
+}  // namespace
+
+extern "C" {
+
+int rvkv_attn_prep(rvkv_pool *pool, uint32_t layer, const float *q_in,
+                   const float *k_in, const float *v_in, uint32_t rows,
+                   uint32_t n_heads, const float *q_bias, const float *k_bias,
+                   const float *v_bias, const float *q_norm,
+                   const float *k_norm, float eps, const float *cos_t,
+                   const float *sin_t, const uint32_t *slot_block,
+                   const uint32_t *slot_off, float *q_out) {
+  const int rc = attn_prep_check(pool, layer, rows, n_heads);
+  if (rc <= 0) return rc;
+  if (!q_in || !k_in || !v_in || !cos_t || !sin_t || !slot_block ||
+      !slot_off || !q_out)
+    return fail(RVKV_EINVAL, "attn_prep",
+                "NULL q/k/v/cos/sin/block_ids/offsets/q_out");
+  const uint32_t hd = pool->head_dim;
+  return attn_prep_impl(pool, layer, q_in, k_in, v_in, n_heads * hd,
+                        pool->n_kv * hd, rows, n_heads, q_bias, k_bias,
+                        v_bias, q_norm, k_norm, eps, cos_t, sin_t,
+                        slot_block, slot_off, q_out);
+}
+
+int rvkv_attn_prep_qkv(rvkv_pool *pool, uint32_t layer, const float *qkv,
+                       uint32_t rows, uint32_t n_heads, const float *bias,
+                       const float *q_norm, const float *k_norm, float eps,
+                       const float *cos_t, const float *sin_t,
+                       const uint32_t *block_ids, const uint32_t *offsets,
+                       float *q_out) {
+  const int rc = attn_prep_check(pool, layer, rows, n_heads);
+  if (rc <= 0) return rc;
+  if (!qkv || !cos_t || !sin_t || !block_ids || !offsets || !q_out)
+    return fail(RVKV_EINVAL, "attn_prep",
+                "NULL qkv/cos/sin/block_ids/offsets/q_out");
+  const uint32_t hd = pool->head_dim, kv = pool->n_kv;
+  const uint32_t width = (n_heads + 2 * kv) * hd;  // the QKV width
+  return attn_prep_impl(
+      pool, layer, qkv, qkv + (size_t)n_heads * hd,
+      qkv + (size_t)(n_heads + kv) * hd, width, width, rows, n_heads, bias,
+      bias ? bias + (size_t)n_heads * hd : nullptr,
+      bias ? bias + (size_t)(n_heads + kv) * hd : nullptr, q_norm, k_norm,
+      eps, cos_t, sin_t, block_ids, offsets, q_out);
 }
 
 int rvkv_copy_blocks(rvkv_pool *pool, const uint32_t *src, const uint32_t *dst,

@@ -410,6 +410,39 @@ class HipKvStorage:
             _ptr(slot_off), _ptr(q_out)))
         return q_out
 
+    def attn_prep_qkv(self, layer: int, qkv: torch.Tensor, n_heads: int,
+                      cos: torch.Tensor, sin: torch.Tensor,
+                      block_ids: torch.Tensor, offsets: torch.Tensor,
+                      bias=None, q_norm=None, k_norm=None, eps: float = 1e-5,
+                      q_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """rvkv_attn_prep_qkv: attn_prep over one fused QKV buffer [rows,
+        (n_heads + 2 n_kv) * hd] with a fused bias, as the reference's
+        fused attn_prep takes them (src/metal/ops.rs:357-420); returns q
+        [rows, n_heads, hd]."""
+        hd, kv = self.head_dim, self.n_kv_heads
+        width = (n_heads + 2 * kv) * hd
+        _need(qkv.dim() == 2 and qkv.shape[1] == width,
+              "attn_prep: qkv length is not a multiple of the QKV width")
+        rows = qkv.shape[0]
+        for t in (qkv, cos, sin, bias, q_norm, k_norm):
+            _need(t is None or (t.dtype == torch.float32 and
+                                t.is_contiguous()),
+                  "attn_prep: float tensors must be contiguous float32")
+        _need(bias is None or bias.numel() == width,
+              "attn_prep: bias must be [QKV width]")
+        _need(cos.shape == (rows, hd // 2) and sin.shape == cos.shape,
+              "attn_prep: cos/sin must be [rows, head_dim / 2]")
+        _need(block_ids.numel() == rows and offsets.numel() == rows,
+              "attn_prep: block_ids/offsets must hold one entry per row")
+        if q_out is None:
+            q_out = torch.empty((rows, n_heads, hd), dtype=torch.float32,
+                                device=qkv.device)
+        check(self._L.rvkv_attn_prep_qkv(
+            self._pool, layer, _ptr(qkv), rows, n_heads, _ptr(bias),
+            _ptr(q_norm), _ptr(k_norm), float(eps), _ptr(cos), _ptr(sin),
+            _ptr(block_ids), _ptr(offsets), _ptr(q_out)))
+        return q_out
+
     # -- a10: copy-on-write -------------------------------------------------
     def copy_blocks(self, src: torch.Tensor, dst: torch.Tensor) -> None:
         """Copies src[i] -> dst[i] for all layers, K and V."""

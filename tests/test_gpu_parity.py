@@ -1074,3 +1074,102 @@ def test_engine_fork_copy_on_write_on_gpu():
     while eng.has_work():
         eng.step()
     assert be.calls > 5
+
+
+@pytest.mark.parametrize("hd,bias_on,qn_on,kn_on", [(64, True, True, True),
+                                                    (128, False, False, False),
+                                                    (6, True, False, True),
+                                                    (2, False, True, False)])
+def test_attn_prep_qkv_metal_cases(hd, bias_on, qn_on, kn_on):
+    """attn_prep_matches_reference (src/metal/ops.rs:771-858) through the
+    fused-QKV entry point: 6 q / 2 kv heads, 5 rows, xorshift values (seeds
+    40-45), row r to (block r % 3 + 1, offset r % 4), eps 1e-5. The expected
+    values are computed as that test computes them (rms in float64, the
+    rotate-half in f32); q within its 1e-5, the f16 cache equal to the
+    expected f32 rounded to f16 (one ulp where the norm's sum order shows).
+    Head widths 6 and 2 are not supported here and must be rejected."""
+    from tests.golden.make_golden import values
+    H, KV, rows, bs = 6, 2, 5, 4
+    width = (H + 2 * KV) * hd
+    if hd % 32:
+        st = HipKvStorage(1, 4, bs, KV, hd)
+        with pytest.raises(RvkvError, match="attn_prep: head_dim"):
+            st.attn_prep_qkv(0, torch.zeros(rows, width, device="cuda"), H,
+                             torch.zeros(rows, hd // 2, device="cuda"),
+                             torch.zeros(rows, hd // 2, device="cuda"),
+                             dev_u32([0] * rows), dev_u32([0] * rows))
+        return
+    half, eps = hd // 2, np.float32(1e-5)
+    qkv = values(rows * width, 40).reshape(rows, width)
+    bias, qn, kn = values(width, 41), values(hd, 42), values(hd, 43)
+    cos = values(rows * half, 44).reshape(rows, half)
+    sin = values(rows * half, 45).reshape(rows, half)
+    blk = np.arange(rows, dtype=np.uint32) % 3 + 1
+    off = np.arange(rows, dtype=np.uint32) % bs
+
+    def head(r, slot):
+        x = qkv[r, slot * hd:(slot + 1) * hd]
+        return (x + bias[slot * hd:(slot + 1) * hd]) if bias_on else x.copy()
+
+    def rotate(r, x, w):
+        if w is not None:
+            ms = np.sum(x.astype(np.float64) ** 2) / hd
+            rms = np.float32(np.sqrt(ms + np.float64(eps)))
+            x = (x / rms) * w
+        c, s = cos[r], sin[r]
+        return np.concatenate([x[:half] * c - x[half:] * s,
+                               x[:half] * s + x[half:] * c]).astype(np.float32)
+
+    want_q = np.stack([[rotate(r, head(r, h), qn if qn_on else None)
+                        for h in range(H)] for r in range(rows)])
+    want_k = np.zeros((4, bs, KV, hd), np.float32)
+    want_v = np.zeros_like(want_k)
+    for r in range(rows):
+        for h in range(KV):
+            want_k[blk[r], off[r], h] = rotate(r, head(r, H + h),
+                                               kn if kn_on else None)
+            want_v[blk[r], off[r], h] = head(r, H + KV + h)
+    st = HipKvStorage(1, 4, bs, KV, hd)
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    q = st.attn_prep_qkv(0, T(qkv), H, T(cos), T(sin), dev_u32(blk),
+                         dev_u32(off), bias=T(bias) if bias_on else None,
+                         q_norm=T(qn) if qn_on else None,
+                         k_norm=T(kn) if kn_on else None, eps=1e-5)
+    assert np.abs(q.cpu().numpy() - want_q).max() < 1e-5
+    ids = dev_u32(np.arange(4))
+    gk, gv = bits(st.read_blocks(0, 0, ids)), bits(st.read_blocks(0, 1, ids))
+    assert np.array_equal(gv, orc.f32_to_f16_bits(want_v))
+    d = np.abs(gk.astype(np.int32) - orc.f32_to_f16_bits(want_k).astype(
+        np.int32))
+    assert d.max() <= (1 if kn_on else 0)
+
+
+def test_attn_prep_qkv_equals_split_entry_point():
+    """The fused-QKV entry point and the split one give identical bits."""
+    rng = np.random.default_rng(44)
+    H, KV, hd, rows, nb, bs = 16, 8, 128, 50, 20, 16
+    width = (H + 2 * KV) * hd
+    qkv = rng.standard_normal((rows, width)).astype(np.float32)
+    bias = rng.standard_normal(width).astype(np.float32)
+    qn, kn = (rng.standard_normal(hd).astype(np.float32) for _ in range(2))
+    from rvllm_amd.rope import rope_cos_sin
+    c, s = rope_cos_sin(1e6, hd, rng.integers(0, 4096, rows))
+    slots = rng.permutation(nb * bs)[:rows]
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    a = HipKvStorage(1, nb, bs, KV, hd)
+    b = HipKvStorage(1, nb, bs, KV, hd)
+    qa = a.attn_prep_qkv(0, T(qkv), H, T(c), T(s), dev_u32(slots // bs),
+                         dev_u32(slots % bs), bias=T(bias), q_norm=T(qn),
+                         k_norm=T(kn), eps=1e-6)
+    qb = b.attn_prep(0, T(qkv[:, :H * hd].reshape(rows, H, hd)),
+                     T(qkv[:, H * hd:(H + KV) * hd].reshape(rows, KV, hd)),
+                     T(qkv[:, (H + KV) * hd:].reshape(rows, KV, hd)), T(c),
+                     T(s), dev_u32(slots // bs), dev_u32(slots % bs),
+                     q_bias=T(bias[:H * hd]),
+                     k_bias=T(bias[H * hd:(H + KV) * hd]),
+                     v_bias=T(bias[(H + KV) * hd:]), q_norm=T(qn),
+                     k_norm=T(kn), eps=1e-6)
+    assert torch.equal(qa, qb)
+    ids = dev_u32(np.arange(nb))
+    for w in (0, 1):
+        assert torch.equal(a.read_blocks(0, w, ids), b.read_blocks(0, w, ids))
