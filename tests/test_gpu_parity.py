@@ -1025,7 +1025,7 @@ def _engine_pair(cfg, num_blocks, bs):
                            OracleBackend(cfg, w, num_blocks, bs))
 
 
-@pytest.mark.parametrize("variant", ["plain", "qwen3", "qwen25"])
+@pytest.mark.parametrize("variant", ["plain", "qwen3", "qwen25", "window"])
 def test_engine_lockstep_with_oracle(variant):
     """The engine over the native scheduler with the GPU backend: every
     prefill and decode forward (attn_prep + append, paged prefill, paged
@@ -1037,7 +1037,8 @@ def test_engine_lockstep_with_oracle(variant):
     cfg = AttnModelConfig(
         vocab=512, hidden=128, n_layers=2, n_heads=8, n_kv_heads=2,
         head_dim=64, qkv_bias=variant == "qwen25",
-        qk_norm=variant == "qwen3", context_length=512)
+        qk_norm=variant == "qwen3", context_length=512,
+        window=24 if variant == "window" else 0)
     be = _engine_pair(cfg, num_blocks=14, bs=16)  # tight: preempts twice
     eng = Engine(be, EngineConfig(block_size=16, num_blocks=14,
                                   max_running=6))
@@ -1173,3 +1174,72 @@ def test_attn_prep_qkv_equals_split_entry_point():
     ids = dev_u32(np.arange(nb))
     for w in (0, 1):
         assert torch.equal(a.read_blocks(0, w, ids), b.read_blocks(0, w, ids))
+
+
+def test_graph_capture_prep_prefill_argmax():
+    """rvkv_attn_prep_qkv (QK norm, bias) -> rvkv_paged_prefill ->
+    rvkv_argmax captured in one HIP graph: on every replay, with new QKV
+    input between replays, the graph's q, attention output, picked ids and
+    cache bits equal an eager run of the same calls on a twin pool."""
+    import ctypes
+    from rvllm_amd import _lib
+    from rvllm_amd.rope import rope_cos_sin
+    L = _lib.load()
+    H, KV, hd, bs, nb = 8, 2, 64, 16, 12
+    rows, off = 40, 7  # a 40-token chunk after 7 cached tokens
+    width = (H + 2 * KV) * hd
+    g = torch.Generator("cuda").manual_seed(3)
+    rnd = lambda *s: torch.randn(*s, device="cuda", generator=g)
+    bias, qn, kn = rnd(width), rnd(hd), rnd(hd)
+    c, s = (torch.from_numpy(a).cuda()
+            for a in rope_cos_sin(1e4, hd, np.arange(off, off + rows)))
+    table = np.random.default_rng(3).permutation(nb).astype(np.uint32)
+    pos = np.arange(off, off + rows)
+    sb, so = dev_u32(table[pos // bs]), dev_u32(pos % bs)
+    tables = dev_u32(table[None, :])
+    offs, reads = dev_u32([off]), dev_u32([off + rows])
+    pools = [HipKvStorage(1, nb, bs, KV, hd) for _ in range(2)]
+    for p in pools:  # the same cached prefix in both
+        fill_layer(p, 0, seed=4)
+    qkv = rnd(rows, width)
+    outs = [dict(q=torch.empty(rows, H, hd, device="cuda"),
+                 att=torch.empty(1, rows, H, hd, device="cuda"),
+                 ids=torch.empty(rows, dtype=torch.int32, device="cuda"))
+            for _ in range(2)]
+
+    def forward(p, o):
+        p.attn_prep_qkv(0, qkv, H, c, s, sb, so, bias=bias, q_norm=qn,
+                        k_norm=kn, eps=1e-6, q_out=o["q"])
+        p.paged_prefill(0, o["q"].view(1, rows, H, hd), tables, offs, reads,
+                        out=o["att"])
+        _lib.check(L.rvkv_argmax(
+            ctypes.c_void_p(o["att"].data_ptr()), rows, H * hd,
+            ctypes.c_void_p(o["ids"].data_ptr()),
+            ctypes.c_void_p(p.stream.cuda_stream)))
+
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        pools[0].set_stream(side)
+        forward(pools[0], outs[0])  # warm-up outside the graph
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        pools[0].set_stream(torch.cuda.current_stream())
+        forward(pools[0], outs[0])
+    pools[0].set_stream(torch.cuda.current_stream())
+    ids = dev_u32(np.arange(nb))
+    for rep in range(3):
+        qkv.copy_(rnd(rows, width))
+        for v in outs[0].values():
+            v.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        forward(pools[1], outs[1])
+        torch.cuda.synchronize()
+        for k in ("q", "att", "ids"):
+            assert torch.equal(outs[0][k], outs[1][k]), (rep, k)
+        for w in (0, 1):
+            assert torch.equal(pools[0].read_blocks(0, w, ids),
+                               pools[1].read_blocks(0, w, ids)), (rep, w)
