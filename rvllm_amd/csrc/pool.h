@@ -28,4 +28,12 @@ namespace rvkv_detail {
 int fail(int code, const char *op, const char *reason);
 // Records "<op>: <HIP error string>" and returns RVKV_EHIP.
 int hip_fail(const char *op, hipError_t e);
+// Matrix-core decode over a decode plan's work items (prefill.hip): used
+// for large GQA groups, where the VALU decode is instruction-bound.
+bool mfma_decode_wanted(const rvkv_pool *pool, uint32_t n_heads);
+int mfma_decode(const rvkv_pool *pool, uint32_t layer, const float *q,
+                const uint32_t *tables, const uint32_t *ctx_lens,
+                uint32_t max_blocks, uint32_t n_heads, float scale,
+                int32_t window, const uint4 *items, uint32_t n_items,
+                float *ws_acc, float *ws_ml, float *out);
 }  // namespace rvkv_detail

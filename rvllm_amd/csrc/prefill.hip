@@ -37,6 +37,7 @@
 
 #include <cmath>
 #include <cstdlib>
+#include <type_traits>
 
 using rvkv_detail::fail;
 using rvkv_detail::hip_fail;
@@ -50,9 +51,11 @@ typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
 // Keys per tile: 64, or 32 at head_dim 256 (one 32-key sub-tile keeps the
 // S accumulators and the tile's load registers within the register file).
-template <int HD>
+// (32 also for one-wave decode workgroups, whose single wave loads the
+// whole tile.)
+template <int HD, int WAVES>
 constexpr int tile_keys() {
-  return HD >= 256 ? 32 : 64;
+  return HD >= 256 || WAVES == 1 ? 32 : 64;
 }
 constexpr int kWaveRows = 32;  // query rows per wave
 constexpr float kNegBig = -1.0e30f;      // finite start value of the row max
@@ -71,11 +74,19 @@ struct PrefillArgs {
   uint32_t n_tiles;  // ceil(rows / (32 * waves per workgroup))
   float qscale;      // scale * log2(e)
   int32_t window;
+  // Decode mode (q_len 1 at position read_num - 1) over a decode plan's
+  // work items {seq, first key, end key, slot}: slot kNoSlot writes the
+  // output; otherwise the unnormalised partial (acc, m, l) goes to ws_acc /
+  // ws_ml [slot][n_heads] for the decode reduction pass. NULL: prefill.
+  const uint4 *items;
+  float *ws_acc, *ws_ml;
 };
 
-template <int HD>
+constexpr uint32_t kNoSlot = 0xFFFFFFFFu;
+
+template <int HD, int WAVES>
 struct Lds {
-  static constexpr int BN = tile_keys<HD>();
+  static constexpr int BN = tile_keys<HD, WAVES>();
   static constexpr int KS = HD + 8;  // K row stride in halves (16 B pad)
   static constexpr int VS = BN + 8;  // Vt row stride in halves
   static constexpr size_t k_bytes = (size_t)BN * KS * 2;
@@ -105,13 +116,16 @@ __device__ __forceinline__ uint32_t lo_bound(uint32_t p, int32_t window) {
 // softmax with another's matrix work. (128-key tiles at head_dim 64 were
 // measured 7-9 % slower than 64.)
 template <int HD, int WAVES>
-__global__ void __launch_bounds__(64 * WAVES,
-                                  (HD <= 64 ? 12 : (HD <= 128 ? 8 : 4)) /
-                                      WAVES)
+__global__ void __launch_bounds__(
+    64 * WAVES,
+    // (a one-wave workgroup may share a SIMD with others: 2 bounds the
+    // registers to two waves per SIMD)
+    WAVES == 1 ? 2 : (HD <= 64 ? 12 : (HD <= 128 ? 8 : 4)) / WAVES)
     prefill_kernel(PrefillArgs a) {
   constexpr int NTH = 64 * WAVES;  // threads per workgroup
   constexpr int kBM = kWaveRows * WAVES;
-  constexpr int KS = Lds<HD>::KS, VS = Lds<HD>::VS, BN = Lds<HD>::BN;
+  using LD = Lds<HD, WAVES>;
+  constexpr int KS = LD::KS, VS = LD::VS, BN = LD::BN;
   constexpr int NT = BN / 32;                 // 32-key sub-tiles per tile
   constexpr int NPR = BN / 2;                 // key pairs per tile
   constexpr int KC = HD / 16;                 // MFMA k-steps of S
@@ -121,8 +135,8 @@ __global__ void __launch_bounds__(64 * WAVES,
   static_assert(CHK >= 1 && BN * CPR % NTH == 0, "tile/thread mismatch");
   extern __shared__ __align__(16) unsigned char smem[];
   uint16_t *ks = reinterpret_cast<uint16_t *>(smem);
-  uint16_t *vt = reinterpret_cast<uint16_t *>(smem + Lds<HD>::k_bytes);
-  uint8_t *kok = smem + Lds<HD>::k_bytes + Lds<HD>::v_bytes;
+  uint16_t *vt = reinterpret_cast<uint16_t *>(smem + LD::k_bytes);
+  uint8_t *kok = smem + LD::k_bytes + LD::v_bytes;
 
   // XCD-aware order: workgroups are dispatched round-robin over the 8 XCDs
   // (each with its own L2), so workgroup w runs on XCD w % 8. Renumber so
@@ -130,20 +144,34 @@ __global__ void __launch_bounds__(64 * WAVES,
   // tiles of one (sequence, KV head) are adjacent: they re-read the same
   // K/V, which then stays in that XCD's L2. Within a head, long (late)
   // rows go first.
-  const uint32_t n_wg = a.n_tiles * a.n_kv * a.batch;
-  const uint32_t w = blockIdx.x, xcd = w % 8, idx = w / 8;
-  const uint32_t per = n_wg / 8, rem = n_wg % 8;
-  const uint32_t logical = xcd < rem ? xcd * (per + 1) + idx
-                                     : rem * (per + 1) + (xcd - rem) * per + idx;
-  const uint32_t tile = a.n_tiles - 1 - logical % a.n_tiles;
-  const uint32_t kvh = (logical / a.n_tiles) % a.n_kv;
-  const uint32_t b = logical / a.n_tiles / a.n_kv;
+  uint32_t tile, kvh, b, item_lo = 0, item_hi = 0xFFFFFFFFu, slot = kNoSlot;
+  if (a.items) {  // decode items: grid (items, n_kv), plan order kept
+    const uint4 it = a.items[blockIdx.x];
+    b = it.x;
+    item_lo = it.y;
+    item_hi = it.z;
+    slot = it.w;
+    kvh = blockIdx.y;
+    tile = 0;
+  } else {
+    const uint32_t n_wg = a.n_tiles * a.n_kv * a.batch;
+    const uint32_t w = blockIdx.x, xcd = w % 8, idx = w / 8;
+    const uint32_t per = n_wg / 8, rem = n_wg % 8;
+    const uint32_t logical =
+        xcd < rem ? xcd * (per + 1) + idx
+                  : rem * (per + 1) + (xcd - rem) * per + idx;
+    tile = a.n_tiles - 1 - logical % a.n_tiles;
+    kvh = (logical / a.n_tiles) % a.n_kv;
+    b = logical / a.n_tiles / a.n_kv;
+  }
   const int tid = threadIdx.x;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63, hl = lane >> 5, ln = lane & 31;
   const uint32_t bs_mask = (1u << a.bs_log2) - 1u;
 
-  const uint32_t off = a.pos_offset[b];
+  // Decode: the one query row sits at position read_num - 1 (an empty
+  // sequence wraps to 2^32 - 1 and sees no key).
+  const uint32_t off = a.items ? a.read_num[b] - 1u : a.pos_offset[b];
   const uint32_t cap = a.max_blocks << a.bs_log2;
   const uint32_t ctx = min(a.read_num[b], cap);
   const uint32_t *table = a.tables + (size_t)b * a.max_blocks;
@@ -151,18 +179,22 @@ __global__ void __launch_bounds__(64 * WAVES,
   // Key range any row of the workgroup sees, in whole tiles.
   const uint32_t r_first = tile * kBM;
   const uint32_t r_last = min(r_first + kBM, a.rows) - 1u;
-  const uint32_t k_end = min(ctx, off + r_last / a.group + 1u);
-  const uint32_t k_begin =
-      lo_bound(off + r_first / a.group, a.window) & ~(uint32_t)(BN - 1);
+  const uint32_t k_end = min(min(ctx, off + r_last / a.group + 1u), item_hi);
+  // (item_lo is a multiple of 256, so of BN)
+  const uint32_t k_begin = max(
+      lo_bound(off + r_first / a.group, a.window) & ~(uint32_t)(BN - 1),
+      item_lo);
 
   // The same for this wave's 32 rows (wave-uniform).
   const uint32_t rw0 = r_first + wave * kWaveRows;
   const bool wave_live = rw0 < a.rows;
   const uint32_t rw1 = min(rw0 + kWaveRows, a.rows) - 1u;
-  const uint32_t w_end = wave_live ? min(ctx, off + rw1 / a.group + 1u) : 0u;
+  const uint32_t w_end =
+      wave_live ? min(min(ctx, off + rw1 / a.group + 1u), item_hi) : 0u;
   const uint32_t w_begin = lo_bound(off + rw0 / a.group, a.window);
   // Keys every row of the wave sees: [w_lo_max, w_hi_min).
-  const uint32_t w_hi_min = wave_live ? min(ctx, off + rw0 / a.group + 1u) : 0u;
+  const uint32_t w_hi_min =
+      wave_live ? min(min(ctx, off + rw0 / a.group + 1u), item_hi) : 0u;
   const uint32_t w_lo_max = lo_bound(off + rw1 / a.group, a.window);
 
   // This lane's query row.
@@ -171,8 +203,8 @@ __global__ void __launch_bounds__(64 * WAVES,
   const uint32_t qi = row_ok ? r / a.group : 0u;
   const uint32_t head = kvh * a.group + (row_ok ? r - qi * a.group : 0u);
   const uint32_t p = off + qi;
-  const uint32_t row_hi = row_ok ? min(ctx, p + 1u) : 0u;
-  const uint32_t row_lo = lo_bound(p, a.window);
+  const uint32_t row_hi = row_ok ? min(min(ctx, p + 1u), item_hi) : 0u;
+  const uint32_t row_lo = max(lo_bound(p, a.window), item_lo);
   const size_t qrow = ((size_t)b * a.q_len + qi) * a.n_heads + head;
 
   half8 qf[KC];
@@ -256,9 +288,16 @@ __global__ void __launch_bounds__(64 * WAVES,
     v_db[j] = v_key[j] >> a.bs_log2;
   }
   const uint64_t blk_bytes = a.block_stride * 2;
+  // Tiles in flight: one ahead, or two for one-wave (decode) workgroups,
+  // whose single wave's compute per tile is shorter than a load's latency.
+  // Register sets are selected by a compile-time index (a runtime index
+  // would put the arrays in scratch).
+  constexpr int DEPTH = WAVES == 1 ? 2 : 1;
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, DEPTH - 1>;
   uint32_t kid[CHK], vid[CHV];
-  u32x4 kr[CHK], vr0[CHV], vr1[CHV];
-  uint32_t kbits = 0, vbits = 0;
+  u32x4 kr[DEPTH][CHK], vr0[DEPTH][CHV], vr1[DEPTH][CHV];
+  uint32_t kbits[DEPTH], vbits[DEPTH];
 
   auto fetch_ids = [&](uint32_t kt) {
     const uint32_t b0 = kt >> a.bs_log2, last = a.max_blocks - 1u;
@@ -267,17 +306,18 @@ __global__ void __launch_bounds__(64 * WAVES,
 #pragma unroll
     for (int j = 0; j < CHV; ++j) vid[j] = table[min(b0 + v_db[j], last)];
   };
-  auto load = [&](uint32_t kt) {
+  auto load = [&](auto S, uint32_t kt) {
+    constexpr int si = decltype(S)::value;
     const uint32_t t_off = (kt & bs_mask) * HD * 2;  // 0 unless bs > 64
-    kbits = 0;
-    vbits = 0;
+    kbits[si] = 0;
+    vbits[si] = 0;
 #pragma unroll
     for (int i = 0; i < CHK; ++i) {
       // The address checks its own block id: all_ok covers only the blocks
       // of keys below k_end, and the last tile may reach past them.
       const bool okb = kid[i] < a.num_blocks;
-      kbits |= (uint32_t)(okb && kt + k_key[i] < k_end) << i;
-      kr[i] = *reinterpret_cast<const u32x4 *>(
+      kbits[si] |= (uint32_t)(okb && kt + k_key[i] < k_end) << i;
+      kr[si][i] = *reinterpret_cast<const u32x4 *>(
           kbase + (uint64_t)(okb ? kid[i] : 0u) * blk_bytes + t_off +
           k_off[i]);
     }
@@ -285,23 +325,21 @@ __global__ void __launch_bounds__(64 * WAVES,
     for (int j = 0; j < CHV; ++j) {
       const bool okb = vid[j] < a.num_blocks;
       const uint32_t tok = kt + v_key[j];
-      vbits |= (uint32_t)(okb && tok < k_end) << (2 * j);
-      vbits |= (uint32_t)(okb && tok + 1 < k_end) << (2 * j + 1);
+      vbits[si] |= (uint32_t)(okb && tok < k_end) << (2 * j);
+      vbits[si] |= (uint32_t)(okb && tok + 1 < k_end) << (2 * j + 1);
       const char *vp = vbase + (uint64_t)(okb ? vid[j] : 0u) * blk_bytes +
                        t_off + v_off[j];
       if (v_lane) {
-        vr0[j] = *reinterpret_cast<const u32x4 *>(vp);
-        vr1[j] = *reinterpret_cast<const u32x4 *>(vp + HD * 2);
+        vr0[si][j] = *reinterpret_cast<const u32x4 *>(vp);
+        vr1[si][j] = *reinterpret_cast<const u32x4 *>(vp + HD * 2);
       }
     }
   };
 
-  if (k_begin < k_end) {
-    fetch_ids(k_begin);
-    load(k_begin);
-    fetch_ids(k_begin + BN);
-  }
-  for (uint32_t kt = k_begin; kt < k_end; kt += BN) {
+  // One tile: stage register set S into LDS, refill S with the tile DEPTH
+  // ahead, compute.
+  auto step = [&](auto S, uint32_t kt) {
+    constexpr int si = decltype(S)::value;
     // Every key of the tile readable: all blocks valid, tile inside k_end.
     const bool tile_ok = all_ok && kt + BN <= k_end;
     __syncthreads();  // the previous tile is no longer read
@@ -309,9 +347,9 @@ __global__ void __launch_bounds__(64 * WAVES,
     for (int i = 0; i < CHK; ++i) {
       const int c = tid + NTH * i;
       const int key = c / CPR, dc = c % CPR;
-      *reinterpret_cast<u32x4 *>(ks + key * KS + dc * 8) = kr[i];
+      *reinterpret_cast<u32x4 *>(ks + key * KS + dc * 8) = kr[si][i];
       // Every loader of a key writes the same flag.
-      if (!all_ok) kok[key] = (uint8_t)((kbits >> i) & 1u);
+      if (!all_ok) kok[key] = (uint8_t)((kbits[si] >> i) & 1u);
     }
     if (v_lane) {
 #pragma unroll
@@ -324,32 +362,32 @@ __global__ void __launch_bounds__(64 * WAVES,
           for (int e = 0; e < 4; ++e) {
             // d = 8dc + 2e: low halves of both keys; d + 1: high halves.
             row[(2 * e) * (VS / 2)] =
-                __builtin_amdgcn_perm(vr1[j][e], vr0[j][e], 0x05040100u);
+                __builtin_amdgcn_perm(vr1[si][j][e], vr0[si][j][e], 0x05040100u);
             row[(2 * e + 1) * (VS / 2)] =
-                __builtin_amdgcn_perm(vr1[j][e], vr0[j][e], 0x07060302u);
+                __builtin_amdgcn_perm(vr1[si][j][e], vr0[si][j][e], 0x07060302u);
           }
         } else {
           const uint32_t mask =
-              ((vbits >> (2 * j)) & 1u ? 0xffffu : 0u) |
-              ((vbits >> (2 * j + 1)) & 1u ? 0xffff0000u : 0u);
+              ((vbits[si] >> (2 * j)) & 1u ? 0xffffu : 0u) |
+              ((vbits[si] >> (2 * j + 1)) & 1u ? 0xffff0000u : 0u);
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             row[(2 * e) * (VS / 2)] =
-                __builtin_amdgcn_perm(vr1[j][e], vr0[j][e], 0x05040100u) &
+                __builtin_amdgcn_perm(vr1[si][j][e], vr0[si][j][e], 0x05040100u) &
                 mask;
             row[(2 * e + 1) * (VS / 2)] =
-                __builtin_amdgcn_perm(vr1[j][e], vr0[j][e], 0x07060302u) &
+                __builtin_amdgcn_perm(vr1[si][j][e], vr0[si][j][e], 0x07060302u) &
                 mask;
           }
         }
       }
     }
     __syncthreads();
-    if (kt + BN < k_end) {
-      load(kt + BN);
-      fetch_ids(kt + 2 * BN);
+    if (kt + DEPTH * BN < k_end) {
+      load(S, kt + DEPTH * BN);
+      fetch_ids(kt + (DEPTH + 1) * BN);
     }
-    if (!(kt < w_end && kt + BN > w_begin)) continue;  // nothing for this wave
+    if (!(kt < w_end && kt + BN > w_begin)) return;  // nothing for this wave
 
     f32x16 s[NT];
 #pragma unroll
@@ -439,9 +477,48 @@ __global__ void __launch_bounds__(64 * WAVES,
           o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pb[t][c], o[dt],
                                                          0, 0, 0);
         }
+  };
+
+  if (k_begin < k_end) {
+    fetch_ids(k_begin);
+    load(I0{}, k_begin);
+    fetch_ids(k_begin + BN);
+    if constexpr (DEPTH == 2) {
+      if (k_begin + BN < k_end) load(I1{}, k_begin + BN);
+      fetch_ids(k_begin + 2 * BN);
+    }
+  }
+  if constexpr (DEPTH == 1) {
+    for (uint32_t kt = k_begin; kt < k_end; kt += BN) step(I0{}, kt);
+  } else {
+    for (uint32_t kt = k_begin; kt < k_end;) {
+      step(I0{}, kt);
+      kt += BN;
+      if (kt >= k_end) break;
+      step(I1{}, kt);
+      kt += BN;
+    }
   }
 
   const float lt = l + __shfl_xor(l, 32);
+  if (slot != kNoSlot) {  // a split decode sequence: unnormalised partial
+    if (row_ok) {
+      const size_t idx = (size_t)slot * a.n_heads + head;
+      float *op = a.ws_acc + idx * HD;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4)
+          *reinterpret_cast<float4 *>(op + dt * 32 + 8 * q4 + 4 * hl) =
+              make_float4(o[dt][4 * q4], o[dt][4 * q4 + 1], o[dt][4 * q4 + 2],
+                          o[dt][4 * q4 + 3]);
+      if (hl == 0) {
+        a.ws_ml[idx * 2] = m;
+        a.ws_ml[idx * 2 + 1] = lt;
+      }
+    }
+    return;
+  }
   const float inv = lt > 0.f ? 1.0f / lt : 0.f;
   if (row_ok) {
     float *op = a.out + qrow * HD;
@@ -458,7 +535,7 @@ __global__ void __launch_bounds__(64 * WAVES,
 template <int HD, int WAVES>
 void launch_prefill(const PrefillArgs &a, dim3 grid, hipStream_t st) {
   hipLaunchKernelGGL((prefill_kernel<HD, WAVES>), grid, dim3(64 * WAVES),
-                     Lds<HD>::bytes, st, a);
+                     (Lds<HD, WAVES>::bytes), st, a);
 }
 
 // Waves per workgroup: 8 at head_dim 128 (measured ~5 % faster than 4);
@@ -558,3 +635,59 @@ int rvkv_paged_prefill(rvkv_pool *pool, uint32_t layer, const float *q,
 }
 
 }  // extern "C"
+
+namespace rvkv_detail {
+
+bool mfma_decode_wanted(const rvkv_pool *pool, uint32_t n_heads) {
+  static const char *env = getenv("RVKV_DECODE_MFMA");
+  const uint32_t group = pool->n_kv ? n_heads / pool->n_kv : 0;
+  const bool shape_ok = pool->head_dim == 64 && group >= 1 && group <= 32 &&
+                        pool->block_size >= 8 &&
+                        (pool->block_size & (pool->block_size - 1)) == 0 &&
+                        pool->block_size <= 256;
+  if (env && env[0] == '0') return false;
+  if (env && env[0] == '1') return shape_ok;
+  return shape_ok && group >= 5;
+}
+
+int mfma_decode(const rvkv_pool *pool, uint32_t layer, const float *q,
+                const uint32_t *tables, const uint32_t *ctx_lens,
+                uint32_t max_blocks, uint32_t n_heads, float scale,
+                int32_t window, const uint4 *items, uint32_t n_items,
+                float *ws_acc, float *ws_ml, float *out) {
+  const char *op = "paged_decode";
+  if (n_items == 0) return RVKV_OK;
+  PrefillArgs a{};
+  a.q = q;
+  a.out = out;
+  a.kc = pool->tensor(layer, 0);
+  a.vc = pool->tensor(layer, 1);
+  a.tables = tables;
+  a.pos_offset = ctx_lens;  // unused in decode mode
+  a.read_num = ctx_lens;
+  a.block_stride = pool->block_elems;
+  a.head_stride = pool->block_size * pool->head_dim;
+  a.q_len = 1;
+  a.max_blocks = max_blocks;
+  a.num_blocks = pool->num_blocks;
+  a.n_heads = n_heads;
+  a.group = n_heads / pool->n_kv;
+  uint32_t lg = 0;
+  while ((1u << lg) < pool->block_size) ++lg;
+  a.bs_log2 = lg;
+  a.rows = a.group;
+  a.n_tiles = 1;
+  a.qscale = scale * 1.4426950408889634f;
+  a.window = window;
+  a.batch = 0;
+  a.n_kv = pool->n_kv;
+  a.items = items;
+  a.ws_acc = ws_acc;
+  a.ws_ml = ws_ml;
+  hipLaunchKernelGGL((prefill_kernel<64, 1>), dim3(n_items, pool->n_kv),
+                     dim3(64), (Lds<64, 1>::bytes), pool->stream, a);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? RVKV_OK : hip_fail(op, e);
+}
+
+}  // namespace rvkv_detail

@@ -1314,6 +1314,26 @@ int launch_decode_pair(const char *op, const DecodeArgs &a, uint32_t hd,
   return e == hipSuccess ? RVKV_OK : hip_fail(op, e);
 }
 
+int launch_reduce(const char *op, const DecodeArgs &a, uint32_t hd,
+                  dim3 rgrid, hipStream_t st) {
+  switch (hd) {
+    case 32: hipLaunchKernelGGL(decode_reduce_kernel<32>, rgrid, dim3(64), 0, st, a); break;
+    case 64: hipLaunchKernelGGL(decode_reduce_kernel<64>, rgrid, dim3(64), 0, st, a); break;
+    case 128: hipLaunchKernelGGL(decode_reduce_kernel<128>, rgrid, dim3(64), 0, st, a); break;
+    default: hipLaunchKernelGGL(decode_reduce_kernel<256>, rgrid, dim3(64), 0, st, a); break;
+  }
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? RVKV_OK : hip_fail(op, e);
+}
+
+}  // namespace
+
+struct rvkv_decode_plan;
+
+namespace {
+int planned_mfma(const char *op, const rvkv_pool *pool,
+                 const rvkv_decode_plan *plan, uint32_t layer,
+                 const DecodeArgs &a, uint32_t max_blocks, float scale);
 }  // namespace
 
 struct rvkv_decode_plan {
@@ -1329,6 +1349,21 @@ struct rvkv_decode_plan {
 };
 
 namespace {
+
+// A planned decode on the matrix cores (large GQA groups): the plan's work
+// items through the prefill kernel in decode mode, which writes the output
+// of whole-context items and the partials of split ones; then the same
+// reduction pass as the VALU decode.
+int planned_mfma(const char *op, const rvkv_pool *pool,
+                 const rvkv_decode_plan *plan, uint32_t layer,
+                 const DecodeArgs &a, uint32_t max_blocks, float scale) {
+  int rc = rvkv_detail::mfma_decode(
+      pool, layer, a.q, a.tables, a.ctx_lens, max_blocks, plan->n_heads,
+      scale, plan->window, a.items, plan->n_items, a.ws_acc, a.ws_ml, a.out);
+  if (rc || plan->n_reds == 0) return rc;
+  return launch_reduce(op, a, pool->head_dim, dim3(plan->n_heads, plan->n_reds),
+                       pool->stream);
+}
 
 // (Re)builds the work list of `pl` for these context lengths and uploads it
 // on the pool's stream. Device-side ordering after earlier decodes comes from
@@ -1353,9 +1388,13 @@ int plan_build(rvkv_decode_plan *pl, const uint32_t *ctx_lens_host,
   }
   // Tokens per work item: about one sequence, but at least enough that the
   // grid has <= ~1024 workgroups and at most what keeps >= ~256 of them.
-  const double avg = (double)total / batch;
-  const double lo_p = (double)total * n_hy / 1024.0;
-  const double hi_p = (double)total * n_hy / 256.0;
+  // The matrix-core decode runs one wave per item (the VALU decode four),
+  // so it gets items a quarter as long and four times as many.
+  const bool mfma = rvkv_detail::mfma_decode_wanted(pool, pl->n_heads);
+  const double per = mfma ? 4.0 : 1.0;
+  const double avg = (double)total / batch / per;
+  const double lo_p = (double)total * n_hy / (1024.0 * per);
+  const double hi_p = (double)total * n_hy / (256.0 * per);
   double want = avg < lo_p ? lo_p : avg;
   if (want > hi_p) want = hi_p;
   uint32_t P = 256;
@@ -1551,6 +1590,8 @@ int rvkv_paged_decode_planned(const rvkv_pool *pool,
   a.reds = plan->d_buf + plan->n_items;
   a.part_tokens = plan->part_tokens;
   a.n_parts = 1;
+  if (rvkv_detail::mfma_decode_wanted(pool, plan->n_heads))
+    return planned_mfma(op, pool, plan, layer, a, max_blocks, scale);
   const dim3 grid(plan->n_items, pool->n_kv * a.n_sub, 1);
   return launch_decode_pair(op, a, pool->head_dim, gt, grid,
                             dim3(plan->n_heads, plan->n_reds ? plan->n_reds : 1),
@@ -1601,6 +1642,14 @@ int rvkv_decode_step(rvkv_pool *pool, const rvkv_decode_plan *plan,
     a.reds = plan->d_buf + plan->n_items;
     a.part_tokens = plan->part_tokens;
     a.n_parts = 1;
+    if (rvkv_detail::mfma_decode_wanted(pool, n_heads)) {
+      // The matrix-core decode reads the appended rows from the cache, so
+      // the append runs first (one more launch).
+      if ((rc = rvkv_append(pool, layer, k, v, src_dtype, slot_block,
+                            slot_off, batch)))
+        return rc;
+      return planned_mfma(op, pool, plan, layer, a, max_blocks, scale);
+    }
     const dim3 grid(plan->n_items, pool->n_kv * a.n_sub, 1);
     return launch_decode_pair(
         op, a, pool->head_dim, gt, grid,
