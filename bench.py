@@ -641,6 +641,22 @@ def main():
             raise SystemExit("--graph cannot capture the per-step plan "
                              "rebuild; use --no-plan with --graph")
 
+    # The library's choice for planned decodes of large groups (hd 64,
+    # group >= 5): the matrix-core decode, preceded by its own append.
+    mfma = (plan is not None and c.head_dim == 64 and
+            c.n_heads // c.n_kv_heads >= 5 and
+            os.environ.get("RVKV_DECODE_MFMA", "") != "0")
+    if mfma:
+        decode_kernels = ("prefill_kernel<64, 1> in decode mode (matrix "
+                          "cores) + decode_reduce_kernel for split sequences"
+                          + ("" if args.unfused else
+                             ", after append_kernel (rvkv_decode_step)"))
+    else:
+        decode_kernels = ("decode_part_kernel (+ decode_reduce_kernel for "
+                          "split sequences)" + ("" if args.unfused else
+                                                ", fused append "
+                                                "(rvkv_decode_step)"))
+
     def decode(layer):
         if args.unfused:
             if plan is not None:
@@ -746,9 +762,7 @@ def main():
         "tok_per_s": round(B / dt, 1),
         "roofline": {
             "bound": "hbm",
-            "kernel": ("decode_part_kernel (+ decode_reduce_kernel for split "
-                       "sequences)" + ("" if args.unfused else
-                                       ", fused append (rvkv_decode_step)")),
+            "kernel": decode_kernels,
             "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

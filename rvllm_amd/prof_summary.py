@@ -3,7 +3,8 @@
     python -m rvllm_amd.prof_summary stats <kernel_stats.csv> [--cmd "..."]
     python -m rvllm_amd.prof_summary traffic --fetch <counter_collection.csv>
         --write <counter_collection.csv> --copy-fetch <...> --copy-write <...>
-        --copy-bytes N --kernel decode_part_kernel [--launch-bytes N]
+        --copy-bytes N --kernel "decode_part_kernel[|other|...]"
+        [--launch-bytes N]
 
 `stats` prints a markdown table of per-kernel calls / average / total time.
 `traffic` prints the mean FETCH_SIZE and WRITE_SIZE (KiB per dispatch) of
@@ -69,8 +70,19 @@ def main(argv=None):
             print(f"| `{n}` | {c} | {avg / 1e3:.2f} | {tot / 1e6:.3f} | "
                   f"{pct:.1f} | {mn / 1e3:.2f} | {mx / 1e3:.2f} |")
         return
-    kf, fetch = _pick(counter_means(args.fetch, "FETCH_SIZE"), args.kernel)
-    _, write = _pick(counter_means(args.write, "WRITE_SIZE"), args.kernel)
+    # --kernel may list several kernels ("|"-separated: kernel names hold
+    # commas) that together make one launch of the measured call; their
+    # per-dispatch means add.
+    fm = counter_means(args.fetch, "FETCH_SIZE")
+    wm = counter_means(args.write, "WRITE_SIZE")
+    names, fetch, write = [], 0.0, 0.0
+    for needle in args.kernel.split("|"):
+        kf, f = _pick(fm, needle)
+        _, w = _pick(wm, needle)
+        names.append(kf)
+        fetch += f
+        write += w
+    kf = " + ".join(names)
     _, cfetch = _pick(counter_means(args.copy_fetch, "FETCH_SIZE"),
                       args.copy_kernel)
     _, cwrite = _pick(counter_means(args.copy_write, "WRITE_SIZE"),
