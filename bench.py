@@ -504,13 +504,19 @@ def run_churn(args, torch, W):
                       steps=args.warmup + args.steps + 1)
     for _ in range(args.warmup):
         drv.step()
+    evs = [torch.cuda.Event(enable_timing=True)
+           for _ in range(args.steps + 1)]
     torch.cuda.synchronize()
     b0 = drv.bytes_moved
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    evs[0].record()
+    for i in range(args.steps):
         drv.step()
+        evs[i + 1].record()
     torch.cuda.synchronize()
     dt = (time.perf_counter() - t0) / args.steps
+    step_median_ms = float(np.median([evs[i].elapsed_time(evs[i + 1])
+                                      for i in range(args.steps)]))
     step_bytes = (drv.bytes_moved - b0) / args.steps
     # Per-launch decode time at the final state (back-to-back over layers).
     st, plan = drv.st, drv.plan
