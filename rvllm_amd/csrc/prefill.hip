@@ -91,7 +91,12 @@ struct Lds {
   static constexpr int VS = BN + 8;  // Vt row stride in halves
   static constexpr size_t k_bytes = (size_t)BN * KS * 2;
   static constexpr size_t v_bytes = (size_t)HD * VS * 2;
-  static constexpr size_t bytes = k_bytes + v_bytes + BN;  // + key flags
+  // Workgroups of several waves double-buffer the tile, so one barrier a
+  // tile both publishes it and retires the buffer the next tile overwrites
+  // (a one-wave workgroup orders its own LDS accesses).
+  static constexpr int NBUF = WAVES > 1 ? 2 : 1;
+  static constexpr size_t buf = (k_bytes + v_bytes + BN + 15) / 16 * 16;
+  static constexpr size_t bytes = NBUF * buf;  // + key flags in each buffer
 };
 
 // max(a, b, c) in one v_max3_f32. Written as an instruction because the
@@ -134,9 +139,6 @@ __global__ void __launch_bounds__(
   constexpr int CHK = BN * CPR / NTH;         // K chunks per thread per tile
   static_assert(CHK >= 1 && BN * CPR % NTH == 0, "tile/thread mismatch");
   extern __shared__ __align__(16) unsigned char smem[];
-  uint16_t *ks = reinterpret_cast<uint16_t *>(smem);
-  uint16_t *vt = reinterpret_cast<uint16_t *>(smem + LD::k_bytes);
-  uint8_t *kok = smem + LD::k_bytes + LD::v_bytes;
 
   // XCD-aware order: workgroups are dispatched round-robin over the 8 XCDs
   // (each with its own L2), so workgroup w runs on XCD w % 8. Renumber so
@@ -342,7 +344,15 @@ __global__ void __launch_bounds__(
     constexpr int si = decltype(S)::value;
     // Every key of the tile readable: all blocks valid, tile inside k_end.
     const bool tile_ok = all_ok && kt + BN <= k_end;
-    __syncthreads();  // the previous tile is no longer read
+    // Tile i uses buffer i % NBUF; with two, every wave has passed the
+    // previous tile's barrier, so none still reads tile i - 2's buffer.
+    unsigned char *lb =
+        smem + (LD::NBUF == 2 ? ((kt - k_begin) / BN) & 1u : 0u) * LD::buf;
+    uint16_t *ks = reinterpret_cast<uint16_t *>(lb);
+    uint16_t *vt = reinterpret_cast<uint16_t *>(lb + LD::k_bytes);
+    uint8_t *kok = lb + LD::k_bytes + LD::v_bytes;
+    if constexpr (LD::NBUF == 1)
+      __syncthreads();  // the previous tile is no longer read
 #pragma unroll
     for (int i = 0; i < CHK; ++i) {
       const int c = tid + NTH * i;
@@ -534,6 +544,15 @@ __global__ void __launch_bounds__(
 
 template <int HD, int WAVES>
 void launch_prefill(const PrefillArgs &a, dim3 grid, hipStream_t st) {
+  // Past 64 KiB (head_dim 128 and 256 double-buffered) the dynamic LDS size
+  // is declared to the runtime once per instantiation.
+  if constexpr (Lds<HD, WAVES>::bytes > 65536) {
+    static const hipError_t set = hipFuncSetAttribute(
+        reinterpret_cast<const void *>(&prefill_kernel<HD, WAVES>),
+        hipFuncAttributeMaxDynamicSharedMemorySize,
+        (int)Lds<HD, WAVES>::bytes);
+    (void)set;  // a refusal shows as the launch's own error
+  }
   hipLaunchKernelGGL((prefill_kernel<HD, WAVES>), grid, dim3(64 * WAVES),
                      (Lds<HD, WAVES>::bytes), st, a);
 }
