@@ -108,6 +108,22 @@ __device__ __forceinline__ float vmax3(float a, float b, float c) {
   return r;
 }
 
+// Lanes i and i ^ 32 combined: v_permlane32_swap exchanges the wave's two
+// 32-lane halves in the VALU (no LDS round trip as for a bpermute).
+__device__ __forceinline__ float max_halves(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v),
+                                                  __float_as_uint(v), false,
+                                                  false);
+  return vmax3(__uint_as_float(r[0]), __uint_as_float(r[1]),
+               __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_halves(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v),
+                                                  __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 __device__ __forceinline__ uint32_t lo_bound(uint32_t p, int32_t window) {
   return (window > 0 && p + 1 > (uint32_t)window) ? p + 1 - (uint32_t)window
                                                   : 0u;
@@ -289,7 +305,8 @@ __global__ void __launch_bounds__(
     v_off[j] = ((v_key[j] & bs_mask) * HD + (c / NPR) * 8) * 2;
     v_db[j] = v_key[j] >> a.bs_log2;
   }
-  const uint64_t blk_bytes = a.block_stride * 2;
+  // (one block of all heads is far below 4 GiB; checked on the host)
+  const uint32_t blk_bytes = (uint32_t)(a.block_stride * 2);
   // Tiles in flight: one ahead, or two for one-wave (decode) workgroups,
   // whose single wave's compute per tile is shorter than a load's latency.
   // Register sets are selected by a compile-time index (a runtime index
@@ -311,6 +328,26 @@ __global__ void __launch_bounds__(
   auto load = [&](auto S, uint32_t kt) {
     constexpr int si = decltype(S)::value;
     const uint32_t t_off = (kt & bs_mask) * HD * 2;  // 0 unless bs > 64
+    if (all_ok && kt + BN <= k_end) {
+      // Every key of the tile is below k_end and every block valid: no
+      // flags, no id checks (the common case, uniform).
+      kbits[si] = ~0u;
+      vbits[si] = ~0u;
+#pragma unroll
+      for (int i = 0; i < CHK; ++i)
+        kr[si][i] = *reinterpret_cast<const u32x4 *>(
+            kbase + (uint64_t)kid[i] * blk_bytes + (t_off + k_off[i]));
+      if (v_lane) {
+#pragma unroll
+        for (int j = 0; j < CHV; ++j) {
+          const char *vp =
+              vbase + (uint64_t)vid[j] * blk_bytes + (t_off + v_off[j]);
+          vr0[si][j] = *reinterpret_cast<const u32x4 *>(vp);
+          vr1[si][j] = *reinterpret_cast<const u32x4 *>(vp + HD * 2);
+        }
+      }
+      return;
+    }
     kbits[si] = 0;
     vbits[si] = 0;
 #pragma unroll
@@ -320,8 +357,8 @@ __global__ void __launch_bounds__(
       const bool okb = kid[i] < a.num_blocks;
       kbits[si] |= (uint32_t)(okb && kt + k_key[i] < k_end) << i;
       kr[si][i] = *reinterpret_cast<const u32x4 *>(
-          kbase + (uint64_t)(okb ? kid[i] : 0u) * blk_bytes + t_off +
-          k_off[i]);
+          kbase + (uint64_t)(okb ? kid[i] : 0u) * blk_bytes +
+          (t_off + k_off[i]));
     }
 #pragma unroll
     for (int j = 0; j < CHV; ++j) {
@@ -330,7 +367,7 @@ __global__ void __launch_bounds__(
       vbits[si] |= (uint32_t)(okb && tok < k_end) << (2 * j);
       vbits[si] |= (uint32_t)(okb && tok + 1 < k_end) << (2 * j + 1);
       const char *vp = vbase + (uint64_t)(okb ? vid[j] : 0u) * blk_bytes +
-                       t_off + v_off[j];
+                       (t_off + v_off[j]);
       if (v_lane) {
         vr0[si][j] = *reinterpret_cast<const u32x4 *>(vp);
         vr1[si][j] = *reinterpret_cast<const u32x4 *>(vp + HD * 2);
@@ -426,6 +463,10 @@ __global__ void __launch_bounds__(
 #pragma unroll
         for (int j = 0; j < 16; j += 2) mx = vmax3(mx, s[t][j], s[t][j + 1]);
     } else {
+      // Register j of sub-tile t holds key kt + 8hl + c, c = 32t + 16(j/8)
+      // + j%8 (a constant): valid for lo <= c < hi and a readable block.
+      const int32_t lo = (int32_t)(row_lo - kt) - 8 * hl;
+      const int32_t hi = (int32_t)(row_hi - kt) - 8 * hl;
 #pragma unroll
       for (int t = 0; t < NT; ++t)
 #pragma unroll
@@ -435,16 +476,16 @@ __global__ void __launch_bounds__(
               all_ok ? ~0ull : *reinterpret_cast<const uint64_t *>(kok + k0);
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            const uint32_t key = kt + k0 + e;
+            const int32_t c = 32 * t + 16 * g8 + e;
             const bool valid = (all_ok || ((okw >> (8 * e)) & 1u)) &&
-                               key >= row_lo && key < row_hi;
+                               c >= lo && c < hi;
             const float x = valid ? s[t][8 * g8 + e] : -__builtin_inff();
             s[t][8 * g8 + e] = x;
             mx = fmaxf(mx, x);
           }
         }
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    mx = max_halves(mx);
     // Lazy rescale: the reference max m moves only when the tile's max
     // exceeds it by more than 2^8, so probabilities stay <= 256 (exact
     // in f16's range) and O and l are rescaled on few tiles; the final
@@ -510,7 +551,7 @@ __global__ void __launch_bounds__(
     }
   }
 
-  const float lt = l + __shfl_xor(l, 32);
+  const float lt = sum_halves(l);
   if (slot != kNoSlot) {  // a split decode sequence: unnormalised partial
     if (row_ok) {
       const size_t idx = (size_t)slot * a.n_heads + head;
@@ -601,6 +642,8 @@ int rvkv_paged_prefill(rvkv_pool *pool, uint32_t layer, const float *q,
     return fail(RVKV_EINVAL, op, "q and out must be 16-byte aligned");
   if ((uint64_t)max_blocks * bs > 0x80000000ull)
     return fail(RVKV_EUNSUPPORTED, op, "max_blocks * block_size too large");
+  if (pool->block_elems * 2 >= 0x100000000ull)
+    return fail(RVKV_EUNSUPPORTED, op, "one block of all heads is >= 4 GiB");
   const uint64_t rows = (uint64_t)(n_heads / pool->n_kv) * q_len;
   if (rows > 0x7fffffffull)
     return fail(RVKV_EUNSUPPORTED, op, "q_len too large for one launch");
@@ -661,6 +704,7 @@ bool mfma_decode_wanted(const rvkv_pool *pool, uint32_t n_heads) {
   static const char *env = getenv("RVKV_DECODE_MFMA");
   const uint32_t group = pool->n_kv ? n_heads / pool->n_kv : 0;
   const bool shape_ok = pool->head_dim == 64 && group >= 1 && group <= 32 &&
+                        pool->block_elems * 2 < 0x100000000ull &&
                         pool->block_size >= 8 &&
                         (pool->block_size & (pool->block_size - 1)) == 0 &&
                         pool->block_size <= 256;
