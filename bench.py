@@ -97,6 +97,40 @@ def copy_calibration(torch, steps):
         "GB/s": round(2 * n * 4 / (ms * 1e-3) / 1e9, 1)}}), flush=True)
 
 
+def read_ceiling(torch, nbytes, steps):
+    """The plain streaming-read rate at one launch's size: rvkv_read_probe
+    (16-byte loads, 2048 contiguous slices, nothing written) timed with HIP
+    events over buffers of `nbytes`, rotated so at least 1.5 GiB separates
+    two reads of one buffer (no MALL reuse, as for the layer launches)."""
+    import ctypes
+
+    from rvllm_amd import _lib
+    lib = _lib.load()
+    nb = (int(nbytes) + 15) // 16 * 16
+    n_buf = max(2, -(-(3 << 29) // nb))
+    bufs = [torch.zeros(nb // 4, dtype=torch.int32, device="cuda")
+            for _ in range(n_buf)]
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def sweep():
+        for b in bufs:
+            _lib.check(lib.rvkv_read_probe(ctypes.c_void_p(b.data_ptr()), nb,
+                                           0, None, stream))
+    sweep()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        sweep()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / (steps * n_buf)
+    del bufs
+    return {"bytes_per_launch": nb, "avg_launch_ms": round(ms, 5),
+            "GB/s": round(nb / (ms * 1e-3) / 1e9, 2)}
+
+
 def measured_traffic(config, batch, unfused, ctx=0):
     """HBM bytes per decode launch measured by rocprofv3 --pmc (FETCH_SIZE +
     WRITE_SIZE, each scaled by the same counter's reading for a copy of
@@ -778,6 +812,10 @@ def main():
             "avg_launch_ms": round(dec_ms, 5),
         },
     }
+    # Context for frac: the best plain read of the same bytes per launch.
+    rc = read_ceiling(torch, dec_bytes, max(args.steps, 3))
+    rc["frac"] = round(achieved / rc["GB/s"], 4)
+    res["roofline"]["stream_read_ceiling"] = rc
     if not args.no_cpu:
         from oracle import oracle as orc
         res["cpu_baseline"] = cpu_baseline(orc, W, st, db, args.cpu_seconds)

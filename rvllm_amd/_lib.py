@@ -71,6 +71,7 @@ SIGNATURES = {
     "rvkv_bm_refcount": (_u32, [_P, _u32]),
     "rvkv_bm_table": (_int, [_P, _i64, _pu32, _u32]),
     "rvkv_argmax": (_int, [_P, _u32, _u32, _P, _P]),
+    "rvkv_read_probe": (_int, [_P, _sz, _u32, _P, _P]),
     "rvkv_sched_last_error": (ctypes.c_char_p, []),
     "rvkv_sched_create": (_P, [_u32, _u32]),
     "rvkv_sched_destroy": (None, [_P]),

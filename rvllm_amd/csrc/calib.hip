@@ -1,0 +1,62 @@
+// calib.hip - the streaming-read calibration the roofline figures are read
+// against: how fast this device reads a buffer of a given size once, with
+// nothing else in the launch (no tables, no arithmetic worth the name).
+// It has no counterpart in rvllm; it exists so a paged-KV launch of B bytes
+// can be compared with the best plain read of B bytes on the same device.
+//
+// Each workgroup streams one contiguous slice with 16-byte loads, four in
+// flight per lane, and folds them into a sum that is stored only if it
+// equals an impossible sentinel (so the loads are not optimised away and
+// nothing is written).
+#include "pool.h"
+
+using rvkv_detail::fail;
+using rvkv_detail::hip_fail;
+
+namespace {
+
+constexpr int kReadThreads = 256;
+constexpr int kReadUnroll = 4;
+
+__global__ void __launch_bounds__(kReadThreads)
+    read_probe_kernel(const uint4 *__restrict__ buf, uint64_t n16,
+                      uint64_t per_wg, uint32_t *__restrict__ sink) {
+  const uint64_t lo = (uint64_t)blockIdx.x * per_wg;
+  const uint64_t hi = lo + per_wg < n16 ? lo + per_wg : n16;
+  uint32_t acc = 0;
+  for (uint64_t i = lo + threadIdx.x; i < hi;
+       i += (uint64_t)kReadThreads * kReadUnroll) {
+    uint4 v[kReadUnroll];
+#pragma unroll
+    for (int u = 0; u < kReadUnroll; ++u) {
+      const uint64_t j = i + (uint64_t)u * kReadThreads;
+      v[u] = j < hi ? buf[j] : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < kReadUnroll; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+  }
+  if (acc == 0x9e3779b9u && sink) sink[0] = acc;  // practically never
+}
+
+}  // namespace
+
+extern "C" {
+
+int rvkv_read_probe(const void *buf, size_t bytes, uint32_t workgroups,
+                    uint32_t *sink, rvkv_stream stream) {
+  const char *op = "read_probe";
+  if (bytes == 0) return RVKV_OK;
+  if (!buf) return fail(RVKV_EINVAL, op, "buf is NULL");
+  if ((uintptr_t)buf % 16 || bytes % 16)
+    return fail(RVKV_EINVAL, op, "buf and bytes must be 16-byte aligned");
+  if (workgroups == 0) workgroups = 2048;
+  const uint64_t n16 = bytes / 16;
+  const uint64_t per_wg = (n16 + workgroups - 1) / workgroups;
+  hipLaunchKernelGGL(read_probe_kernel, dim3(workgroups), dim3(kReadThreads),
+                     0, reinterpret_cast<hipStream_t>(stream),
+                     static_cast<const uint4 *>(buf), n16, per_wg, sink);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? RVKV_OK : hip_fail(op, e);
+}
+
+}  // extern "C"
