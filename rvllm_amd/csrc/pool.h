@@ -35,5 +35,8 @@ int mfma_decode(const rvkv_pool *pool, uint32_t layer, const float *q,
                 const uint32_t *tables, const uint32_t *ctx_lens,
                 uint32_t max_blocks, uint32_t n_heads, float scale,
                 int32_t window, const uint4 *items, uint32_t n_items,
-                float *ws_acc, float *ws_ml, float *out);
+                float *ws_acc, float *ws_ml, float *out,
+                const void *new_k = nullptr, const void *new_v = nullptr,
+                const uint32_t *new_blk = nullptr,
+                const uint32_t *new_off = nullptr, bool new_f32 = false);
 }  // namespace rvkv_detail

@@ -80,6 +80,13 @@ struct PrefillArgs {
   // ws_ml [slot][n_heads] for the decode reduction pass. NULL: prefill.
   const uint4 *items;
   float *ws_acc, *ws_ml;
+  // Fused append (decode mode): this step's K/V row of every sequence
+  // ([batch, n_kv, hd], f32 or f16) goes to slot (new_blk[b], new_off[b])
+  // and is the key at position ctx - 1; the work item holding that key
+  // stores the row and uses it from registers. NULL: no append.
+  const void *new_k, *new_v;
+  const uint32_t *new_blk, *new_off;
+  bool new_f32;
 };
 
 constexpr uint32_t kNoSlot = 0xFFFFFFFFu;
@@ -122,6 +129,31 @@ __device__ __forceinline__ float sum_halves(float v) {
                                                   __float_as_uint(v), false,
                                                   false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Eight elements of an appended K or V row as f16, rounded to nearest even
+// from an f32 source exactly as the append kernel does.
+__device__ __forceinline__ u32x4 new_row_chunk(const void *src, bool f32,
+                                               size_t elem) {
+  u32x4 r;
+  if (f32) {
+    const float4 *p =
+        reinterpret_cast<const float4 *>(static_cast<const float *>(src) + elem);
+    const float4 x = p[0], y = p[1];
+    auto pk = [](float lo, float hi) {
+      const _Float16 l = (_Float16)lo, h = (_Float16)hi;
+      return (uint32_t)__builtin_bit_cast(uint16_t, l) |
+             ((uint32_t)__builtin_bit_cast(uint16_t, h) << 16);
+    };
+    r[0] = pk(x.x, x.y);
+    r[1] = pk(x.z, x.w);
+    r[2] = pk(y.x, y.y);
+    r[3] = pk(y.z, y.w);
+  } else {
+    r = *reinterpret_cast<const u32x4 *>(static_cast<const uint16_t *>(src) +
+                                         elem);
+  }
+  return r;
 }
 
 __device__ __forceinline__ uint32_t lo_bound(uint32_t p, int32_t window) {
@@ -224,6 +256,11 @@ __global__ void __launch_bounds__(
   const uint32_t row_hi = row_ok ? min(min(ctx, p + 1u), item_hi) : 0u;
   const uint32_t row_lo = max(lo_bound(p, a.window), item_lo);
   const size_t qrow = ((size_t)b * a.q_len + qi) * a.n_heads + head;
+  // The appended key (fused decode step) when this item holds it.
+  const uint32_t newtok =
+      (a.new_k && ctx >= 1u && ctx - 1u >= item_lo && ctx - 1u < item_hi)
+          ? ctx - 1u
+          : 0xFFFFFFFFu;
 
   half8 qf[KC];
   {
@@ -325,6 +362,14 @@ __global__ void __launch_bounds__(
 #pragma unroll
     for (int j = 0; j < CHV; ++j) vid[j] = table[min(b0 + v_db[j], last)];
   };
+  // Fused append (decode mode only: the one-wave instantiation): the item
+  // holding the appended key loads the new K/V row into registers (after
+  // its first tiles' loads are out), writes it into LDS over whatever the
+  // cache held in the tile holding that key, and stores it to its slot at
+  // the end (lanes < CPR, one 16-byte chunk each).
+  u32x4 new_kc{}, new_vc{};
+  uint16_t new_ve = 0;  // V element tid of the new row (f16 bits)
+  const size_t new_src = ((size_t)b * a.n_kv + kvh) * HD;
   auto load = [&](auto S, uint32_t kt) {
     constexpr int si = decltype(S)::value;
     const uint32_t t_off = (kt & bs_mask) * HD * 2;  // 0 unless bs > 64
@@ -427,6 +472,15 @@ __global__ void __launch_bounds__(
                 mask;
           }
         }
+      }
+    }
+    if constexpr (WAVES == 1) {
+      if (newtok - kt < (uint32_t)BN) {  // this tile holds the new key
+        const uint32_t r = newtok - kt;
+        if (tid < CPR)
+          *reinterpret_cast<u32x4 *>(ks + r * KS + tid * 8) = new_kc;
+        if (tid < HD) vt[tid * VS + r] = new_ve;
+        if (!all_ok && tid == 0) kok[r] = 1;
       }
     }
     __syncthreads();
@@ -539,6 +593,22 @@ __global__ void __launch_bounds__(
       fetch_ids(k_begin + 2 * BN);
     }
   }
+  if constexpr (WAVES == 1) {
+    if (newtok != 0xFFFFFFFFu) {
+      if (tid < CPR) {
+        new_kc = new_row_chunk(a.new_k, a.new_f32, new_src + tid * 8);
+        new_vc = new_row_chunk(a.new_v, a.new_f32, new_src + tid * 8);
+      }
+      if (tid < HD) {
+        const _Float16 v =
+            a.new_f32
+                ? (_Float16) static_cast<const float *>(a.new_v)[new_src + tid]
+                : __builtin_bit_cast(_Float16, static_cast<const uint16_t *>(
+                                                   a.new_v)[new_src + tid]);
+        new_ve = __builtin_bit_cast(uint16_t, v);
+      }
+    }
+  }
   if constexpr (DEPTH == 1) {
     for (uint32_t kt = k_begin; kt < k_end; kt += BN) step(I0{}, kt);
   } else {
@@ -551,6 +621,19 @@ __global__ void __launch_bounds__(
     }
   }
 
+  if constexpr (WAVES == 1) {
+    if (newtok != 0xFFFFFFFFu && tid < CPR) {
+      const uint32_t nb = a.new_blk[b], no = a.new_off[b];
+      if (nb < a.num_blocks && no < (1u << a.bs_log2)) {
+        const size_t dst =
+            ((size_t)nb * a.n_kv + kvh) * a.head_stride + (size_t)no * HD;
+        *reinterpret_cast<u32x4 *>(const_cast<uint16_t *>(a.kc) + dst +
+                                   tid * 8) = new_kc;
+        *reinterpret_cast<u32x4 *>(const_cast<uint16_t *>(a.vc) + dst +
+                                   tid * 8) = new_vc;
+      }
+    }
+  }
   const float lt = sum_halves(l);
   if (slot != kNoSlot) {  // a split decode sequence: unnormalised partial
     if (row_ok) {
@@ -717,7 +800,9 @@ int mfma_decode(const rvkv_pool *pool, uint32_t layer, const float *q,
                 const uint32_t *tables, const uint32_t *ctx_lens,
                 uint32_t max_blocks, uint32_t n_heads, float scale,
                 int32_t window, const uint4 *items, uint32_t n_items,
-                float *ws_acc, float *ws_ml, float *out) {
+                float *ws_acc, float *ws_ml, float *out, const void *new_k,
+                const void *new_v, const uint32_t *new_blk,
+                const uint32_t *new_off, bool new_f32) {
   const char *op = "paged_decode";
   if (n_items == 0) return RVKV_OK;
   PrefillArgs a{};
@@ -747,6 +832,11 @@ int mfma_decode(const rvkv_pool *pool, uint32_t layer, const float *q,
   a.items = items;
   a.ws_acc = ws_acc;
   a.ws_ml = ws_ml;
+  a.new_k = new_k;
+  a.new_v = new_v;
+  a.new_blk = new_blk;
+  a.new_off = new_off;
+  a.new_f32 = new_f32;
   hipLaunchKernelGGL((prefill_kernel<64, 1>), dim3(n_items, pool->n_kv),
                      dim3(64), (Lds<64, 1>::bytes), pool->stream, a);
   hipError_t e = hipGetLastError();

@@ -905,26 +905,50 @@ __global__ void __launch_bounds__(64) decode_reduce_kernel(DecodeArgs a) {
     slot0 = b * a.n_parts;
     np = (ctx + a.part_tokens - 1) / a.part_tokens;
   }
+  // Lane i holds partition c + i's (m, l) for the 64-partition chunk at c;
+  // M comes first, then every partial is weighted by 2^(m_i - M): the loads
+  // of different partitions are independent, so they are all in flight at
+  // once instead of one round trip per partition.
+  const float *ml = a.ws_ml + ((size_t)slot0 * a.n_heads + h) * 2;
+  const size_t ml_step = (size_t)a.n_heads * 2;
+  float M = kNegBig;
+  for (uint32_t c = 0; c < np; c += 64) {
+    const uint32_t p = c + lane;
+    if (p < np && ml[p * ml_step + 1] != 0.f) M = fmaxf(M, ml[p * ml_step]);
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
   float acc[EPL];
 #pragma unroll
   for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
-  float M = kNegBig, L = 0.f;
-  for (uint32_t p = 0; p < np; ++p) {
-    const size_t idx = (size_t)(slot0 + p) * a.n_heads + h;
-    const float mp = a.ws_ml[idx * 2], lp = a.ws_ml[idx * 2 + 1];
-    if (lp == 0.f) continue;
-    const float mx = fmaxf(M, mp);
-    const float w_old = __builtin_amdgcn_exp2f(M - mx);
-    const float w_new = __builtin_amdgcn_exp2f(mp - mx);
-    L = L * w_old + lp * w_new;
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) {
-      const int d = lane * EPL + e;
-      const float x = d < HD ? a.ws_acc[idx * HD + d] : 0.f;
-      acc[e] = acc[e] * w_old + x * w_new;
+  float L = 0.f;
+  const float *accp = a.ws_acc + ((size_t)slot0 * a.n_heads + h) * HD;
+  const size_t acc_step = (size_t)a.n_heads * HD;
+  for (uint32_t c = 0; c < np; c += 64) {
+    const uint32_t p = c + lane;
+    float w = 0.f;
+    if (p < np) {
+      const float lp = ml[p * ml_step + 1];
+      // (l = 0: a partition that saw no visible key)
+      if (lp != 0.f) w = __builtin_amdgcn_exp2f(ml[p * ml_step] - M);
+      L += lp * w;
     }
-    M = mx;
+    const uint32_t n = min(np - c, 64u);
+#pragma unroll 8
+    for (uint32_t i = 0; i < n; ++i) {
+      const float wi =
+          __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), i));
+      const float *src = accp + (size_t)(c + i) * acc_step;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) {
+        const int d = lane * EPL + e;
+        const float x = d < HD ? src[d] : 0.f;
+        acc[e] += wi != 0.f ? wi * x : 0.f;  // skipped partials stay out
+      }
+    }
   }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) L += __shfl_xor(L, o);
   const float inv = L > 0.f ? 1.0f / L : 0.f;
   const size_t hrow = (size_t)b * a.n_heads + h;
 #pragma unroll
@@ -1359,7 +1383,8 @@ int planned_mfma(const char *op, const rvkv_pool *pool,
                  const DecodeArgs &a, uint32_t max_blocks, float scale) {
   int rc = rvkv_detail::mfma_decode(
       pool, layer, a.q, a.tables, a.ctx_lens, max_blocks, plan->n_heads,
-      scale, plan->window, a.items, plan->n_items, a.ws_acc, a.ws_ml, a.out);
+      scale, plan->window, a.items, plan->n_items, a.ws_acc, a.ws_ml, a.out,
+      a.new_k, a.new_v, a.new_blk, a.new_off, a.new_f32);
   if (rc || plan->n_reds == 0) return rc;
   return launch_reduce(op, a, pool->head_dim, dim3(plan->n_heads, plan->n_reds),
                        pool->stream);
@@ -1642,14 +1667,8 @@ int rvkv_decode_step(rvkv_pool *pool, const rvkv_decode_plan *plan,
     a.reds = plan->d_buf + plan->n_items;
     a.part_tokens = plan->part_tokens;
     a.n_parts = 1;
-    if (rvkv_detail::mfma_decode_wanted(pool, n_heads)) {
-      // The matrix-core decode reads the appended rows from the cache, so
-      // the append runs first (one more launch).
-      if ((rc = rvkv_append(pool, layer, k, v, src_dtype, slot_block,
-                            slot_off, batch)))
-        return rc;
+    if (rvkv_detail::mfma_decode_wanted(pool, n_heads))
       return planned_mfma(op, pool, plan, layer, a, max_blocks, scale);
-    }
     const dim3 grid(plan->n_items, pool->n_kv * a.n_sub, 1);
     return launch_decode_pair(
         op, a, pool->head_dim, gt, grid,

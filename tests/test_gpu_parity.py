@@ -545,12 +545,14 @@ def test_config_qwen25_planned():
 @pytest.mark.parametrize("planned", [False, True])
 @pytest.mark.parametrize("src", [torch.float32, torch.float16])
 @pytest.mark.parametrize("G,hd,bs,window", [(4, 64, 16, 0), (2, 128, 16, 0),
-                                            (9, 64, 32, 0), (4, 256, 16, 300)])
+                                            (9, 64, 32, 0), (4, 256, 16, 300),
+                                            (7, 64, 16, 500)])
 def test_decode_step_equals_append_then_decode(planned, src, G, hd, bs,
                                                window):
     """rvkv_decode_step leaves the same cache bits as rvkv_append followed by
     the decode (uniform or planned) and the same output up to summation
-    order."""
+    order. Planned with G >= 5 at hd 64 is the matrix-core decode, whose
+    fused append puts the new rows into its tile from registers."""
     from rvllm_amd.kv_storage import HipDecodePlan
     nkv = 2
     lens = np.array([5000, 1, 16, 17, 700, 2049, 64, 333], np.uint32)
