@@ -688,9 +688,9 @@ def main():
             os.environ.get("RVKV_DECODE_MFMA", "") != "0")
     if mfma:
         decode_kernels = ("prefill_kernel<64, 1> in decode mode (matrix "
-                          "cores) + decode_reduce_kernel for split sequences"
-                          + ("" if args.unfused else
-                             ", after append_kernel (rvkv_decode_step)"))
+                          "cores" + ("" if args.unfused else
+                                     ", fused append (rvkv_decode_step)")
+                          + ") + decode_reduce_kernel for split sequences")
     else:
         decode_kernels = ("decode_part_kernel (+ decode_reduce_kernel for "
                           "split sequences)" + ("" if args.unfused else
