@@ -63,6 +63,16 @@ def parse():
     p.add_argument("--prefill-attn", action="store_true",
                    help="time whole-prompt paged prefill attention over the "
                    "uniform batch of --config (default batch 16)")
+    p.add_argument("--gather", choices=["f32", "f16"], default=None,
+                   help="time the block-table gather (rvkv_gather) of the "
+                        "decode workload of --config into rvllm's padded "
+                        "[batch, n_kv, ctx, hd] layout, all layers")
+    p.add_argument("--cow", action="store_true",
+                   help="time the copy-on-write block copy (rvkv_copy_blocks, "
+                        "all layers, K and V) of the prefix sharers' pairs of "
+                        "--config (default qwen2.5-0.5b), or of --cow-blocks "
+                        "random pairs")
+    p.add_argument("--cow-blocks", type=int, default=0)
     p.add_argument("--prep", action="store_true",
                    help="time the fused attention prep + append over the "
                    "prefill batch of --config instead")
@@ -355,6 +365,136 @@ def run_prefill_attn(args, torch, W):
     print(json.dumps(res), flush=True)
 
 
+def _time_launches(torch, fn, n_launch, steps, warmup):
+    """(wall seconds per step, HIP-event ms per launch) of `steps` calls of
+    fn (each making n_launch launches) after `warmup` untimed ones."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    return dt, e0.elapsed_time(e1) / (steps * n_launch)
+
+
+def _hbm_line(metric, value_bytes_per_step, dt, launch_ms, per_launch,
+              kernel, args, config, dtype):
+    achieved = per_launch / (launch_ms * 1e-3) / 1e9
+    return {
+        "metric": metric,
+        "value": round(value_bytes_per_step / dt / 1e9, 2),
+        "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(dt * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": dtype,
+        "data": "synthetic N(0,1)*scale f16 KV, seeded permuted block tables",
+        "config": config,
+        "roofline": {"bound": "hbm", "kernel": kernel,
+                     "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None,
+                     "algorithmic_bytes_per_launch": per_launch,
+                     "avg_launch_ms": round(launch_ms, 5)},
+    }
+
+
+def run_gather(args, torch, W):
+    """The reference's attention read path, materialised: every sequence's
+    K and V gathered through its block table into rvllm's padded
+    [batch, n_kv, ctx_len, hd] (f32 as kv_gather.cu writes it, or f16 raw
+    bits), one rvkv_gather per layer over the decode workload of --config.
+    Algorithmic bytes: the cache rows read (f16) + the padded outputs
+    written + the tables."""
+    from rvllm_amd.kv_storage import HipGatherPlan, HipKvStorage
+    db = build_workload(W, args.config, args.batch, args.ctx)
+    c = db.cfg
+    st = HipKvStorage(c.n_layers, db.num_blocks, c.block_size, c.n_kv_heads,
+                      c.head_dim)
+    fill_pool(torch, st, c.seed, c.value_scale)
+    plan = HipGatherPlan([(db.tables[b], int(db.ctx_lens[b]))
+                          for b in range(db.batch)])
+    dt_out = torch.float32 if args.gather == "f32" else torch.float16
+    n_out = db.batch * c.n_kv_heads * plan.ctx_len * c.head_dim
+    ok = torch.empty(n_out, dtype=dt_out, device="cuda")
+    ov = torch.empty(n_out, dtype=dt_out, device="cuda")
+
+    def step():
+        for layer in range(c.n_layers):
+            st.gather(layer, plan, ok, ov)
+
+    dt, launch_ms = _time_launches(torch, step, c.n_layers, args.steps,
+                                   args.warmup)
+    # Rows read: each sequence's own tokens (padding positions re-read its
+    # last block, already counted); rows written: the whole padded output.
+    read = int(db.ctx_lens.sum()) * c.n_kv_heads * c.head_dim * 2 * 2
+    per_launch = (read + 2 * n_out * ok.element_size() +
+                  4 * db.batch * plan.max_blocks)
+    res = _hbm_line(
+        "block-table gather HBM GB/s, 1 MI355X", per_launch * c.n_layers, dt,
+        launch_ms, per_launch, f"gather_kernel (out {args.gather})", args,
+        {"workload": f"{c.name}: gather of {db.batch} seqs, padded ctx "
+                     f"{plan.ctx_len}, {c.n_kv_heads} kv heads, head_dim "
+                     f"{c.head_dim}, block_size {c.block_size}, "
+                     f"{c.n_layers} layers",
+         "global_batch": db.batch, "seq_len": plan.ctx_len,
+         "parallelism": "single GPU"},
+        f"f16 cache -> {args.gather}")
+    print(json.dumps(res), flush=True)
+    st.close()
+
+
+def run_cow(args, torch, W):
+    """Copy-on-write block copies: the prefix sharers' (shared -> private)
+    pairs of the --config workload (Qwen2.5 by default: sharers whose last
+    block is a partial shared one), or --cow-blocks random distinct pairs;
+    one rvkv_copy_blocks covers every layer, K and V. Algorithmic bytes:
+    each copied block read and written, all layers, K and V."""
+    from rvllm_amd.kv_storage import HipKvStorage
+    # (The default config has no sharers; its pairs come from Qwen2.5.)
+    name = ("qwen2.5-0.5b" if args.config == "llama-3.2-1b" and
+            not args.cow_blocks else args.config)
+    db = build_workload(W, name, args.batch, args.ctx)
+    c = db.cfg
+    st = HipKvStorage(c.n_layers, db.num_blocks, c.block_size, c.n_kv_heads,
+                      c.head_dim)
+    if args.cow_blocks:
+        rng = np.random.default_rng(c.seed + 11)
+        pick = rng.permutation(db.num_blocks)[:2 * args.cow_blocks]
+        src, dst = pick[:args.cow_blocks], pick[args.cow_blocks:]
+    else:
+        src, dst = db.cow_src, db.cow_dst
+    if len(src) == 0:
+        raise SystemExit(f"{name} has no copy-on-write pairs; use "
+                         "--cow-blocks N")
+
+    def u32(a):
+        return torch.from_numpy(np.ascontiguousarray(a, np.uint32)
+                                .view(np.int32).copy()).cuda()
+
+    s_t, d_t = u32(src), u32(dst)
+    dt, launch_ms = _time_launches(
+        torch, lambda: st.copy_blocks(s_t, d_t), 1, args.steps, args.warmup)
+    block_bytes = c.block_size * c.n_kv_heads * c.head_dim * 2
+    per_launch = len(src) * block_bytes * 2 * c.n_layers * 2 + 8 * len(src)
+    res = _hbm_line(
+        "copy-on-write block copy HBM GB/s, 1 MI355X", per_launch, dt,
+        launch_ms, per_launch, "copy_blocks_kernel", args,
+        {"workload": f"{c.name}: {len(src)} block pairs x {c.n_layers} "
+                     f"layers x K/V, block {block_bytes} B",
+         "global_batch": len(src), "seq_len": c.block_size,
+         "parallelism": "single GPU"},
+        "f16 (bit copy)")
+    print(json.dumps(res), flush=True)
+    st.close()
+
+
 def run_prep(args, torch, W):
     """Fused attention prep over a prefill batch: per token, q/k/v rows
     (f32, as the QKV projection leaves them) get the bias, the per-head
@@ -641,6 +781,12 @@ def main():
         return
     if args.prefill_attn:
         run_prefill_attn(args, torch, W)
+        return
+    if args.gather:
+        run_gather(args, torch, W)
+        return
+    if args.cow:
+        run_cow(args, torch, W)
         return
     db = build_workload(W, args.config, args.batch, args.ctx)
     c = db.cfg
