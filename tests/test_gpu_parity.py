@@ -502,6 +502,27 @@ def test_planned_decode_ragged_splits(window):
     assert np.abs(ref - out).max() < ATOL
 
 
+@pytest.mark.parametrize("G", [4, 7])
+def test_decode_reduction_over_more_than_64_partitions(G):
+    """A 40000-token sequence beside a short one, one KV head: the uniform
+    path splits it into ~157 partitions of 256 tokens and the planned path
+    into ~79 items of 512, so the reduction merges more than one
+    64-partition chunk (G 7 planned: the matrix-core decode's partials)."""
+    bs, nkv, hd = 16, 1, 64
+    lens = np.array([40000, 300], np.uint32)
+    cfg = W.Config("long", 9, 1, G * nkv, nkv, hd, bs, len(lens))
+    db = W.ragged_batch(cfg, lens, seed=G)
+    st = HipKvStorage(1, db.num_blocks, bs, nkv, hd)
+    fill_layer(st, 0, seed=5)
+    q = torch.randn(len(lens), G * nkv, hd, device="cuda",
+                    generator=torch.Generator("cuda").manual_seed(G))
+    assert st.decode_partition_tokens(len(lens), G, 40000) * 64 < 40000
+    assert _decode_vs_oracle(st, 0, db, q) < ATOL
+    err, plan, _ = _planned_vs_oracle(st, 0, db, q)
+    assert err < ATOL
+    assert plan.items > 64
+
+
 def test_planned_decode_update_reuses_plan():
     """update() with new lengths (a decode step later, batch change) gives
     the same results as a freshly built plan."""
