@@ -35,6 +35,7 @@
 // denominator see the same weights. Products are exact in f32; sums are f32.
 #include "pool.h"
 
+#include <atomic>
 #include <cmath>
 #include <cstdlib>
 #include <type_traits>
@@ -669,13 +670,19 @@ __global__ void __launch_bounds__(
 template <int HD, int WAVES>
 void launch_prefill(const PrefillArgs &a, dim3 grid, hipStream_t st) {
   // Past 64 KiB (head_dim 128 and 256 double-buffered) the dynamic LDS size
-  // is declared to the runtime once per instantiation.
+  // is declared to the runtime, once per instantiation and device.
   if constexpr (Lds<HD, WAVES>::bytes > 65536) {
-    static const hipError_t set = hipFuncSetAttribute(
-        reinterpret_cast<const void *>(&prefill_kernel<HD, WAVES>),
-        hipFuncAttributeMaxDynamicSharedMemorySize,
-        (int)Lds<HD, WAVES>::bytes);
-    (void)set;  // a refusal shows as the launch's own error
+    static std::atomic<uint64_t> done{0};
+    int dev = 0;
+    if (hipGetDevice(&dev) == hipSuccess && dev < 64 &&
+        !(done.load(std::memory_order_relaxed) >> dev & 1u)) {
+      // (a refusal shows as the launch's own error)
+      if (hipFuncSetAttribute(
+              reinterpret_cast<const void *>(&prefill_kernel<HD, WAVES>),
+              hipFuncAttributeMaxDynamicSharedMemorySize,
+              (int)Lds<HD, WAVES>::bytes) == hipSuccess)
+        done.fetch_or(1ull << dev, std::memory_order_relaxed);
+    }
   }
   hipLaunchKernelGGL((prefill_kernel<HD, WAVES>), grid, dim3(64 * WAVES),
                      (Lds<HD, WAVES>::bytes), st, a);
