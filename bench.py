@@ -5,7 +5,7 @@ append each sequence's new K/V row (f32 source rounded to f16) into its
 slot, then paged GQA decode attention over the full context. Inputs are
 resident in HBM before the timed region. Prints one JSON line.
 
-Default workload: BASELINE configs[1], Llama-3.2-1B shape (16 layers, 32 q
+Default workload: the Llama-3.2-1B shape (16 layers, 32 q
 heads / 8 KV heads, head_dim 64, block_size 16, 64 sequences x 2048 tokens,
 block tables a random permutation of a pool sized for exactly the live
 tokens). Other configs: --config qwen3-0.6b | gemma-3-270m | qwen2.5-0.5b.
@@ -52,12 +52,12 @@ def parse():
                         "(rvkv_append + rvkv_paged_decode) instead of the "
                         "fused rvkv_decode_step")
     p.add_argument("--churn", action="store_true",
-                   help="continuous-batching churn (BASELINE configs[4]): each "
+                   help="continuous-batching churn (gemma-3-270m shape): each "
                         "step 10%% of sequences finish and as many are "
                         "admitted with 64-token prompts, over a fragmented "
                         "pool; --steps counts engine steps")
     p.add_argument("--prefill", choices=["f32", "f16"], default=None,
-                   help="time the prefill append instead (BASELINE configs[2]: "
+                   help="time the prefill append instead (Qwen3 shape: "
                         "every sequence's whole context scattered into the "
                         "paged cache, all layers; source dtype f32 or f16)")
     p.add_argument("--prefill-attn", action="store_true",
@@ -743,7 +743,7 @@ def run_prefill(args, torch, W):
 
 
 def run_churn(args, torch, W):
-    """gemma-3-270m shape, 1024 sequences starting at
+    """The churn workload: gemma-3-270m shape, 1024 sequences starting at
     1024 tokens; every engine step 10% finish and 10% are admitted with
     64-token prompts (prefill append), then all decode one token (fused
     append + decode per layer under a per-step decode plan). The pool is

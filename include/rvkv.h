@@ -61,7 +61,7 @@ enum {
  * ("" if none). Replaces the Box<dyn Error> strings of src/cuda/ops.rs. */
 const char *rvkv_last_error(void);
 
-/* ---- a1: pool ------------------------------------------------------------
+/* ---- pool ------------------------------------------------------------
  * Replaces CudaKvStorage::new (src/cuda/kv_storage.rs:77-100) /
  * KvStorage::new (src/kv_storage.rs:84-104): zeroed K and V storage for
  * n_layers attention layers. One device allocation for all layers; 64-bit
@@ -77,7 +77,7 @@ size_t rvkv_pool_bytes(const rvkv_pool *pool);
 /* Rebinds the pool to another stream on the same device. */
 int rvkv_pool_set_stream(rvkv_pool *pool, rvkv_stream stream);
 
-/* ---- a2: KV append -------------------------------------------------------
+/* ---- KV append -------------------------------------------------------
  * Replaces CudaKvStorage::write_tokens (src/cuda/kv_storage.rs:105-126) ->
  * kv_write_wrapper (src/cuda/ops.rs:313-373) -> kv_write.cu, and the CPU
  * KvStorage::write_tokens (src/kv_storage.rs:116-150).
@@ -91,7 +91,7 @@ int rvkv_append(rvkv_pool *pool, uint32_t layer, const void *k, const void *v,
                 rvkv_dtype src_dtype, const uint32_t *slot_block,
                 const uint32_t *slot_off, uint32_t n_tokens);
 
-/* ---- a4: block-table gather ---------------------------------------------
+/* ---- block-table gather ---------------------------------------------
  * Replaces CudaKvStorage::gather (src/cuda/kv_storage.rs:132-164) ->
  * kv_gather_wrapper (src/cuda/ops.rs:381-445) -> kv_gather.cu, and
  * KvStorage::gather (src/kv_storage.rs:157-173).
@@ -105,7 +105,7 @@ int rvkv_gather(const rvkv_pool *pool, uint32_t layer,
                 uint32_t ctx_len, void *out_k, void *out_v,
                 rvkv_dtype out_dtype);
 
-/* ---- a5 + a6: paged GQA decode attention ---------------------------------
+/* ---- paged GQA decode attention ---------------------------------
  * Replaces, for q_len == 1, the chain kv_gather x2 -> attention_scores ->
  * mask_add_broadcast -> softmax -> attention_apply
  * (src/cuda/model.rs:528-569) and the CPU gather + batch_mask +
@@ -140,7 +140,7 @@ size_t rvkv_decode_workspace_bytes(const rvkv_pool *pool, uint32_t batch,
 uint32_t rvkv_decode_partition_tokens(const rvkv_pool *pool, uint32_t batch,
                                       uint32_t n_heads, uint32_t max_ctx_len);
 
-/* ---- a3 + a5 + a6: planned paged decode (ragged batches) ------------------
+/* ---- planned paged decode (ragged batches) ------------------
  * The counterpart of GatherPlan::new / CudaGatherPlan::new
  * (src/kv_storage.rs:50-75, src/cuda/kv_storage.rs:26-54): built once per
  * forward from the host-side read_num_tokens (BatchItem::read_num_tokens,
@@ -179,7 +179,7 @@ int rvkv_paged_decode_planned(const rvkv_pool *pool,
                               float scale, float *out, void *ws,
                               size_t ws_bytes);
 
-/* ---- a2 + a5 + a6 fused: one layer of a decode step ----------------------
+/* ---- one layer of a decode step ----------------------
  * The per-layer order of src/model.rs:628-644 (write_tokens, then attend
  * over the context including the new token) in ONE launch: row b of k/v
  * ([batch, n_kv_heads, head_dim], F32 rounded to f16 nearest-even or F16) is
@@ -200,7 +200,7 @@ int rvkv_decode_step(rvkv_pool *pool, const rvkv_decode_plan *plan,
                      uint32_t max_ctx_len, float scale, int32_t window,
                      float *out, void *ws, size_t ws_bytes);
 
-/* ---- next row (f)1: attention prep fused with the append -----------------
+/* ---- attention prep fused with the append -----------------
  * Everything between the QKV projection and attention for `rows` tokens,
  * as src/model.rs:600-639 computes it (the reference's own fused form is
  * the Metal attn_prep, src/metal/kernels/attention.metal:8-88):
@@ -223,7 +223,7 @@ int rvkv_attn_prep(rvkv_pool *pool, uint32_t layer, const float *q_in,
                    const float *sin_t, const uint32_t *slot_block,
                    const uint32_t *slot_off, float *q_out);
 
-/* ---- next row (f)2: paged prefill / chunked-prefill attention ------------
+/* ---- paged prefill / chunked-prefill attention ------------
  * Attention for q_len >= 1 query rows per sequence straight over the paged
  * cache: what rvllm's prefill computes with kv_gather + batch_mask +
  * gqa_attention (src/model.rs:346-415 called at :628-644; CUDA:
@@ -256,7 +256,7 @@ int rvkv_attn_prep_qkv(rvkv_pool *pool, uint32_t layer, const float *qkv,
                        const uint32_t *block_ids, const uint32_t *offsets,
                        float *q_out);
 
-/* ---- a10: prefix-cache copy-on-write -------------------------------------
+/* ---- prefix-cache copy-on-write -------------------------------------
  * No counterpart in the reference (rvllm never mutates a shared block; its
  * only copy is the whole-cache KvStorage::clone, src/kv_storage.rs:15-33).
  * Copies block src[i] -> dst[i] for every layer, K and V, bit for bit.
@@ -278,7 +278,7 @@ int rvkv_block_checksums(const rvkv_pool *pool, uint32_t layer,
                          uint32_t which, const uint32_t *block_ids, uint32_t n,
                          uint64_t *out);
 
-/* ---- a8/a9/a10 host side: block manager -----------------------------------
+/* ---- host side: block manager -----------------------------------
  * Host-only (no device memory). Stands in for the external
  * kv-cache-scheduler 0.2.0 crate as rvllm's engine uses it
  * (src/engine.rs:351-539): a block pool with a free list, per-sequence block
@@ -343,7 +343,7 @@ uint32_t rvkv_bm_refcount(const rvkv_bm *bm, uint32_t block);
 int rvkv_bm_table(const rvkv_bm *bm, int64_t seq, uint32_t *table,
                   uint32_t cap);
 
-/* ---- next row (f)4: greedy token pick on the GPU --------------------------
+/* ---- greedy token pick on the GPU --------------------------
  * out[r] = index of the maximum of logits[r * row_len ...] (f32, device):
  * ties go to the lowest index, NaN is ignored, a row with nothing above
  * -inf gives 0 - the greedy scan of Sampler::sample_slice
@@ -360,7 +360,7 @@ int rvkv_argmax(const float *logits, uint32_t rows, uint32_t row_len,
 int rvkv_read_probe(const void *buf, size_t bytes, uint32_t workgroups,
                     uint32_t *sink, rvkv_stream stream);
 
-/* ---- next row (f)3: continuous-batching scheduler with prefix cache -----
+/* ---- continuous-batching scheduler with prefix cache -----
  * The contract rvllm's engine uses from the kv-cache-scheduler crate (0.2.0,
  * not vendored; used at src/engine.rs:351-539): a refcounted block pool
  * (pool.available(), pool.total_allocs), FIFO `waiting` and `running`

@@ -298,7 +298,7 @@ def decode_step(cache: KvCache, slot_block, slot_off, new_k, new_v,
     return out
 
 
-# ---- SURVEY (f)1: attention prep (bias, QK RMS norm, RoPE) + append ------
+# ---- attention prep (bias, QK RMS norm, RoPE) + append ------
 def rope_cos_sin(rope_theta, head_dim, positions, factors=None):
     """rope_cos_sin (src/model.rs:224-250): f32 cos, sin [n, hd/2]."""
     pos = _u32(positions)

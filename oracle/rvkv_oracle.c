@@ -108,7 +108,7 @@ static inline void cell_set(void *cache, int dtype, size_t i, float x) {
     ((float *)cache)[i] = x;
 }
 
-/* ---- a2: KvStorage::write_tokens (src/kv_storage.rs:116-150) -------------
+/* ---- KvStorage::write_tokens (src/kv_storage.rs:116-150) -------------
  * Consecutive tokens landing in consecutive slots of one block form a run
  * copied together (the reference's slice_set); a run is exactly the
  * per-token scatter of kv_write.cu:17-35, dest = ((block*bs + offset)*n_kv +
@@ -154,7 +154,7 @@ int orc_write_tokens_f16src(uint16_t *cache_k, uint16_t *cache_v,
   return 0;
 }
 
-/* ---- a3: GatherPlan::new (src/kv_storage.rs:50-75) ------------------------
+/* ---- GatherPlan::new (src/kv_storage.rs:50-75) ------------------------
  * tables: the sequences' block tables concatenated; table_lens[b] entries
  * each; n_tokens[b] = read_num_tokens. Pads each table to max_blocks with
  * its own last block (0 for an empty table). out_idx may be NULL to only
@@ -181,7 +181,7 @@ void orc_gather_plan(uint32_t batch, const uint32_t *table_lens,
   }
 }
 
-/* ---- a4: KvStorage::gather (src/kv_storage.rs:157-173) --------------------
+/* ---- KvStorage::gather (src/kv_storage.rs:157-173) --------------------
  * index_select over the padded plan, reshape to [batch, max_blocks*bs, n_kv,
  * hd], narrow to ctx_len, transpose to [batch, n_kv, ctx_len, hd]. Element
  * formula as kv_gather.cu:53-71. Out-of-range block ids read zeros. */
@@ -203,7 +203,7 @@ void orc_gather(const void *cache, int dtype, uint32_t num_blocks, uint32_t bs,
       }
 }
 
-/* ---- a5: batch_mask (src/model.rs:346-369) ---------------------------------
+/* ---- batch_mask (src/model.rs:346-369) ---------------------------------
  * mask[b][i][j] = -inf if j >= read_num_tokens[b] or j > offset_b + i or (a
  * window w > 0 and) j + w <= offset_b + i; 0 otherwise. */
 void orc_batch_mask(uint32_t batch, const uint32_t *position_offset,
@@ -219,7 +219,7 @@ void orc_batch_mask(uint32_t batch, const uint32_t *position_offset,
       }
 }
 
-/* ---- a6: gqa_attention (src/model.rs:377-415), f32 ------------------------
+/* ---- gqa_attention (src/model.rs:377-415), f32 ------------------------
  * q [batch, n_heads, q_len, hd]; k, v [batch, n_kv, ctx_len, hd];
  * mask [batch, q_len, ctx_len]; out [batch, n_heads, q_len, hd].
  * Query head h reads KV head h / (n_heads/n_kv) (the group fold of
@@ -329,7 +329,7 @@ void orc_paged_decode_f64(const void *cache_k, const void *cache_v, int dtype,
   free(acc);
 }
 
-/* ---- next row (f)2: paged prefill / chunked attention, q_len >= 1 ---------
+/* ---- paged prefill / chunked attention, q_len >= 1 ---------
  * Float64 attention straight over the paged cache for q_len query rows per
  * sequence, with batch_mask's rule (src/model.rs:346-369): row i of
  * sequence b sits at position p = pos_offset[b] + i and sees key j iff
@@ -392,7 +392,7 @@ void orc_paged_prefill_f64(const void *cache_k, const void *cache_v,
   free(acc);
 }
 
-/* ---- a10: copy-on-write block copy (new behaviour; invariants only) -------
+/* ---- copy-on-write block copy (new behaviour; invariants only) -------
  * dst block := src block, every cell, for one layer's K or V tensor. */
 void orc_copy_blocks(void *cache, int dtype, uint32_t bs, uint32_t n_kv,
                      uint32_t hd, const uint32_t *src, const uint32_t *dst,
@@ -521,7 +521,7 @@ int orc_decode_step(uint16_t *cache_k, uint16_t *cache_v, uint32_t num_blocks,
   return 0;
 }
 
-/* ---- SURVEY (f)1: attention prep before the append -------------------------
+/* ---- attention prep before the append -------------------------
  * rope_cos_sin (src/model.rs:224-250): theta_j = rope_theta^(-2j/hd) (f32),
  * divided by factors[j] when given (Llama 3); angle = pos * theta_j;
  * cos/sin [n, hd/2] in f32. */

@@ -55,7 +55,7 @@ __device__ __forceinline__ uint32_t as_u32(h2 x) {
 
 
 // ---------------------------------------------------------------------------
-// a2: KV append. One thread per VW contiguous elements of one (token, head)
+// KV append. One thread per VW contiguous elements of one (token, head)
 // row; VW = 8 (16-byte f16 store) when head_dim % 8 == 0.
 // Replaces kv_write.cu (one thread per f32 scalar, 32-bit indices).
 // ---------------------------------------------------------------------------
@@ -120,7 +120,7 @@ __global__ void __launch_bounds__(256)
 }
 
 // ---------------------------------------------------------------------------
-// a4: block-table gather into rvllm's padded [batch, n_kv, ctx_len, hd].
+// Block-table gather into rvllm's padded [batch, n_kv, ctx_len, hd].
 // Replaces kv_gather.cu. One thread per VW output elements.
 // ---------------------------------------------------------------------------
 template <int VW, bool OUT_F32>
@@ -186,7 +186,7 @@ __global__ void __launch_bounds__(256)
 }
 
 // ---------------------------------------------------------------------------
-// SURVEY (f)1: attention prep + append. Per (row, head slot) - slots are the
+// Attention prep + append. Per (row, head slot) - slots are the
 // n_heads q heads, then the n_kv k heads, then the n_kv v heads - T threads
 // each hold PPT rotate-half pairs (j, j + HD/2): optional bias, optional
 // per-head RMS norm (q and k; sum of squares reduced over the T lanes), RoPE
@@ -313,7 +313,7 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(PrepArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// a10: copy-on-write block copy, every layer, K and V. grid.y = pair,
+// Copy-on-write block copy, every layer, K and V. grid.y = pair,
 // grid.z = tensor (2 * n_layers); threads stride over the block's 16-byte
 // (or 2-byte) words.
 // ---------------------------------------------------------------------------
@@ -379,7 +379,7 @@ __global__ void __launch_bounds__(64)
 }
 
 // ---------------------------------------------------------------------------
-// a5 + a6: paged GQA decode attention.
+// Paged GQA decode attention.
 //
 // Work unit: one wavefront per (sequence, KV head, query sub-group of <= 8
 // heads, context partition of P tokens). The wave streams its partition's

@@ -1,7 +1,7 @@
 """Continuous-batching decode driver over the native block manager.
 
 Drives the paged KV path the way rvllm's engine does (src/engine.rs:344-490)
-for BASELINE configs[4] (gemma-3-270m churn):
+for the gemma-3-270m churn workload:
 - every step a fraction of the running sequences finishes, and their blocks
   return to a seeded-shuffled, fragmented free list;
 - the same number of new sequences is admitted with short prompts, whose

@@ -163,7 +163,7 @@ class HipKvStorage:
     def nbytes(self) -> int:
         return self._L.rvkv_pool_bytes(self._pool)
 
-    # -- a2: append ---------------------------------------------------------
+    # -- append ---------------------------------------------------------
     def write_tokens(self, layer: int, block_ids: torch.Tensor,
                      offsets: torch.Tensor, k: torch.Tensor,
                      v: torch.Tensor) -> None:
@@ -189,7 +189,7 @@ class HipKvStorage:
                                   _DT[k.dtype], _ptr(block_ids),
                                   _ptr(offsets), n_tokens))
 
-    # -- a4: gather ---------------------------------------------------------
+    # -- gather ---------------------------------------------------------
     def gather(self, layer: int, plan: HipGatherPlan, out_k: torch.Tensor,
                out_v: torch.Tensor) -> None:
         """CudaKvStorage::gather -> kv_gather_wrapper
@@ -212,7 +212,7 @@ class HipKvStorage:
                                   plan.batch, plan.max_blocks, plan.ctx_len,
                                   _ptr(out_k), _ptr(out_v), _DT[out_k.dtype]))
 
-    # -- a5 + a6: paged decode attention -----------------------------------
+    # -- paged decode attention -----------------------------------
     def decode_workspace_bytes(self, batch: int, n_heads: int,
                                max_ctx_len: int) -> int:
         return self._L.rvkv_decode_workspace_bytes(self._pool, batch, n_heads,
@@ -378,7 +378,7 @@ class HipKvStorage:
             ws.numel() if ws is not None else 0))
         return out
 
-    # -- (f)1: attention prep + append ------------------------------------
+    # -- attention prep + append ------------------------------------
     def attn_prep(self, layer: int, q_in: torch.Tensor, k_in: torch.Tensor,
                   v_in: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
                   slot_block: torch.Tensor, slot_off: torch.Tensor,
@@ -443,7 +443,7 @@ class HipKvStorage:
             _ptr(block_ids), _ptr(offsets), _ptr(q_out)))
         return q_out
 
-    # -- a10: copy-on-write -------------------------------------------------
+    # -- copy-on-write -------------------------------------------------
     def copy_blocks(self, src: torch.Tensor, dst: torch.Tensor) -> None:
         """Copies src[i] -> dst[i] for all layers, K and V."""
         _need(src.numel() == dst.numel(),

@@ -1,4 +1,4 @@
-"""The BASELINE configs as concrete, seeded synthetic workloads.
+"""The benchmark workloads as concrete, seeded synthetic inputs.
 
 Shapes follow the attention geometry of the named models (layers, query
 heads, KV heads, head_dim) and rvllm's paged cache (block_size, block
@@ -92,11 +92,11 @@ class Config:
 
 
 CONFIGS = {
-    # CPU reference path (f32 cache in the reference).
+    # The CPU-sized workload (rvllm runs it with an f32 cache).
     "smollm2-360m": Config("smollm2-360m", 0, 1, 15, 5, 64, 16, 8,
                            description="SmolLM2-360M attention, CPU config",
                            rope_theta=100000.0),
-    # the headline bench workload.
+    # The headline bench workload.
     "llama-3.2-1b": Config("llama-3.2-1b", 1, 16, 32, 8, 64, 16, 64,
                            description="Llama-3.2-1B shape, 64 x 2048",
                            rope_theta=500000.0),
@@ -197,7 +197,7 @@ def _with_slots(cfg, nb, ctx, tables) -> DecodeBatch:
 
 
 def smollm2_batch(seed: Optional[int] = None) -> DecodeBatch:
-    """8 sequences, ctx drawn uniformly in [17, 512], tables
+    """The CPU-sized workload: 8 sequences, ctx drawn uniformly in [17, 512], tables
     drawn from a permutation of a 512-block pool."""
     cfg = CONFIGS["smollm2-360m"]
     rng = Rng(cfg.seed if seed is None else seed)
@@ -214,7 +214,7 @@ def smollm2_batch(seed: Optional[int] = None) -> DecodeBatch:
 
 def qwen25_batch(batch: Optional[int] = None, seed: Optional[int] = None,
                  prefix: int = 1024, share_frac: float = 0.3) -> DecodeBatch:
-    """lengths log-uniform in [32, 8192]; a share_frac of the
+    """The ragged Qwen2.5 workload: lengths log-uniform in [32, 8192]; a share_frac of the
     sequences reuse the first min(len, prefix) tokens of one common prefix
     through identical block ids. A sharer whose last block is shared and
     partially filled gets a private copy before this step's append (the

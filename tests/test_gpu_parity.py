@@ -378,7 +378,7 @@ def test_decode_group_sizes(G):
     assert _decode_vs_oracle(st, 0, db, q) < ATOL
 
 
-# ---- BASELINE configs (one layer each, full batch and context) ------------
+# ---- benchmark workloads (one layer each, full batch and context) ------------
 def test_config_smollm2():
     db = W.smollm2_batch()
     c = db.cfg
@@ -762,7 +762,7 @@ def test_graph_capture_replays_match_eager():
         assert torch.equal(out_g2, e2), rep
 
 
-# ---- (f)1: attention prep + append -------------------------------------------
+# ---- attention prep + append -------------------------------------------
 @pytest.mark.parametrize("hd,H,KV", [(64, 32, 8), (128, 16, 8), (256, 4, 1),
                                      (64, 14, 2), (32, 9, 1)])
 @pytest.mark.parametrize("bias,norm", [(False, False), (True, False),
@@ -870,7 +870,7 @@ def test_attn_prep_then_decode_end_to_end(hd, H, KV):
     assert np.max(np.abs(a - b)) > 1e-2
 
 
-# ---- (f)2: paged prefill / chunked-prefill attention -------------------------
+# ---- paged prefill / chunked-prefill attention -------------------------
 @pytest.mark.parametrize("case", [0, 1, 2, 4])
 def test_prefill_metal_cases(golden, case):
     """The attn_decode cases of src/metal/ops.rs:676-766 with their own
@@ -1012,7 +1012,7 @@ def test_prefill_rejections():
                          dev_u32([[0]]), dev_u32([0]), dev_u32([2]))
 
 
-# ---- (f)4 argmax and the engine over the paged KV path -------------------------
+# ---- argmax and the engine over the paged KV path -------------------------
 def test_argmax_kat_and_random():
     """rvkv_argmax: the reference KAT (src/cuda/ops.rs:1447-1477) and random
     rows with ties/NaN at vocab sizes that are and are not multiples of 4."""

@@ -320,7 +320,7 @@ def test_block_checksums_match_independent_fnv():
         assert int(got[i]) == _fnv1a64(c.k[b].astype("<u2").tobytes())
 
 
-# ---- (f)1: RMS norm / RoPE / attention prep ---------------------------------
+# ---- RMS norm / RoPE / attention prep ---------------------------------
 def test_rms_norm_kat():
     """src/model.rs:758-776: x = [1, 2, 3], w = 1, eps 1e-5."""
     out = orc.rms_norm([[1.0, 2.0, 3.0]], [1.0, 1.0, 1.0], 1e-5)
@@ -393,7 +393,7 @@ def test_attn_prep_composes_the_pinned_parts():
                                   orc.f32_to_f16_bits(y))
 
 
-# ---- (f)2: paged prefill / chunked attention ----------------------------------
+# ---- paged prefill / chunked attention ----------------------------------
 @pytest.mark.parametrize("case", range(6))
 def test_paged_prefill_f64_matches_metal_golden(golden, case):
     """orc_paged_prefill_f64 on all six attn_decode cases of
@@ -459,7 +459,7 @@ def test_paged_prefill_f64_q_len_one_is_decode():
         assert np.array_equal(a[:, 0], b)
 
 
-# ---- (f)4: greedy argmax -------------------------------------------------------
+# ---- greedy argmax -------------------------------------------------------
 def argmax_kat_rows():
     """The rows of argmax_matches_hand_computed (src/cuda/ops.rs:1447-1477):
     unique max; tie between 1 and 3 with a NaN; all -inf; max at 599."""
