@@ -9,7 +9,7 @@
  * toolchain), so this C file is the oracle. Storage follows rvllm's LOGICAL
  * per-layer layout [num_blocks, block_size, n_kv_heads, head_dim]
  * (src/kv_storage.rs:7-13) with either f32 cells (the reference's own dtype,
- * src/kv_storage.rs:94-97) or f16 cells (the north-star storage type; values
+ * src/kv_storage.rs:94-97) or f16 cells (this build's storage type; values
  * are rounded f32->f16 round-to-nearest-even on write).
  *
  * Pinning (see the tests): the reference's known-answer tests

@@ -21,7 +21,7 @@ from tests.gpu_util import dev_u32, fill_layer, oracle_subset
 
 pytestmark = pytest.mark.gpu
 
-ATOL = 2e-3  # north-star tolerance, f16 KV with f32 accumulation
+ATOL = 2e-3  # decode/prefill tolerance: f16 KV with f32 accumulation
 
 
 @pytest.fixture(autouse=True)
