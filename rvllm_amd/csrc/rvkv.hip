@@ -1416,7 +1416,8 @@ int plan_build(rvkv_decode_plan *pl, const uint32_t *ctx_lens_host,
   // The matrix-core decode runs one wave per item (the VALU decode four),
   // so it gets items a quarter as long and four times as many.
   const bool mfma = rvkv_detail::mfma_decode_wanted(pool, pl->n_heads);
-  const double per = mfma ? 4.0 : 1.0;
+  static const uint32_t forced_div = env_u32("RVKV_DECODE_PLAN_DIV");
+  const double per = forced_div ? (double)forced_div : (mfma ? 4.0 : 1.0);
   const double avg = (double)total / batch / per;
   const double lo_p = (double)total * n_hy / (1024.0 * per);
   const double hi_p = (double)total * n_hy / (256.0 * per);
