@@ -437,6 +437,9 @@ struct DecodeArgs {
   uint32_t bs_log2, part_tokens, n_parts, ctx_cap;
   float qscale;
   int32_t window;
+  // Host-side launch hint (not read by the kernels): average context
+  // tokens per workgroup.
+  uint32_t avg_tokens;
 };
 
 constexpr uint32_t kNoSlot = 0xFFFFFFFFu;
@@ -1045,8 +1048,9 @@ void launch_decode(const DecodeArgs &a, dim3 grid, hipStream_t st) {
   const uint32_t W = decode_waves((uint64_t)grid.x * grid.y * grid.z);
   // Eight loads per chunk pay off for 512-byte rows and for large groups
   // in single-wave workgroups; otherwise four keep more waves resident.
-  const bool u8 =
-      forced_u ? forced_u == 8 : (HD >= 256 || (GT >= 5 && W == 1));
+  const bool u8 = forced_u ? forced_u == 8
+                           : ((HD >= 256 && a.avg_tokens >= 512) ||
+                              (GT >= 5 && W == 1));
   const size_t lds = (size_t)W * GT * (HD + 2) * sizeof(float);
   if (u8)
     hipLaunchKernelGGL((decode_part_kernel<HD, GT, 8, 1>), grid, dim3(64 * W),
@@ -1364,7 +1368,7 @@ struct rvkv_decode_plan {
   const rvkv_pool *pool;
   uint32_t batch, n_heads, n_kv, head_dim, max_ctx;
   int32_t window;
-  uint32_t part_tokens, n_items, n_reds, n_slots;
+  uint32_t part_tokens, n_items, n_reds, n_slots, avg_tokens = 0;
   uint4 *d_buf = nullptr;   // items, then reduction rows (device)
   uint4 *h_buf = nullptr;   // pinned staging copy of the same
   size_t cap = 0;           // entries both buffers hold
@@ -1489,6 +1493,7 @@ int plan_build(rvkv_decode_plan *pl, const uint32_t *ctx_lens_host,
   pl->batch = batch;
   pl->max_ctx = max_ctx;
   pl->part_tokens = P;
+  pl->avg_tokens = items.empty() ? 0u : (uint32_t)(total / items.size());
   pl->n_items = (uint32_t)items.size();
   pl->n_reds = (uint32_t)reds.size();
   pl->n_slots = slots;
@@ -1537,6 +1542,7 @@ int rvkv_paged_decode(const rvkv_pool *pool, uint32_t layer, const float *q,
   a.ws_ml = w.n_parts > 1 ? (float *)((char *)ws + w.ml_off) : nullptr;
   a.part_tokens = partition_tokens(pool, batch, n_heads, max_ctx_len);
   a.n_parts = w.n_parts;
+  a.avg_tokens = a.part_tokens < max_ctx_len ? a.part_tokens : max_ctx_len;
   const dim3 grid(w.n_parts, pool->n_kv * a.n_sub, batch);
   return launch_decode_pair(op, a, pool->head_dim, gt, grid,
                             dim3(n_heads, batch), w.n_parts > 1, pool->stream);
@@ -1615,6 +1621,7 @@ int rvkv_paged_decode_planned(const rvkv_pool *pool,
   a.items = plan->d_buf;
   a.reds = plan->d_buf + plan->n_items;
   a.part_tokens = plan->part_tokens;
+  a.avg_tokens = plan->avg_tokens;
   a.n_parts = 1;
   if (rvkv_detail::mfma_decode_wanted(pool, plan->n_heads))
     return planned_mfma(op, pool, plan, layer, a, max_blocks, scale);
@@ -1667,6 +1674,7 @@ int rvkv_decode_step(rvkv_pool *pool, const rvkv_decode_plan *plan,
     a.items = plan->d_buf;
     a.reds = plan->d_buf + plan->n_items;
     a.part_tokens = plan->part_tokens;
+    a.avg_tokens = plan->avg_tokens;
     a.n_parts = 1;
     if (rvkv_detail::mfma_decode_wanted(pool, n_heads))
       return planned_mfma(op, pool, plan, layer, a, max_blocks, scale);
@@ -1684,6 +1692,7 @@ int rvkv_decode_step(rvkv_pool *pool, const rvkv_decode_plan *plan,
   a.ws_ml = w.n_parts > 1 ? (float *)((char *)ws + w.ml_off) : nullptr;
   a.part_tokens = partition_tokens(pool, batch, n_heads, max_ctx_len);
   a.n_parts = w.n_parts;
+  a.avg_tokens = a.part_tokens < max_ctx_len ? a.part_tokens : max_ctx_len;
   const dim3 grid(w.n_parts, pool->n_kv * a.n_sub, batch);
   return launch_decode_pair(op, a, pool->head_dim, gt, grid,
                             dim3(n_heads, batch), w.n_parts > 1, pool->stream);
