@@ -368,6 +368,8 @@ __global__ void __launch_bounds__(
   // its first tiles' loads are out), writes it into LDS over whatever the
   // cache held in the tile holding that key, and stores it to its slot at
   // the end (lanes < CPR, one 16-byte chunk each).
+  static_assert(WAVES != 1 || (HD <= NTH && CPR <= NTH),
+                "one lane per V element and per 16-byte chunk of the row");
   u32x4 new_kc{}, new_vc{};
   uint16_t new_ve = 0;  // V element tid of the new row (f16 bits)
   const size_t new_src = ((size_t)b * a.n_kv + kvh) * HD;
