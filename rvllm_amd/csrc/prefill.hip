@@ -116,20 +116,22 @@ __device__ __forceinline__ float vmax3(float a, float b, float c) {
   return r;
 }
 
-// Lanes i and i ^ 32 combined: v_permlane32_swap exchanges the wave's two
-// 32-lane halves in the VALU (no LDS round trip as for a bpermute).
+// Lanes i and i ^ 32 combined: v_permlane32_swap of v with itself leaves
+// the lower half's value in element 0 and the upper half's in element 1 of
+// every lane, in the VALU (no LDS round trip as for a bpermute).
 __device__ __forceinline__ float max_halves(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v),
                                                   __float_as_uint(v), false,
                                                   false);
-  return vmax3(__uint_as_float(r[0]), __uint_as_float(r[1]),
-               __uint_as_float(r[1]));
+  const uint32_t r0 = r[0], r1 = r[1];
+  return vmax3(__uint_as_float(r0), __uint_as_float(r1), __uint_as_float(r1));
 }
 __device__ __forceinline__ float sum_halves(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v),
                                                   __float_as_uint(v), false,
                                                   false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  const uint32_t r0 = r[0], r1 = r[1];
+  return __uint_as_float(r0) + __uint_as_float(r1);
 }
 
 // Eight elements of an appended K or V row as f16, rounded to nearest even
