@@ -937,17 +937,34 @@ __global__ void __launch_bounds__(64) decode_reduce_kernel(DecodeArgs a) {
       L += lp * w;
     }
     const uint32_t n = min(np - c, 64u);
-#pragma unroll 8
-    for (uint32_t i = 0; i < n; ++i) {
+    // Eight partitions per pass: their loads all issue before any is used.
+    auto add = [&](uint32_t i, const float (&x)[EPL]) {
       const float wi =
           __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), i));
+#pragma unroll
+      for (int e = 0; e < EPL; ++e)
+        acc[e] += wi != 0.f ? wi * x[e] : 0.f;  // skipped partials stay out
+    };
+    auto fetch = [&](uint32_t i, float (&x)[EPL]) {
       const float *src = accp + (size_t)(c + i) * acc_step;
 #pragma unroll
       for (int e = 0; e < EPL; ++e) {
         const int d = lane * EPL + e;
-        const float x = d < HD ? src[d] : 0.f;
-        acc[e] += wi != 0.f ? wi * x : 0.f;  // skipped partials stay out
+        x[e] = d < HD ? src[d] : 0.f;
       }
+    };
+    uint32_t i = 0;
+    for (; i + 8 <= n; i += 8) {
+      float x[8][EPL];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) fetch(i + k, x[k]);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) add(i + k, x[k]);
+    }
+    for (; i < n; ++i) {
+      float x[EPL];
+      fetch(i, x);
+      add(i, x);
     }
   }
 #pragma unroll
