@@ -6,7 +6,8 @@ src/cuda/engine.rs:339-404): token embedding, then per layer the Q/K/V
 projection (one fused QKV GEMM), attention prep with the K/V append
 (rvkv_attn_prep_qkv),
 attention straight over the paged cache (rvkv_paged_prefill for a prefill
-item, rvkv_paged_decode for a decode batch) and the output projection with
+item, rvkv_paged_decode_planned under a per-forward decode plan for a decode
+batch) and the output projection with
 a residual add; then tied-embedding logits and the greedy pick on the GPU
 (rvkv_argmax). The MLP, norms and real checkpoints are outside the KV path
 and left out: the weights are seeded random. The projections are plain
@@ -29,7 +30,7 @@ import torch
 
 from . import _lib
 from ._lib import check
-from .kv_storage import HipKvStorage
+from .kv_storage import HipDecodePlan, HipKvStorage
 from .rope import rope_cos_sin
 
 
@@ -113,6 +114,7 @@ class HipBackend:
         self._L = _lib.load()
         self.last_logits = None
         self.forwards = 0
+        self._plans = {}
 
     def _u32(self, a) -> torch.Tensor:
         arr = np.ascontiguousarray(np.asarray(a, np.uint32)).view(np.int32)
@@ -143,6 +145,16 @@ class HipBackend:
         x = w["embed"][torch.from_numpy(toks).to(self.dev)]
         scale = 1.0 / math.sqrt(hd)
         decode = not last_only and all(len(it.tokens) == 1 for it in items)
+        if decode:
+            # One decode plan per forward, shared by every layer (rvllm's
+            # GatherPlan); kept per batch size and updated in place.
+            lens = [it.read_num_tokens for it in items]
+            plan = self._plans.get(len(items))
+            if plan is None:
+                plan = HipDecodePlan(st, lens, H, window=c.window)
+                self._plans[len(items)] = plan
+            else:
+                plan.update(lens)
         for l in range(c.n_layers):
             qkv = x @ w[f"wqkv{l}"]
             qr = st.attn_prep_qkv(l, qkv, H, cos, sin, sb, so,
@@ -150,10 +162,8 @@ class HipBackend:
                                   q_norm=w.get(f"qn{l}"),
                                   k_norm=w.get(f"kn{l}"), eps=c.eps)
             if decode:
-                att = st.paged_decode(
-                    l, qr, tables, reads,
-                    max(it.read_num_tokens for it in items), scale=scale,
-                    window=c.window)
+                att = st.paged_decode_planned(l, plan, qr, tables, reads,
+                                              scale=scale)
             else:
                 att = torch.empty_like(qr)
                 r0 = 0

@@ -83,6 +83,9 @@ class HipDecodePlan:
             store._pool, lens.ctypes.data_as(ctypes.c_void_p), self.batch,
             n_heads, self.window, ctypes.byref(handle)))
         self._plan = handle
+        # The native plan reaches its pool's stream when destroyed, so the
+        # pool must outlive it: hold the storage.
+        self._store = store
         self._device = store.device
         self.ws = None
         self._sync()
