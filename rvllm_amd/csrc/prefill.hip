@@ -15,7 +15,9 @@
 // folded into the query axis, row r = (query qi = r / G, head g = r % G), so
 // every key/value tile read from HBM serves G heads * 128/G positions.
 // Keys stream in tiles of 64 through LDS; the next tile's global loads are
-// in flight while the current one is computed.
+// in flight while the current one is computed. At head_dim 256 a workgroup
+// is eight waves in four pairs; the two waves of a pair hold the same 32
+// rows and one half of the head dimension each (tiles of 32 keys).
 //
 // Matrix layout (v_mfma_f32_32x32x16_f16, f32 accumulate):
 //   S^T = K . Q^T   (M = 32 keys, N = 32 query rows, K = 16 of head_dim)
@@ -59,6 +61,14 @@ constexpr int tile_keys() {
   return HD >= 256 || WAVES == 1 ? 32 : 64;
 }
 constexpr int kWaveRows = 32;  // query rows per wave
+// At head_dim 256 the two waves of a pair share 32 query rows: each holds
+// half of the head dimension of Q and O (the S product's two halves are
+// added through LDS), so a wave's O and Q fit two waves per SIMD.
+constexpr bool split_dims(int hd) { return hd >= 256; }
+template <int HD, int WAVES>
+constexpr int block_rows() {
+  return kWaveRows * (split_dims(HD) ? WAVES / 2 : WAVES);
+}
 constexpr float kNegBig = -1.0e30f;      // finite start value of the row max
 
 struct PrefillArgs {
@@ -72,7 +82,7 @@ struct PrefillArgs {
   uint32_t q_len, max_blocks, num_blocks, n_heads, group, bs_log2;
   uint32_t batch, n_kv;
   uint32_t rows;     // group * q_len rows per (sequence, KV head)
-  uint32_t n_tiles;  // ceil(rows / (32 * waves per workgroup))
+  uint32_t n_tiles;  // ceil(rows / rows per workgroup)
   float qscale;      // scale * log2(e)
   int32_t window;
   // Decode mode (q_len 1 at position read_num - 1) over a decode plan's
@@ -104,7 +114,10 @@ struct Lds {
   // (a one-wave workgroup orders its own LDS accesses).
   static constexpr int NBUF = WAVES > 1 ? 2 : 1;
   static constexpr size_t buf = (k_bytes + v_bytes + BN + 15) / 16 * 16;
-  static constexpr size_t bytes = NBUF * buf;  // + key flags in each buffer
+  // Split head dimension: one f32 S^T tile per wave for its partner.
+  static constexpr size_t x_bytes =
+      split_dims(HD) ? (size_t)WAVES * 64 * BN / 2 * 4 : 0;
+  static constexpr size_t bytes = NBUF * buf + x_bytes;  // + key flags
 };
 
 // max(a, b, c) in one v_max3_f32. Written as an instruction because the
@@ -167,25 +180,30 @@ __device__ __forceinline__ uint32_t lo_bound(uint32_t p, int32_t window) {
 // WAVES wave64s per workgroup (4 or 8, 32 query rows each); the K/V tile
 // loads and LDS stores are shared among them, so more waves halve each
 // wave's share of that work. Registers are bounded for 8 resident waves per
-// CU at head_dim 128 (<= 256 a lane, so the O accumulators stay in arch
-// VGPRs), 12 below and 4 at 256: two or more waves per SIMD overlap one's
-// softmax with another's matrix work. (128-key tiles at head_dim 64 were
+// CU at head_dim 128 and 256 (<= 256 a lane, so the O accumulators stay in
+// arch VGPRs; at 256 only because each wave holds half of O and Q), 12
+// below: two or more waves per SIMD overlap one's softmax with another's
+// matrix work. (With all of O and Q in one wave, head_dim 256 ran one wave
+// per SIMD, its S product serialised on LDS reads: 18 % slower.) (128-key tiles at head_dim 64 were
 // measured 7-9 % slower than 64.)
 template <int HD, int WAVES>
 __global__ void __launch_bounds__(
     64 * WAVES,
     // (a one-wave workgroup may share a SIMD with others: 2 bounds the
     // registers to two waves per SIMD)
-    WAVES == 1 ? 2 : (HD <= 64 ? 12 : (HD <= 128 ? 8 : 4)) / WAVES)
+    WAVES == 1 ? 2 : (HD <= 64 ? 12 : 8) / WAVES)
     prefill_kernel(PrefillArgs a) {
   constexpr int NTH = 64 * WAVES;  // threads per workgroup
-  constexpr int kBM = kWaveRows * WAVES;
+  constexpr bool SPLIT = split_dims(HD);
+  static_assert(!SPLIT || (WAVES % 2 == 0 && WAVES > 1), "wave pairs");
+  constexpr int kBM = block_rows<HD, WAVES>();
   using LD = Lds<HD, WAVES>;
   constexpr int KS = LD::KS, VS = LD::VS, BN = LD::BN;
   constexpr int NT = BN / 32;                 // 32-key sub-tiles per tile
   constexpr int NPR = BN / 2;                 // key pairs per tile
-  constexpr int KC = HD / 16;                 // MFMA k-steps of S
-  constexpr int DT = HD / 32;                 // 32-row tiles of O^T
+  // This wave's share of the head dimension: all of it, or one half.
+  constexpr int KC = HD / 16 / (SPLIT ? 2 : 1);  // MFMA k-steps of S
+  constexpr int DT = HD / 32 / (SPLIT ? 2 : 1);  // 32-row tiles of O^T
   constexpr int CPR = HD / 8;                 // 16-byte chunks per key row
   constexpr int CHK = BN * CPR / NTH;         // K chunks per thread per tile
   static_assert(CHK >= 1 && BN * CPR % NTH == 0, "tile/thread mismatch");
@@ -219,6 +237,9 @@ __global__ void __launch_bounds__(
   }
   const int tid = threadIdx.x;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // Row group of the wave, and the half of the head dimension it holds.
+  const uint32_t rgrp = SPLIT ? wave >> 1 : wave;
+  const uint32_t dh = SPLIT ? wave & 1u : 0u;
   const int lane = tid & 63, hl = lane >> 5, ln = lane & 31;
   const uint32_t bs_mask = (1u << a.bs_log2) - 1u;
 
@@ -239,7 +260,7 @@ __global__ void __launch_bounds__(
       item_lo);
 
   // The same for this wave's 32 rows (wave-uniform).
-  const uint32_t rw0 = r_first + wave * kWaveRows;
+  const uint32_t rw0 = r_first + rgrp * kWaveRows;
   const bool wave_live = rw0 < a.rows;
   const uint32_t rw1 = min(rw0 + kWaveRows, a.rows) - 1u;
   const uint32_t w_end =
@@ -267,7 +288,7 @@ __global__ void __launch_bounds__(
 
   half8 qf[KC];
   {
-    const float *qp = a.q + qrow * HD;
+    const float *qp = a.q + qrow * HD + dh * (KC * 16);
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc) {
       const int d0 = kc * 16 + hl * 8;
@@ -348,10 +369,11 @@ __global__ void __launch_bounds__(
   // (one block of all heads is far below 4 GiB; checked on the host)
   const uint32_t blk_bytes = (uint32_t)(a.block_stride * 2);
   // Tiles in flight: one ahead, or two for one-wave (decode) workgroups,
-  // whose single wave's compute per tile is shorter than a load's latency.
+  // whose single wave's compute per tile is shorter than a load's latency,
+  // and for the 32-key tiles of split head_dim (~1 % faster).
   // Register sets are selected by a compile-time index (a runtime index
   // would put the arrays in scratch).
-  constexpr int DEPTH = WAVES == 1 ? 2 : 1;
+  constexpr int DEPTH = WAVES == 1 || SPLIT ? 2 : 1;
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, DEPTH - 1>;
   uint32_t kid[CHK], vid[CHV];
@@ -493,7 +515,10 @@ __global__ void __launch_bounds__(
       load(S, kt + DEPTH * BN);
       fetch_ids(kt + (DEPTH + 1) * BN);
     }
-    if (!(kt < w_end && kt + BN > w_begin)) return;  // nothing for this wave
+    // Does any row of the wave see a key of the tile? (Wave-uniform, and
+    // the same for both waves of a pair.)
+    const bool active = kt < w_end && kt + BN > w_begin;
+    if (!SPLIT && !active) return;
 
     f32x16 s[NT];
 #pragma unroll
@@ -502,15 +527,45 @@ __global__ void __launch_bounds__(
       for (int j = 0; j < 16; ++j) s[t][j] = 0.f;
     // The two sub-tiles' accumulation chains alternate, so each MFMA's
     // dependency on the previous one of its chain is hidden.
+    if (active) {
 #pragma unroll
-    for (int kc = 0; kc < KC; ++kc)
+      for (int kc = 0; kc < KC; ++kc)
 #pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        const half8 kf = *reinterpret_cast<const half8 *>(
-            ks + (32 * t + sig) * KS + kc * 16 + hl * 8);
-        s[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[kc], s[t], 0, 0,
-                                                      0);
+        for (int t = 0; t < NT; ++t) {
+          const half8 kf = *reinterpret_cast<const half8 *>(
+              ks + (32 * t + sig) * KS + dh * (KC * 16) + kc * 16 + hl * 8);
+          s[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[kc], s[t], 0,
+                                                        0, 0);
+        }
+    }
+    if constexpr (SPLIT) {
+      // Add the partner's half of S^T. Each wave writes its own slot after
+      // this tile's first barrier; the partner read it before reaching the
+      // next tile's. Both waves add the same two values, so their S, and
+      // with it their softmax state, are identical.
+      float4 *xs = reinterpret_cast<float4 *>(smem + LD::NBUF * LD::buf);
+      if (active) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4)
+            xs[(wave * NT * 4 + t * 4 + q4) * 64 + lane] =
+                make_float4(s[t][4 * q4], s[t][4 * q4 + 1], s[t][4 * q4 + 2],
+                            s[t][4 * q4 + 3]);
       }
+      __syncthreads();
+      if (!active) return;
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const float4 x = xs[((wave ^ 1u) * NT * 4 + t * 4 + q4) * 64 + lane];
+          s[t][4 * q4] += x.x;
+          s[t][4 * q4 + 1] += x.y;
+          s[t][4 * q4 + 2] += x.z;
+          s[t][4 * q4 + 3] += x.w;
+        }
+    }
 
     // Mask (only where some row of the wave does not see the whole tile),
     // then the online softmax; register j of sub-tile t is key
@@ -583,7 +638,7 @@ __global__ void __launch_bounds__(
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
           const half8 vf = *reinterpret_cast<const half8 *>(
-              vt + (dt * 32 + ln) * VS + 32 * t + 16 * c + 8 * hl);
+              vt + ((dh * DT + dt) * 32 + ln) * VS + 32 * t + 16 * c + 8 * hl);
           o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pb[t][c], o[dt],
                                                          0, 0, 0);
         }
@@ -648,10 +703,11 @@ __global__ void __launch_bounds__(
       for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4)
-          *reinterpret_cast<float4 *>(op + dt * 32 + 8 * q4 + 4 * hl) =
+          *reinterpret_cast<float4 *>(op + (dh * DT + dt) * 32 + 8 * q4 +
+                                      4 * hl) =
               make_float4(o[dt][4 * q4], o[dt][4 * q4 + 1], o[dt][4 * q4 + 2],
                           o[dt][4 * q4 + 3]);
-      if (hl == 0) {
+      if (hl == 0 && dh == 0) {
         a.ws_ml[idx * 2] = m;
         a.ws_ml[idx * 2 + 1] = lt;
       }
@@ -665,7 +721,8 @@ __global__ void __launch_bounds__(
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4)
-        *reinterpret_cast<float4 *>(op + dt * 32 + 8 * q4 + 4 * hl) =
+        *reinterpret_cast<float4 *>(op + (dh * DT + dt) * 32 + 8 * q4 +
+                                    4 * hl) =
             make_float4(o[dt][4 * q4] * inv, o[dt][4 * q4 + 1] * inv,
                         o[dt][4 * q4 + 2] * inv, o[dt][4 * q4 + 3] * inv);
   }
@@ -692,13 +749,14 @@ void launch_prefill(const PrefillArgs &a, dim3 grid, hipStream_t st) {
                      (Lds<HD, WAVES>::bytes), st, a);
 }
 
-// Waves per workgroup: 8 at head_dim 128 (measured ~5 % faster than 4);
-// 4 at 64, where 8-wave workgroups would cost the third resident wave per
-// SIMD (measured ~7 % slower), and at 32 and 256. RVKV_PREFILL_WAVES=4|8
-// overrides (8 only where a K/V tile fills 512 threads: 64, 128).
+// Waves per workgroup: 8 at head_dim 128 (measured ~5 % faster than 4) and
+// at 256 (four pairs, fixed); 4 at 64, where 8-wave workgroups would cost
+// the third resident wave per SIMD (measured ~7 % slower), and at 32.
+// RVKV_PREFILL_WAVES=4|8 overrides at 64 and 128.
 uint32_t prefill_waves(uint32_t hd) {
   static const char *env = getenv("RVKV_PREFILL_WAVES");
   static const uint32_t forced = env ? (uint32_t)atoi(env) : 0u;
+  if (split_dims((int)hd)) return 8u;  // four pairs
   const bool can8 = hd == 64 || hd == 128;
   if (forced == 4 || (forced == 8 && can8)) return forced;
   return hd == 128 ? 8u : 4u;
@@ -764,7 +822,7 @@ int rvkv_paged_prefill(rvkv_pool *pool, uint32_t layer, const float *q,
   a.bs_log2 = lg;
   a.rows = (uint32_t)rows;
   const uint32_t waves = prefill_waves(hd);
-  const uint32_t bm = kWaveRows * waves;
+  const uint32_t bm = kWaveRows * (split_dims((int)hd) ? waves / 2 : waves);
   a.n_tiles = (uint32_t)((rows + bm - 1) / bm);
   a.qscale = scale * 1.4426950408889634f;
   a.window = window;
@@ -784,7 +842,7 @@ int rvkv_paged_prefill(rvkv_pool *pool, uint32_t layer, const float *q,
       if (waves == 8) launch_prefill<128, 8>(a, grid, pool->stream);
       else launch_prefill<128, 4>(a, grid, pool->stream);
       break;
-    default: launch_prefill<256, 4>(a, grid, pool->stream); break;
+    default: launch_prefill<256, 8>(a, grid, pool->stream); break;
   }
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? RVKV_OK : hip_fail(op, e);

@@ -943,9 +943,10 @@ def test_prefill_chunked_vs_oracle(G, hd, bs):
     assert np.isfinite(out).all() and err < ATOL, err
 
 
+@pytest.mark.parametrize("hd", [64, 256])
 @pytest.mark.parametrize("window", [1, 37, 300])
-def test_prefill_window(window):
-    out, want = _prefill_case(window, 2, 200, 2, 4, 64, 16, window,
+def test_prefill_window(window, hd):
+    out, want = _prefill_case(window, 2, 200, 2, 4, hd, 16, window,
                               prior=[0, 333])
     assert np.abs(out - want).max() < ATOL
 
@@ -958,11 +959,13 @@ def test_prefill_full_prompt_from_empty():
     assert np.abs(out - want).max() < ATOL
 
 
-def test_prefill_edges():
+@pytest.mark.parametrize("hd", [64, 256])
+def test_prefill_edges(hd):
     """Rows that see no key (read_num <= pos_offset) are zero; q_len 1
     agrees with the decode kernel; an out-of-range table entry is read as
-    masked, never faults, and leaves rows that do not reach it unchanged."""
-    nb, bs, nkv, hd, H = 40, 16, 2, 64, 8
+    masked, never faults, and leaves rows that do not reach it unchanged.
+    (At head_dim 256 the wave pairs split the head dimension.)"""
+    nb, bs, nkv, H = 40, 16, 2, 8
     st = HipKvStorage(1, nb, bs, nkv, hd)
     fill_layer(st, 0, seed=4)
     rng = np.random.default_rng(4)
