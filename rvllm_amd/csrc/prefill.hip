@@ -369,11 +369,12 @@ __global__ void __launch_bounds__(
   // (one block of all heads is far below 4 GiB; checked on the host)
   const uint32_t blk_bytes = (uint32_t)(a.block_stride * 2);
   // Tiles in flight: one ahead, or two for one-wave (decode) workgroups,
-  // whose single wave's compute per tile is shorter than a load's latency,
-  // and for the 32-key tiles of split head_dim (~1 % faster).
+  // whose single wave's compute per tile is shorter than a load's latency.
+  // (Two in multi-wave workgroups gained at most 1 %, and one head_dim 256
+  // variant with them gave run-to-run differences of ~2e-4; not used.)
   // Register sets are selected by a compile-time index (a runtime index
   // would put the arrays in scratch).
-  constexpr int DEPTH = WAVES == 1 || SPLIT ? 2 : 1;
+  constexpr int DEPTH = WAVES == 1 ? 2 : 1;
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, DEPTH - 1>;
   uint32_t kid[CHK], vid[CHV];

@@ -15,7 +15,7 @@ import torch
 from oracle import oracle as orc
 from rvllm_amd import workloads as W
 from rvllm_amd._lib import RvkvError
-from rvllm_amd.kv_storage import HipGatherPlan, HipKvStorage
+from rvllm_amd.kv_storage import HipDecodePlan, HipGatherPlan, HipKvStorage
 from tests.golden.make_golden import METAL_CASES, metal_case_inputs
 from tests.gpu_util import dev_u32, fill_layer, oracle_subset
 
@@ -949,6 +949,47 @@ def test_prefill_window(window, hd):
     out, want = _prefill_case(window, 2, 200, 2, 4, hd, 16, window,
                               prior=[0, 333])
     assert np.abs(out - want).max() < ATOL
+
+
+@pytest.mark.parametrize("hd", [64, 128, 256])
+def test_prefill_deterministic(hd):
+    """Repeated launches on the same inputs are bitwise equal (the kernels
+    use no atomics; a difference would mean a read of LDS or registers
+    before their data is in place). 1000-token prompts: many tiles per
+    workgroup, a partial last tile."""
+    nb, bs, nkv, H = 200, 16, 2, 8
+    st = HipKvStorage(1, nb, bs, nkv, hd)
+    fill_layer(st, 0, seed=hd)
+    rng = np.random.default_rng(hd)
+    tables = dev_u32(rng.permutation(nb).astype(np.uint32)[:192].reshape(3, 64))
+    q = torch.randn(3, 1000, H, hd, device="cuda")
+    z, full = dev_u32([0, 0, 0]), dev_u32([1000, 1000, 1000])
+    ref = st.paged_prefill(0, q, tables, z, full)
+    for _ in range(6):
+        assert torch.equal(st.paged_prefill(0, q, tables, z, full), ref)
+
+
+@pytest.mark.parametrize("G,hd", [(4, 64), (7, 64), (2, 128), (4, 256)])
+def test_decode_deterministic(G, hd):
+    """The same for planned decode (split sequences, the reduction pass;
+    the matrix-core kernel at G 7)."""
+    nb, bs, nkv = 600, 16, 2
+    H = G * nkv
+    st = HipKvStorage(1, nb, bs, nkv, hd)
+    fill_layer(st, 0, seed=G + hd)
+    rng = np.random.default_rng(G + hd)
+    lens = np.array([1, 37, 900, 4000, 2500], np.uint32)
+    mb = 256
+    tables = np.zeros((lens.size, mb), np.uint32)
+    perm = rng.permutation(nb).astype(np.uint32)
+    for i in range(lens.size):
+        tables[i] = perm[(np.arange(mb) + 97 * i) % nb]
+    q = torch.randn(lens.size, H, hd, device="cuda")
+    plan = HipDecodePlan(st, lens, H)
+    t, ln = dev_u32(tables), dev_u32(lens)
+    ref = st.paged_decode_planned(0, plan, q, t, ln).clone()
+    for _ in range(6):
+        assert torch.equal(st.paged_decode_planned(0, plan, q, t, ln), ref)
 
 
 def test_prefill_full_prompt_from_empty():
