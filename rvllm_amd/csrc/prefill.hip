@@ -120,13 +120,12 @@ struct Lds {
   static constexpr size_t bytes = NBUF * buf + x_bytes;  // + key flags
 };
 
-// max(a, b, c) in one v_max3_f32. Written as an instruction because the
-// IEEE-mode fmaxf would first quiet each (never NaN here) MFMA result with
-// an extra v_max x, x.
+// max(a, b, c): the compiler fuses it into one v_max3_f32 (it knows MFMA
+// results need no NaN quieting). Not inline assembly: the compiler must see
+// the read of the MFMA accumulators to insert the wait states the hardware
+// requires between an MFMA's write of a register and a VALU read of it.
 __device__ __forceinline__ float vmax3(float a, float b, float c) {
-  float r;
-  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-  return r;
+  return __builtin_fmaxf(__builtin_fmaxf(a, b), c);
 }
 
 // Lanes i and i ^ 32 combined: v_permlane32_swap of v with itself leaves
