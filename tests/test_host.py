@@ -204,3 +204,20 @@ def test_rope_table_matches_oracle():
         assert c.dtype == np.float32 and c.shape == (len(pos), hd // 2)
         assert np.max(np.abs(c - oc)) <= 6e-8
         assert np.max(np.abs(s - os_)) <= 6e-8
+
+
+def test_kernels_have_no_inline_assembly():
+    """The HIP sources hold no inline assembly: the compiler inserts the
+    wait states the hardware needs between dependent instructions (an
+    MFMA's write of a register and a VALU read of it, for one) only for
+    instructions it can see."""
+    csrc = os.path.join(os.path.dirname(_lib.__file__), "csrc")
+    pat = re.compile(r"\basm\s*(volatile\s*)?\(|__asm__")
+    found = []
+    for name in sorted(os.listdir(csrc)):
+        if name.endswith((".hip", ".h", ".cpp")):
+            with open(os.path.join(csrc, name)) as f:
+                for i, line in enumerate(f, 1):
+                    if pat.search(line.split("//")[0]):
+                        found.append(f"{name}:{i}")
+    assert not found, found
