@@ -51,6 +51,15 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef short v4s __attribute__((ext_vector_type(4)));
+
+// Four f16 of an LDS column, transposed across the 16-lane group.
+__device__ __forceinline__ v4h tr_read(const uint16_t *p) {
+  const v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4s *)(p));
+  return __builtin_bit_cast(v4h, r);
+}
 
 // Keys per tile: 64, or 32 at head_dim 256 (one 32-key sub-tile keeps the
 // S accumulators and the tile's load registers within the register file).
@@ -61,6 +70,11 @@ constexpr int tile_keys() {
   return HD >= 256 || WAVES == 1 ? 32 : 64;
 }
 constexpr int kWaveRows = 32;  // query rows per wave
+// V in LDS: row-major like K, read transposed (ds_read_b64_tr_b16) for the
+// P.V product, or stored transposed. Row-major measured 1.4-2.6 % faster at
+// head_dim 64 (prefill and the decode mode); transposed was as fast or up to
+// 2.4 % faster at 128 and 256, where the P.V product issues more V reads.
+constexpr bool v_rowmajor(int hd) { return hd <= 64; }
 // At head_dim 256 the two waves of a pair share 32 query rows: each holds
 // half of the head dimension of Q and O (the S product's two halves are
 // added through LDS), so a wave's O and Q fit two waves per SIMD.
@@ -106,9 +120,10 @@ template <int HD, int WAVES>
 struct Lds {
   static constexpr int BN = tile_keys<HD, WAVES>();
   static constexpr int KS = HD + 8;  // K row stride in halves (16 B pad)
-  static constexpr int VS = BN + 8;  // Vt row stride in halves
   static constexpr size_t k_bytes = (size_t)BN * KS * 2;
-  static constexpr size_t v_bytes = (size_t)HD * VS * 2;
+  static constexpr int VS = BN + 8;  // Vt row stride in halves (transposed)
+  static constexpr size_t v_bytes =
+      v_rowmajor(HD) ? k_bytes : (size_t)HD * VS * 2;
   // Workgroups of several waves double-buffer the tile, so one barrier a
   // tile both publishes it and retires the buffer the next tile overwrites
   // (a one-wave workgroup orders its own LDS accesses).
@@ -198,8 +213,8 @@ __global__ void __launch_bounds__(
   constexpr int kBM = block_rows<HD, WAVES>();
   using LD = Lds<HD, WAVES>;
   constexpr int KS = LD::KS, VS = LD::VS, BN = LD::BN;
+  constexpr bool TRV = v_rowmajor(HD);
   constexpr int NT = BN / 32;                 // 32-key sub-tiles per tile
-  constexpr int NPR = BN / 2;                 // key pairs per tile
   // This wave's share of the head dimension: all of it, or one half.
   constexpr int KC = HD / 16 / (SPLIT ? 2 : 1);  // MFMA k-steps of S
   constexpr int DT = HD / 32 / (SPLIT ? 2 : 1);  // 32-row tiles of O^T
@@ -313,6 +328,12 @@ __global__ void __launch_bounds__(
   // K row this lane feeds to the S product: sigma(ln), see the header.
   const int sig = 16 * (ln >> 4) + 8 * ((ln >> 2) & 1) + 4 * ((ln >> 3) & 1) +
                   (ln & 3);
+  // ds_read_b64_tr_b16 over a 16-lane group: lane 4a + c of the group gets
+  // element c of the 8-byte rows addressed by lanes a, a + 4, a + 8, a + 12.
+  // For lane l to receive V[k0 + 8hl + e][d0 + l % 32], e = 0..3, group
+  // lane s addresses key 8hl + s / 4 and dims 16 * (l / 16 % 2) + 4 (s % 4).
+  const int tr_key = 8 * hl + ((lane & 15) >> 2);
+  const int tr_dim = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
   const char *kbase = reinterpret_cast<const char *>(a.kc) +
                       (size_t)kvh * a.head_stride * 2;
@@ -320,16 +341,19 @@ __global__ void __launch_bounds__(
                       (size_t)kvh * a.head_stride * 2;
   // Tile loads. K goes to LDS row-major, so its 16-byte chunks are taken in
   // row order (chunk c: key c / CPR, column chunk c % CPR: whole rows per
-  // lane group, coalesced). V goes to LDS transposed, so its chunks are
-  // taken in key-pair order (pair c % (BN/2), column chunk c / (BN/2)): a
-  // lane loads keys 2p and 2p+1 of one column chunk and writes 8 dwords
-  // Vt[d][2p..2p+1]; consecutive lanes write consecutive dwords of one Vt
-  // row (with BN 64, a half-wave covers the 32 banks once). Block ids are fetched one tile ahead so a tile's loads
-  // issue back to back; loads are unconditional (invalid ones read block 0)
-  // and invalid V is zeroed at the LDS store, because masked keys get
-  // probability 0 and 0 * (stale V) must stay 0.
+  // lane group, coalesced). Row-major V (TRV) is taken the same way (a chunk
+  // of K and the same chunk of V share key, block id and offset) and read
+  // transposed with ds_read_b64_tr_b16. Transposed V is taken in key-pair
+  // order (pair c % (BN/2), column chunk c / (BN/2)): a lane loads keys 2p
+  // and 2p+1 of one column chunk and writes 8 dwords Vt[d][2p..2p+1];
+  // consecutive lanes write consecutive dwords of one Vt row (with BN 64, a
+  // half-wave covers the 32 banks once). Block ids are fetched one tile
+  // ahead so a tile's loads issue back to back; loads are unconditional
+  // (invalid ones read block 0) and invalid V is zeroed at the LDS store,
+  // because masked keys get probability 0 and 0 * (stale V) must stay 0.
+  constexpr int NPR = BN / 2;                     // key pairs per tile
   constexpr int VP = NPR * CPR;                   // V chunk pairs per tile
-  constexpr int CHV = VP >= NTH ? VP / NTH : 1;   // per thread
+  constexpr int CHV = TRV ? 1 : (VP >= NTH ? VP / NTH : 1);  // per thread
   const bool v_lane = VP >= NTH || tid < VP;
 
   // Are all the blocks holding keys below k_end valid? One scan of its
@@ -357,14 +381,6 @@ __global__ void __launch_bounds__(
     k_off[i] = ((k_key[i] & bs_mask) * HD + (c % CPR) * 8) * 2;
     k_db[i] = k_key[i] >> a.bs_log2;
   }
-  uint32_t v_key[CHV], v_off[CHV], v_db[CHV];
-#pragma unroll
-  for (int j = 0; j < CHV; ++j) {
-    const int c = tid + NTH * j;
-    v_key[j] = 2u * (uint32_t)(c % NPR);
-    v_off[j] = ((v_key[j] & bs_mask) * HD + (c / NPR) * 8) * 2;
-    v_db[j] = v_key[j] >> a.bs_log2;
-  }
   // (one block of all heads is far below 4 GiB; checked on the host)
   const uint32_t blk_bytes = (uint32_t)(a.block_stride * 2);
   // Tiles in flight: one ahead, or two for one-wave (decode) workgroups,
@@ -376,26 +392,40 @@ __global__ void __launch_bounds__(
   constexpr int DEPTH = WAVES == 1 ? 2 : 1;
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, DEPTH - 1>;
+  uint32_t v_key[CHV], v_off[CHV], v_db[CHV];
+  if constexpr (!TRV) {
+#pragma unroll
+    for (int j = 0; j < CHV; ++j) {
+      const int c = tid + NTH * j;
+      v_key[j] = 2u * (uint32_t)(c % NPR);
+      v_off[j] = ((v_key[j] & bs_mask) * HD + (c / NPR) * 8) * 2;
+      v_db[j] = v_key[j] >> a.bs_log2;
+    }
+  }
   uint32_t kid[CHK], vid[CHV];
-  u32x4 kr[DEPTH][CHK], vr0[DEPTH][CHV], vr1[DEPTH][CHV];
+  // Row-major V: vr holds the K chunks' V; transposed: vr0 / vr1 the pairs.
+  u32x4 kr[DEPTH][CHK], vr[DEPTH][TRV ? CHK : 1];
+  u32x4 vr0[DEPTH][CHV], vr1[DEPTH][CHV];
   uint32_t kbits[DEPTH], vbits[DEPTH];
 
   auto fetch_ids = [&](uint32_t kt) {
     const uint32_t b0 = kt >> a.bs_log2, last = a.max_blocks - 1u;
 #pragma unroll
     for (int i = 0; i < CHK; ++i) kid[i] = table[min(b0 + k_db[i], last)];
+    if constexpr (!TRV) {
 #pragma unroll
-    for (int j = 0; j < CHV; ++j) vid[j] = table[min(b0 + v_db[j], last)];
+      for (int j = 0; j < CHV; ++j) vid[j] = table[min(b0 + v_db[j], last)];
+    }
   };
   // Fused append (decode mode only: the one-wave instantiation): the item
   // holding the appended key loads the new K/V row into registers (after
   // its first tiles' loads are out), writes it into LDS over whatever the
   // cache held in the tile holding that key, and stores it to its slot at
   // the end (lanes < CPR, one 16-byte chunk each).
-  static_assert(WAVES != 1 || (HD <= NTH && CPR <= NTH),
-                "one lane per V element and per 16-byte chunk of the row");
+  static_assert(WAVES != 1 || (CPR <= NTH && (TRV || HD <= NTH)),
+                "one lane per 16-byte chunk of the row (and per V element)");
   u32x4 new_kc{}, new_vc{};
-  uint16_t new_ve = 0;  // V element tid of the new row (f16 bits)
+  uint16_t new_ve = 0;  // transposed V: element tid of the new row (f16)
   const size_t new_src = ((size_t)b * a.n_kv + kvh) * HD;
   auto load = [&](auto S, uint32_t kt) {
     constexpr int si = decltype(S)::value;
@@ -406,16 +436,21 @@ __global__ void __launch_bounds__(
       kbits[si] = ~0u;
       vbits[si] = ~0u;
 #pragma unroll
-      for (int i = 0; i < CHK; ++i)
-        kr[si][i] = *reinterpret_cast<const u32x4 *>(
-            kbase + (uint64_t)kid[i] * blk_bytes + (t_off + k_off[i]));
-      if (v_lane) {
+      for (int i = 0; i < CHK; ++i) {
+        const uint64_t off = (uint64_t)kid[i] * blk_bytes + (t_off + k_off[i]);
+        kr[si][i] = *reinterpret_cast<const u32x4 *>(kbase + off);
+        if constexpr (TRV)
+          vr[si][i] = *reinterpret_cast<const u32x4 *>(vbase + off);
+      }
+      if constexpr (!TRV) {
+        if (v_lane) {
 #pragma unroll
-        for (int j = 0; j < CHV; ++j) {
-          const char *vp =
-              vbase + (uint64_t)vid[j] * blk_bytes + (t_off + v_off[j]);
-          vr0[si][j] = *reinterpret_cast<const u32x4 *>(vp);
-          vr1[si][j] = *reinterpret_cast<const u32x4 *>(vp + HD * 2);
+          for (int j = 0; j < CHV; ++j) {
+            const char *vp =
+                vbase + (uint64_t)vid[j] * blk_bytes + (t_off + v_off[j]);
+            vr0[si][j] = *reinterpret_cast<const u32x4 *>(vp);
+            vr1[si][j] = *reinterpret_cast<const u32x4 *>(vp + HD * 2);
+          }
         }
       }
       return;
@@ -428,21 +463,25 @@ __global__ void __launch_bounds__(
       // of keys below k_end, and the last tile may reach past them.
       const bool okb = kid[i] < a.num_blocks;
       kbits[si] |= (uint32_t)(okb && kt + k_key[i] < k_end) << i;
-      kr[si][i] = *reinterpret_cast<const u32x4 *>(
-          kbase + (uint64_t)(okb ? kid[i] : 0u) * blk_bytes +
-          (t_off + k_off[i]));
+      const uint64_t off =
+          (uint64_t)(okb ? kid[i] : 0u) * blk_bytes + (t_off + k_off[i]);
+      kr[si][i] = *reinterpret_cast<const u32x4 *>(kbase + off);
+      if constexpr (TRV)
+        vr[si][i] = *reinterpret_cast<const u32x4 *>(vbase + off);
     }
+    if constexpr (!TRV) {
 #pragma unroll
-    for (int j = 0; j < CHV; ++j) {
-      const bool okb = vid[j] < a.num_blocks;
-      const uint32_t tok = kt + v_key[j];
-      vbits[si] |= (uint32_t)(okb && tok < k_end) << (2 * j);
-      vbits[si] |= (uint32_t)(okb && tok + 1 < k_end) << (2 * j + 1);
-      const char *vp = vbase + (uint64_t)(okb ? vid[j] : 0u) * blk_bytes +
-                       (t_off + v_off[j]);
-      if (v_lane) {
-        vr0[si][j] = *reinterpret_cast<const u32x4 *>(vp);
-        vr1[si][j] = *reinterpret_cast<const u32x4 *>(vp + HD * 2);
+      for (int j = 0; j < CHV; ++j) {
+        const bool okb = vid[j] < a.num_blocks;
+        const uint32_t tok = kt + v_key[j];
+        vbits[si] |= (uint32_t)(okb && tok < k_end) << (2 * j);
+        vbits[si] |= (uint32_t)(okb && tok + 1 < k_end) << (2 * j + 1);
+        const char *vp = vbase + (uint64_t)(okb ? vid[j] : 0u) * blk_bytes +
+                         (t_off + v_off[j]);
+        if (v_lane) {
+          vr0[si][j] = *reinterpret_cast<const u32x4 *>(vp);
+          vr1[si][j] = *reinterpret_cast<const u32x4 *>(vp + HD * 2);
+        }
       }
     }
   };
@@ -458,7 +497,8 @@ __global__ void __launch_bounds__(
     unsigned char *lb =
         smem + (LD::NBUF == 2 ? ((kt - k_begin) / BN) & 1u : 0u) * LD::buf;
     uint16_t *ks = reinterpret_cast<uint16_t *>(lb);
-    uint16_t *vt = reinterpret_cast<uint16_t *>(lb + LD::k_bytes);
+    // V: row-major (vs, stride KS) or transposed (Vt[d][key], stride VS).
+    uint16_t *vs = reinterpret_cast<uint16_t *>(lb + LD::k_bytes);
     uint8_t *kok = lb + LD::k_bytes + LD::v_bytes;
     if constexpr (LD::NBUF == 1)
       __syncthreads();  // the previous tile is no longer read
@@ -467,36 +507,44 @@ __global__ void __launch_bounds__(
       const int c = tid + NTH * i;
       const int key = c / CPR, dc = c % CPR;
       *reinterpret_cast<u32x4 *>(ks + key * KS + dc * 8) = kr[si][i];
+      if constexpr (TRV) {
+        const bool vok = tile_ok || ((kbits[si] >> i) & 1u);
+        *reinterpret_cast<u32x4 *>(vs + key * KS + dc * 8) =
+            vok ? vr[si][i] : u32x4{0u, 0u, 0u, 0u};
+      }
       // Every loader of a key writes the same flag.
       if (!all_ok) kok[key] = (uint8_t)((kbits[si] >> i) & 1u);
     }
-    if (v_lane) {
+    if constexpr (!TRV) {
+      if (v_lane) {
 #pragma unroll
-      for (int j = 0; j < CHV; ++j) {
-        const int c = tid + NTH * j;
-        const int pr = c % NPR, dc = c / NPR;
-        uint32_t *row = reinterpret_cast<uint32_t *>(vt + dc * 8 * VS) + pr;
-        if (tile_ok) {  // uniform: every key of the tile is readable
+        for (int j = 0; j < CHV; ++j) {
+          const int c = tid + NTH * j;
+          const int pr = c % NPR, dc = c / NPR;
+          uint32_t *row = reinterpret_cast<uint32_t *>(vs + dc * 8 * VS) + pr;
+          // Low halves of both keys go to row d = 8dc + 2e, high halves to
+          // d + 1; keys past the readable range are zeroed.
+          if (tile_ok) {  // uniform: every key of the tile is readable
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            // d = 8dc + 2e: low halves of both keys; d + 1: high halves.
-            row[(2 * e) * (VS / 2)] =
-                __builtin_amdgcn_perm(vr1[si][j][e], vr0[si][j][e], 0x05040100u);
-            row[(2 * e + 1) * (VS / 2)] =
-                __builtin_amdgcn_perm(vr1[si][j][e], vr0[si][j][e], 0x07060302u);
-          }
-        } else {
-          const uint32_t mask =
-              ((vbits[si] >> (2 * j)) & 1u ? 0xffffu : 0u) |
-              ((vbits[si] >> (2 * j + 1)) & 1u ? 0xffff0000u : 0u);
+            for (int e = 0; e < 4; ++e) {
+              row[(2 * e) * (VS / 2)] = __builtin_amdgcn_perm(
+                  vr1[si][j][e], vr0[si][j][e], 0x05040100u);
+              row[(2 * e + 1) * (VS / 2)] = __builtin_amdgcn_perm(
+                  vr1[si][j][e], vr0[si][j][e], 0x07060302u);
+            }
+          } else {
+            const uint32_t mask =
+                ((vbits[si] >> (2 * j)) & 1u ? 0xffffu : 0u) |
+                ((vbits[si] >> (2 * j + 1)) & 1u ? 0xffff0000u : 0u);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            row[(2 * e) * (VS / 2)] =
-                __builtin_amdgcn_perm(vr1[si][j][e], vr0[si][j][e], 0x05040100u) &
-                mask;
-            row[(2 * e + 1) * (VS / 2)] =
-                __builtin_amdgcn_perm(vr1[si][j][e], vr0[si][j][e], 0x07060302u) &
-                mask;
+            for (int e = 0; e < 4; ++e) {
+              row[(2 * e) * (VS / 2)] =
+                  __builtin_amdgcn_perm(vr1[si][j][e], vr0[si][j][e],
+                                        0x05040100u) & mask;
+              row[(2 * e + 1) * (VS / 2)] =
+                  __builtin_amdgcn_perm(vr1[si][j][e], vr0[si][j][e],
+                                        0x07060302u) & mask;
+            }
           }
         }
       }
@@ -504,9 +552,14 @@ __global__ void __launch_bounds__(
     if constexpr (WAVES == 1) {
       if (newtok - kt < (uint32_t)BN) {  // this tile holds the new key
         const uint32_t r = newtok - kt;
-        if (tid < CPR)
+        if (tid < CPR) {
           *reinterpret_cast<u32x4 *>(ks + r * KS + tid * 8) = new_kc;
-        if (tid < HD) vt[tid * VS + r] = new_ve;
+          if constexpr (TRV)
+            *reinterpret_cast<u32x4 *>(vs + r * KS + tid * 8) = new_vc;
+        }
+        if constexpr (!TRV) {
+          if (tid < HD) vs[tid * VS + r] = new_ve;
+        }
         if (!all_ok && tid == 0) kok[r] = 1;
       }
     }
@@ -637,8 +690,19 @@ __global__ void __launch_bounds__(
       for (int c = 0; c < 2; ++c)
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-          const half8 vf = *reinterpret_cast<const half8 *>(
-              vt + ((dh * DT + dt) * 32 + ln) * VS + 32 * t + 16 * c + 8 * hl);
+          // V^T fragment: dims dt*32 + ln, keys 32t + 16c + 8hl .. +8.
+          half8 vf;
+          if constexpr (TRV) {
+            // Two transposing reads of 4 keys each; the lane's address is
+            // the (key, dim) its 16-lane group hands out.
+            const uint16_t *vp = vs + (32 * t + 16 * c + tr_key) * KS +
+                                 (dh * DT + dt) * 32 + tr_dim;
+            const v4h lo = tr_read(vp), hi = tr_read(vp + 4 * KS);
+            vf = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          } else {
+            vf = *reinterpret_cast<const half8 *>(
+                vs + ((dh * DT + dt) * 32 + ln) * VS + 32 * t + 16 * c + 8 * hl);
+          }
           o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pb[t][c], o[dt],
                                                          0, 0, 0);
         }
@@ -659,13 +723,15 @@ __global__ void __launch_bounds__(
         new_kc = new_row_chunk(a.new_k, a.new_f32, new_src + tid * 8);
         new_vc = new_row_chunk(a.new_v, a.new_f32, new_src + tid * 8);
       }
-      if (tid < HD) {
-        const _Float16 v =
-            a.new_f32
-                ? (_Float16) static_cast<const float *>(a.new_v)[new_src + tid]
-                : __builtin_bit_cast(_Float16, static_cast<const uint16_t *>(
-                                                   a.new_v)[new_src + tid]);
-        new_ve = __builtin_bit_cast(uint16_t, v);
+      if constexpr (!TRV) {
+        if (tid < HD) {
+          const _Float16 v =
+              a.new_f32
+                  ? (_Float16) static_cast<const float *>(a.new_v)[new_src + tid]
+                  : __builtin_bit_cast(_Float16, static_cast<const uint16_t *>(
+                                                     a.new_v)[new_src + tid]);
+          new_ve = __builtin_bit_cast(uint16_t, v);
+        }
       }
     }
   }
