@@ -198,8 +198,8 @@ __device__ __forceinline__ uint32_t lo_bound(uint32_t p, int32_t window) {
 // arch VGPRs; at 256 only because each wave holds half of O and Q), 12
 // below: two or more waves per SIMD overlap one's softmax with another's
 // matrix work. (With all of O and Q in one wave, head_dim 256 ran one wave
-// per SIMD, its S product serialised on LDS reads: 18 % slower.) (128-key tiles at head_dim 64 were
-// measured 7-9 % slower than 64.)
+// per SIMD, its S product serialised on LDS reads: 18 % slower. 128-key
+// tiles at head_dim 64 were measured 7-9 % slower than 64.)
 template <int HD, int WAVES>
 __global__ void __launch_bounds__(
     64 * WAVES,
@@ -385,8 +385,7 @@ __global__ void __launch_bounds__(
   const uint32_t blk_bytes = (uint32_t)(a.block_stride * 2);
   // Tiles in flight: one ahead, or two for one-wave (decode) workgroups,
   // whose single wave's compute per tile is shorter than a load's latency.
-  // (Two in multi-wave workgroups gained at most 1 %, and one head_dim 256
-  // variant with them gave run-to-run differences of ~2e-4; not used.)
+  // (Two in multi-wave workgroups gained at most 1 %; not used.)
   // Register sets are selected by a compile-time index (a runtime index
   // would put the arrays in scratch).
   constexpr int DEPTH = WAVES == 1 ? 2 : 1;
