@@ -484,11 +484,13 @@ def _planned_vs_oracle(st, layer, db, q, window=0, sample=None):
     return np.abs(out[idx] - want).max(), plan, out
 
 
+@pytest.mark.parametrize("bs", [32, 128])
 @pytest.mark.parametrize("window", [0, 300])
-def test_planned_decode_ragged_splits(window):
+def test_planned_decode_ragged_splits(window, bs):
     """One long sequence among short ones forces split work items (and the
-    reduction rows); an empty sequence gets a zero row."""
-    bs, nkv, hd, H = 32, 2, 64, 14
+    reduction rows); an empty sequence gets a zero row. (Block size 128:
+    the matrix-core decode's 32-key tiles start inside blocks.)"""
+    nkv, hd, H = 2, 64, 14
     lens = np.array([9000, 0, 1, 31, 33, 700, 2048, 5], np.uint32)
     cfg = W.Config("pl", 9, 1, H, nkv, hd, bs, len(lens))
     db = W.ragged_batch(cfg, np.maximum(lens, 1), seed=4)
@@ -592,7 +594,7 @@ def test_config_qwen25_planned():
 @pytest.mark.parametrize("src", [torch.float32, torch.float16])
 @pytest.mark.parametrize("G,hd,bs,window", [(4, 64, 16, 0), (2, 128, 16, 0),
                                             (9, 64, 32, 0), (4, 256, 16, 300),
-                                            (7, 64, 16, 500)])
+                                            (7, 64, 16, 500), (7, 64, 128, 0)])
 def test_decode_step_equals_append_then_decode(planned, src, G, hd, bs,
                                                window):
     """rvkv_decode_step leaves the same cache bits as rvkv_append followed by
@@ -959,7 +961,8 @@ def _prefill_case(seed, B, Q, nkv, G, hd, bs, window, ragged=True,
 @pytest.mark.parametrize("G,hd,bs", [(1, 64, 16), (2, 128, 16), (4, 64, 32),
                                      (7, 64, 32), (8, 128, 8), (3, 32, 16),
                                      (16, 64, 16), (4, 256, 16), (1, 256, 8),
-                                     (2, 256, 64)])
+                                     (2, 256, 64), (4, 64, 128), (3, 32, 128),
+                                     (2, 128, 128)])
 def test_prefill_chunked_vs_oracle(G, hd, bs):
     """Several query-row tiles per (sequence, KV head) (G * Q > 128),
     chunk offsets that are not tile or block aligned, ragged read counts."""
