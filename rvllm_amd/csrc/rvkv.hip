@@ -908,12 +908,53 @@ __global__ void __launch_bounds__(64) decode_reduce_kernel(DecodeArgs a) {
     slot0 = b * a.n_parts;
     np = (ctx + a.part_tokens - 1) / a.part_tokens;
   }
+  const float *ml = a.ws_ml + ((size_t)slot0 * a.n_heads + h) * 2;
+  const size_t ml_step = (size_t)a.n_heads * 2;
+  const float *accp = a.ws_acc + ((size_t)slot0 * a.n_heads + h) * HD;
+  const size_t acc_step = (size_t)a.n_heads * HD;
+  const size_t hrow = (size_t)b * a.n_heads + h;
+  if (np <= 8) {
+    // Few partitions (the common case): every (m, l) pair (uniform loads)
+    // and every partial row are fetched at once, one round trip in all.
+    float m[8], l[8], x[8][EPL];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const bool live = (uint32_t)k < np;
+      m[k] = live ? ml[k * ml_step] : kNegBig;
+      l[k] = live ? ml[k * ml_step + 1] : 0.f;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) {
+        const int d = lane * EPL + e;
+        x[k][e] = live && d < HD ? accp[k * acc_step + d] : 0.f;
+      }
+    }
+    float M = kNegBig;
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (l[k] != 0.f) M = fmaxf(M, m[k]);
+    float acc[EPL], L = 0.f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      // (l = 0: a partition that saw no visible key stays out)
+      const float w = l[k] != 0.f ? __builtin_amdgcn_exp2f(m[k] - M) : 0.f;
+      L += l[k] * w;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) acc[e] += w != 0.f ? w * x[k][e] : 0.f;
+    }
+    const float inv = L > 0.f ? 1.0f / L : 0.f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      const int d = lane * EPL + e;
+      if (d < HD) a.out[hrow * HD + d] = acc[e] * inv;
+    }
+    return;
+  }
   // Lane i holds partition c + i's (m, l) for the 64-partition chunk at c;
   // M comes first, then every partial is weighted by 2^(m_i - M): the loads
   // of different partitions are independent, so they are all in flight at
   // once instead of one round trip per partition.
-  const float *ml = a.ws_ml + ((size_t)slot0 * a.n_heads + h) * 2;
-  const size_t ml_step = (size_t)a.n_heads * 2;
   float M = kNegBig;
   for (uint32_t c = 0; c < np; c += 64) {
     const uint32_t p = c + lane;
@@ -925,8 +966,6 @@ __global__ void __launch_bounds__(64) decode_reduce_kernel(DecodeArgs a) {
 #pragma unroll
   for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
   float L = 0.f;
-  const float *accp = a.ws_acc + ((size_t)slot0 * a.n_heads + h) * HD;
-  const size_t acc_step = (size_t)a.n_heads * HD;
   for (uint32_t c = 0; c < np; c += 64) {
     const uint32_t p = c + lane;
     float w = 0.f;
@@ -970,7 +1009,6 @@ __global__ void __launch_bounds__(64) decode_reduce_kernel(DecodeArgs a) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) L += __shfl_xor(L, o);
   const float inv = L > 0.f ? 1.0f / L : 0.f;
-  const size_t hrow = (size_t)b * a.n_heads + h;
 #pragma unroll
   for (int e = 0; e < EPL; ++e) {
     const int d = lane * EPL + e;
