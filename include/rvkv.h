@@ -352,14 +352,6 @@ int rvkv_bm_table(const rvkv_bm *bm, int64_t seq, uint32_t *table,
 int rvkv_argmax(const float *logits, uint32_t rows, uint32_t row_len,
                 uint32_t *out, rvkv_stream stream);
 
-/* ---- calibration (no counterpart in the reference) -------------------------
- * Reads `bytes` of device memory at `buf` once, in `workgroups` contiguous
- * slices (0: 2048), and writes nothing (sink may be NULL). Timing it on
- * buffers of a paged launch's size gives the plain streaming-read rate that
- * launch is compared with. Both 16-byte aligned. Asynchronous on `stream`. */
-int rvkv_read_probe(const void *buf, size_t bytes, uint32_t workgroups,
-                    uint32_t *sink, rvkv_stream stream);
-
 /* ---- continuous-batching scheduler with prefix cache -----
  * The contract rvllm's engine uses from the kv-cache-scheduler crate (0.2.0,
  * not vendored; used at src/engine.rs:351-539): a refcounted block pool

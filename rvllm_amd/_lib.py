@@ -71,7 +71,6 @@ SIGNATURES = {
     "rvkv_bm_refcount": (_u32, [_P, _u32]),
     "rvkv_bm_table": (_int, [_P, _i64, _pu32, _u32]),
     "rvkv_argmax": (_int, [_P, _u32, _u32, _P, _P]),
-    "rvkv_read_probe": (_int, [_P, _sz, _u32, _P, _P]),
     "rvkv_sched_last_error": (ctypes.c_char_p, []),
     "rvkv_sched_create": (_P, [_u32, _u32]),
     "rvkv_sched_destroy": (None, [_P]),
@@ -128,6 +127,33 @@ def load() -> ctypes.CDLL:
             fn.argtypes = args
         _lib = L
     return _lib
+
+
+_calib = None
+
+
+def load_calib() -> ctypes.CDLL:
+    """Loads librvkv_calib.so, the benchmark's streaming-read probe (not part
+    of the product ABI): rvkv_calib_read_probe(buf, bytes, workgroups, sink,
+    stream) -> 0 or -1, reason in rvkv_calib_last_error()."""
+    global _calib
+    if _calib is None:
+        path = os.path.join(HERE, "librvkv_calib.so")
+        if not os.path.exists(path):
+            raise RvkvError(f"{path} is not built (run: python -m "
+                            "rvllm_amd.build)", RVKV_EUNSUPPORTED)
+        L = ctypes.CDLL(path)
+        L.rvkv_calib_read_probe.restype = _int
+        L.rvkv_calib_read_probe.argtypes = [_P, _sz, _u32, _P, _P]
+        L.rvkv_calib_last_error.restype = ctypes.c_char_p
+        L.rvkv_calib_last_error.argtypes = []
+        _calib = L
+    return _calib
+
+
+def check_calib(rc: int) -> None:
+    if rc != 0:
+        raise RvkvError(load_calib().rvkv_calib_last_error().decode(), rc)
 
 
 def check(rc: int) -> None:

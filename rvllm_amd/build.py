@@ -1,4 +1,5 @@
-"""Builds librvkv.so (HIP kernels + C ABI + host block manager) for gfx950.
+"""Builds librvkv.so (HIP kernels + C ABI + host block manager) for gfx950,
+and the benchmark's streaming-read probe as a separate librvkv_calib.so.
 
 Run as ``python -m rvllm_amd.build``. hipcc cross-compiles for gfx950 on a
 host without a GPU; the .so is written in-tree next to this file.
@@ -12,13 +13,13 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 LIB = os.path.join(HERE, "librvkv.so")
+CALIB_LIB = os.path.join(HERE, "librvkv_calib.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 SOURCES = [
     os.path.join(HERE, "csrc", "rvkv.hip"),
     os.path.join(HERE, "csrc", "prefill.hip"),
     os.path.join(HERE, "csrc", "argmax.hip"),
-    os.path.join(HERE, "csrc", "calib.hip"),
     os.path.join(HERE, "csrc", "block_manager.cpp"),
     os.path.join(HERE, "csrc", "scheduler.cpp"),
 ]
@@ -49,6 +50,14 @@ def build(verbose: bool = False) -> str:
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp,
           *objs], verbose)
     os.replace(tmp, LIB)
+    # The bench-only read probe: its own library, outside the product ABI.
+    cobj = os.path.join(build_dir, "calib.hip.o")
+    _run([HIPCC, *HIP_FLAGS, "-c", os.path.join(HERE, "csrc", "calib.hip"),
+          "-o", cobj], verbose)
+    tmp = CALIB_LIB + ".tmp"
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp,
+          cobj], verbose)
+    os.replace(tmp, CALIB_LIB)
     return LIB
 
 

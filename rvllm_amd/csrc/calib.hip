@@ -3,17 +3,27 @@
 // nothing else in the launch (no tables, no arithmetic worth the name).
 // It has no counterpart in rvllm; it exists so a paged-KV launch of B bytes
 // can be compared with the best plain read of B bytes on the same device.
+// Built into its own librvkv_calib.so for the benchmark: it is not part of
+// the product ABI (include/rvkv.h).
 //
 // Each workgroup streams one contiguous slice with 16-byte loads, four in
 // flight per lane, and folds them into a sum that is stored only if it
 // equals an impossible sentinel (so the loads are not optimised away and
 // nothing is written).
-#include "pool.h"
+#include <hip/hip_runtime.h>
 
-using rvkv_detail::fail;
-using rvkv_detail::hip_fail;
+#include <cstddef>
+#include <cstdint>
+#include <string>
 
 namespace {
+
+thread_local std::string g_calib_error;
+
+int calib_fail(const char *reason) {
+  g_calib_error = std::string("read_probe: ") + reason;
+  return -1;
+}
 
 constexpr int kReadThreads = 256;
 constexpr int kReadUnroll = 4;
@@ -42,13 +52,15 @@ __global__ void __launch_bounds__(kReadThreads)
 
 extern "C" {
 
-int rvkv_read_probe(const void *buf, size_t bytes, uint32_t workgroups,
-                    uint32_t *sink, rvkv_stream stream) {
-  const char *op = "read_probe";
-  if (bytes == 0) return RVKV_OK;
-  if (!buf) return fail(RVKV_EINVAL, op, "buf is NULL");
+const char *rvkv_calib_last_error(void) { return g_calib_error.c_str(); }
+
+// Returns 0, or -1 with the reason in rvkv_calib_last_error().
+int rvkv_calib_read_probe(const void *buf, size_t bytes, uint32_t workgroups,
+                          uint32_t *sink, void *stream) {
+  if (bytes == 0) return 0;
+  if (!buf) return calib_fail("buf is NULL");
   if ((uintptr_t)buf % 16 || bytes % 16)
-    return fail(RVKV_EINVAL, op, "buf and bytes must be 16-byte aligned");
+    return calib_fail("buf and bytes must be 16-byte aligned");
   if (workgroups == 0) workgroups = 2048;
   const uint64_t n16 = bytes / 16;
   const uint64_t per_wg = (n16 + workgroups - 1) / workgroups;
@@ -56,7 +68,7 @@ int rvkv_read_probe(const void *buf, size_t bytes, uint32_t workgroups,
                      0, reinterpret_cast<hipStream_t>(stream),
                      static_cast<const uint4 *>(buf), n16, per_wg, sink);
   hipError_t e = hipGetLastError();
-  return e == hipSuccess ? RVKV_OK : hip_fail(op, e);
+  return e == hipSuccess ? 0 : calib_fail(hipGetErrorString(e));
 }
 
 }  // extern "C"

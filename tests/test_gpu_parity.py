@@ -1120,23 +1120,23 @@ def test_argmax_kat_and_random():
 
 
 def test_read_probe_runs_and_writes_nothing():
-    """rvkv_read_probe (the bench's streaming-read calibration) reads the
+    """The bench's streaming-read probe (librvkv_calib.so) reads the
     buffer, leaves the sink alone, and rejects unaligned sizes."""
     from rvllm_amd import _lib
     import ctypes
-    L = _lib.load()
+    L = _lib.load_calib()
     buf = torch.arange(1 << 20, dtype=torch.int32, device="cuda")
     sink = torch.full((1,), 7, dtype=torch.int32, device="cuda")
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     for wg in (0, 1, 3, 4096):
-        _lib.check(L.rvkv_read_probe(ctypes.c_void_p(buf.data_ptr()),
-                                     buf.numel() * 4, wg,
-                                     ctypes.c_void_p(sink.data_ptr()), stream))
+        _lib.check_calib(L.rvkv_calib_read_probe(
+            ctypes.c_void_p(buf.data_ptr()), buf.numel() * 4, wg,
+            ctypes.c_void_p(sink.data_ptr()), stream))
     torch.cuda.synchronize()
     assert sink.item() == 7
     with pytest.raises(RvkvError, match="read_probe: buf and bytes"):
-        _lib.check(L.rvkv_read_probe(ctypes.c_void_p(buf.data_ptr()), 20, 0,
-                                     None, stream))
+        _lib.check_calib(L.rvkv_calib_read_probe(
+            ctypes.c_void_p(buf.data_ptr()), 20, 0, None, stream))
 
 
 def _engine_pair(cfg, num_blocks, bs):

@@ -221,3 +221,20 @@ def test_kernels_have_no_inline_assembly():
                     if pat.search(line.split("//")[0]):
                         found.append(f"{name}:{i}")
     assert not found, found
+
+
+def test_bench_cpu_sample_keeps_the_batch_shape():
+    """bench.py's CPU-baseline sample: the first sequences over a compact
+    pool, shared blocks kept shared, tables and slots renumbered alike, and
+    the same per-sequence bytes as in the full batch."""
+    import bench
+    from rvllm_amd import workloads as W
+    db = W.qwen25_batch(batch=64)
+    sub, ids = bench.sample_batch(W, db, 20)
+    assert sub.batch == 20 and len(set(ids.tolist())) == len(ids)
+    for t_new, t_old in zip(sub.tables, db.tables[:20]):
+        assert np.array_equal(ids[t_new], t_old)
+    assert np.array_equal(ids[sub.slot_block], db.slot_block[:20])
+    assert sub.unique_kv_tokens() == W.DecodeBatch(
+        db.cfg, db.num_blocks, db.ctx_lens[:20], db.tables[:20],
+        db.slot_block[:20], db.slot_off[:20]).unique_kv_tokens()
