@@ -32,9 +32,11 @@
 // V is the one operand read across its rows (8 keys of one d column); it is
 // staged transposed in LDS, Vt[d][key], so that read is one 16-byte load.
 //
-// q is pre-scaled by scale*log2(e) and rounded to f16; probabilities are
-// rounded to f16 and the row sum adds the rounded values, so numerator and
-// denominator see the same weights. Products are exact in f32; sums are f32.
+// q is pre-scaled by scale*log2(e) and split into f16 hi + lo parts, each
+// multiplied with K on the matrix cores (so scores keep q's f32 precision);
+// probabilities are rounded to f16 and the row sum adds the rounded values,
+// so numerator and denominator see the same weights. Products are exact in
+// f32; sums are f32.
 #include "pool.h"
 
 #include <atomic>
@@ -300,7 +302,9 @@ __global__ void __launch_bounds__(
           ? ctx - 1u
           : 0xFFFFFFFFu;
 
-  half8 qf[KC];
+  // q pre-scaled, as f16 hi + lo (lo = the rounding residual of hi): the S
+  // product runs once on each, so scores keep q's f32 precision.
+  half8 qf[KC], ql[KC];
   {
     const float *qp = a.q + qrow * HD + dh * (KC * 16);
 #pragma unroll
@@ -311,10 +315,20 @@ __global__ void __launch_bounds__(
         x = *reinterpret_cast<const float4 *>(qp + d0);
         y = *reinterpret_cast<const float4 *>(qp + d0 + 4);
       }
-      qf[kc] = half8{(_Float16)(x.x * a.qscale), (_Float16)(x.y * a.qscale),
-                     (_Float16)(x.z * a.qscale), (_Float16)(x.w * a.qscale),
-                     (_Float16)(y.x * a.qscale), (_Float16)(y.y * a.qscale),
-                     (_Float16)(y.z * a.qscale), (_Float16)(y.w * a.qscale)};
+      const float xs[8] = {x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        // hi: the f32 product rounded to f16; lo: the residual of the exact
+        // product (fma). The empty asm pins the f32 product, so every use of
+        // hi sees one rounding (the compiler would otherwise also fuse the
+        // product into an f16 conversion, a different rounding, for some
+        // uses).
+        float v = xs[e] * a.qscale;
+        asm volatile("" : "+v"(v));
+        const _Float16 h = (_Float16)v;
+        qf[kc][e] = h;
+        ql[kc][e] = (_Float16)__builtin_fmaf(xs[e], a.qscale, -(float)h);
+      }
     }
   }
 
@@ -581,14 +595,20 @@ __global__ void __launch_bounds__(
     // dependency on the previous one of its chain is hidden.
     if (active) {
 #pragma unroll
-      for (int kc = 0; kc < KC; ++kc)
+      for (int kc = 0; kc < KC; ++kc) {
+        half8 kf[NT];
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-          const half8 kf = *reinterpret_cast<const half8 *>(
+          kf[t] = *reinterpret_cast<const half8 *>(
               ks + (32 * t + sig) * KS + dh * (KC * 16) + kc * 16 + hl * 8);
-          s[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[kc], s[t], 0,
+          s[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[t], qf[kc], s[t], 0,
                                                         0, 0);
         }
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+          s[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[t], ql[kc], s[t], 0,
+                                                        0, 0);
+      }
     }
     if constexpr (SPLIT) {
       // Add the partner's half of S^T. Each wave writes its own slot after
@@ -814,17 +834,16 @@ void launch_prefill(const PrefillArgs &a, dim3 grid, hipStream_t st) {
                      (Lds<HD, WAVES>::bytes), st, a);
 }
 
-// Waves per workgroup: 8 at head_dim 128 (measured ~5 % faster than 4) and
-// at 256 (four pairs, fixed); 4 at 64, where 8-wave workgroups would cost
-// the third resident wave per SIMD (measured ~7 % slower), and at 32.
-// RVKV_PREFILL_WAVES=4|8 overrides at 64 and 128.
+// Waves per workgroup: 8 at head_dim 128 (measured ~5 % faster than 4; 4
+// would not fit the hi/lo q in registers) and at 256 (four pairs); 4 at 64,
+// where 8-wave workgroups would cost the third resident wave per SIMD
+// (measured ~7 % slower), and at 32. RVKV_PREFILL_WAVES=4|8 overrides at 64.
 uint32_t prefill_waves(uint32_t hd) {
   static const char *env = getenv("RVKV_PREFILL_WAVES");
   static const uint32_t forced = env ? (uint32_t)atoi(env) : 0u;
-  if (split_dims((int)hd)) return 8u;  // four pairs
-  const bool can8 = hd == 64 || hd == 128;
-  if (forced == 4 || (forced == 8 && can8)) return forced;
-  return hd == 128 ? 8u : 4u;
+  if (split_dims((int)hd) || hd == 128) return 8u;  // (256: four pairs)
+  if (hd == 64 && (forced == 4 || forced == 8)) return forced;
+  return 4u;
 }
 
 }  // namespace
@@ -904,8 +923,7 @@ int rvkv_paged_prefill(rvkv_pool *pool, uint32_t layer, const float *q,
       else launch_prefill<64, 4>(a, grid, pool->stream);
       break;
     case 128:
-      if (waves == 8) launch_prefill<128, 8>(a, grid, pool->stream);
-      else launch_prefill<128, 4>(a, grid, pool->stream);
+      launch_prefill<128, 8>(a, grid, pool->stream);
       break;
     default: launch_prefill<256, 8>(a, grid, pool->stream); break;
   }

@@ -468,6 +468,51 @@ __device__ __forceinline__ float row_group_sum(float x) {
 
 constexpr float kNegBig = -1.0e30f;  // finite "minus infinity" for m
 
+// Zero bytes covering one wave-wide load (64 lanes x 16 B, two loads per
+// row at most): the V source of masked keys.
+__device__ __align__(16) uint4 g_zero_rows[128];
+
+// q.k over the lane's NL*8 elements. q is carried as an f16 pair (hi, lo)
+// with hi + lo = q to ~2^-22 relative, so the score keeps q's f32 precision
+// while every product stays an exact f16 x f16 fdot2 with f32 accumulation
+// (K is f16 in the cache, so nothing else is rounded).
+template <int NL>
+__device__ __forceinline__ float qk_dot(const h2 (&qh)[NL][4],
+                                        const h2 (&ql)[NL][4],
+                                        const uint4 (&k)[NL]) {
+  float d = 0.f;
+#pragma unroll
+  for (int j = 0; j < NL; ++j) {
+    d = __builtin_amdgcn_fdot2(ql[j][0], as_h2(k[j].x), d, false);
+    d = __builtin_amdgcn_fdot2(ql[j][1], as_h2(k[j].y), d, false);
+    d = __builtin_amdgcn_fdot2(ql[j][2], as_h2(k[j].z), d, false);
+    d = __builtin_amdgcn_fdot2(ql[j][3], as_h2(k[j].w), d, false);
+  }
+#pragma unroll
+  for (int j = 0; j < NL; ++j) {
+    d = __builtin_amdgcn_fdot2(qh[j][0], as_h2(k[j].x), d, false);
+    d = __builtin_amdgcn_fdot2(qh[j][1], as_h2(k[j].y), d, false);
+    d = __builtin_amdgcn_fdot2(qh[j][2], as_h2(k[j].z), d, false);
+    d = __builtin_amdgcn_fdot2(qh[j][3], as_h2(k[j].w), d, false);
+  }
+  return d;
+}
+
+// Splits x*sc into f16 hi + lo: hi = the f32 product rounded to f16 and
+// lo = the residual of the exact product (fma) rounded to f16. The empty
+// asm pins the f32 product, so every use of hi sees one rounding (the
+// compiler would otherwise also fuse the product into an f16 conversion, a
+// different rounding, for some uses).
+__device__ __forceinline__ void split_f16(float x0, float x1, float sc, h2 &hi,
+                                          h2 &lo) {
+  float p0 = x0 * sc, p1 = x1 * sc;
+  asm volatile("" : "+v"(p0), "+v"(p1));
+  const _Float16 a = (_Float16)p0, b = (_Float16)p1;
+  hi = h2{a, b};
+  lo = h2{(_Float16)__builtin_fmaf(x0, sc, -(float)a),
+          (_Float16)__builtin_fmaf(x1, sc, -(float)b)};
+}
+
 // Online-softmax state of one row group for GT query heads: running max m
 // (log2 domain), running sum l and acc over the lane's NL*8 elements.
 template <int GT, int NL>
@@ -478,9 +523,15 @@ struct SoftmaxState {
 // One chunk of U wave-wide loads (U*RPL tokens): scores, online softmax
 // update and P.V. MASKED handles partial chunks (keys outside [lo, t1) or
 // unreadable blocks get probability 0); full chunks skip every test.
+// Masked keys are excluded twice: their score becomes -inf (probability 0)
+// and, in the caller, their V row is loaded from g_zero_rows instead of the
+// cache, so whatever the slot holds (an inf from an overflowing append,
+// another sequence's data behind an unreadable block id) never meets a
+// zero probability as 0 * inf.
 template <int R, int GT, int U, int NL, bool MASKED>
 __device__ __forceinline__ void decode_chunk(SoftmaxState<GT, NL> &st,
                                              const h2 (&qh)[GT][NL][4],
+                                             const h2 (&ql)[GT][NL][4],
                                              const uint4 (&kr)[U][NL],
                                              const uint4 (&vr)[U][NL],
                                              uint32_t tok0, uint32_t lo,
@@ -492,15 +543,7 @@ __device__ __forceinline__ void decode_chunk(SoftmaxState<GT, NL> &st,
   for (int u = 0; u < U; ++u) {
 #pragma unroll
     for (int g = 0; g < GT; ++g) {
-      float d = 0.f;
-#pragma unroll
-      for (int j = 0; j < NL; ++j) {
-        d = __builtin_amdgcn_fdot2(qh[g][j][0], as_h2(kr[u][j].x), d, false);
-        d = __builtin_amdgcn_fdot2(qh[g][j][1], as_h2(kr[u][j].y), d, false);
-        d = __builtin_amdgcn_fdot2(qh[g][j][2], as_h2(kr[u][j].z), d, false);
-        d = __builtin_amdgcn_fdot2(qh[g][j][3], as_h2(kr[u][j].w), d, false);
-      }
-      s[u][g] = row_group_sum<R>(d);
+      s[u][g] = row_group_sum<R>(qk_dot<NL>(qh[g], ql[g], kr[u]));
     }
     if constexpr (MASKED) {
       const uint32_t tok = tok0 + u * RPL;
@@ -676,18 +719,19 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
   const uint32_t skip = lo > t0 ? (lo - t0) / (TC * W) * (TC * W) : 0;
   const uint32_t start = first + skip;
   if (start < t1) {
-    // q for the GT heads, this lane's elements, pre-scaled, as f16 pairs.
-    h2 qh[GT][NL][4];
+    // q for the GT heads, this lane's elements, pre-scaled, as f16 hi/lo
+    // pairs.
+    h2 qh[GT][NL][4], ql[GT][NL][4];
 #pragma unroll
     for (int g = 0; g < GT; ++g) {
 #pragma unroll
       for (int j = 0; j < NL; ++j) {
         const float sc = a.qscale;
         const float4 x0 = qraw[g][j][0], x1 = qraw[g][j][1];
-        qh[g][j][0] = h2{(_Float16)(x0.x * sc), (_Float16)(x0.y * sc)};
-        qh[g][j][1] = h2{(_Float16)(x0.z * sc), (_Float16)(x0.w * sc)};
-        qh[g][j][2] = h2{(_Float16)(x1.x * sc), (_Float16)(x1.y * sc)};
-        qh[g][j][3] = h2{(_Float16)(x1.z * sc), (_Float16)(x1.w * sc)};
+        split_f16(x0.x, x0.y, sc, qh[g][j][0], ql[g][j][0]);
+        split_f16(x0.z, x0.w, sc, qh[g][j][1], ql[g][j][1]);
+        split_f16(x1.x, x1.y, sc, qh[g][j][2], ql[g][j][2]);
+        split_f16(x1.z, x1.w, sc, qh[g][j][3], ql[g][j][3]);
       }
     }
 
@@ -708,18 +752,31 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
         ids[u] = table[min((start + u * RPL) >> a.bs_log2, last_blk)];
     }
 
+    const char *zero_v = reinterpret_cast<const char *>(g_zero_rows) + lane_off;
     for (uint32_t ch = start; ch < t1; ch += stride) {
       uint4 kr[U][NL], vr[U][NL];
       uint32_t okmask = 0;
 #pragma unroll
+      for (int u = 0; u < U; ++u)
+        okmask |= (uint32_t)(ids[u] < a.num_blocks) << u;
+      // The chunk holding this step's appended key takes the masked path,
+      // which leaves that key out.
+      const bool has_new = newtok >= ch && newtok < ch + TC;
+      const bool full = !has_new && ch >= lo && ch + TC <= t1 &&
+                        okmask == (1u << U) - 1u;
+#pragma unroll
       for (int u = 0; u < U; ++u) {
         const uint32_t tb = ch + u * RPL;  // first token of this load
-        const bool ok = ids[u] < a.num_blocks;
-        okmask |= (uint32_t)ok << u;
+        const bool ok = (okmask >> u) & 1u;
         const uint64_t uoff = (uint64_t)(ok ? ids[u] : 0u) * blk_bytes +
                               (uint64_t)(tb & bs_mask) * (HD * 2);
         const char *kp = kbase + uoff + lane_off;
         const char *vp = vbase + uoff + lane_off;
+        if (!full) {  // (wave-uniform)
+          const uint32_t tok = tb + rg;
+          const bool valid = ok && tok >= lo && tok < t1 && tok != newtok;
+          vp = valid ? vp : zero_v;
+        }
 #pragma unroll
         for (int j = 0; j < NL; ++j) {
           kr[u][j] = *reinterpret_cast<const uint4 *>(kp + j * R * 16);
@@ -731,16 +788,11 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
       for (int u = 0; u < U; ++u)
         ids[u] = table[min((ch + stride + u * RPL) >> a.bs_log2, last_blk)];
 
-      // The chunk holding this step's appended key takes the masked path,
-      // which leaves that key out.
-      const bool has_new = newtok >= ch && newtok < ch + TC;
-      const bool full = !has_new && ch >= lo && ch + TC <= t1 &&
-                        okmask == (1u << U) - 1u;
       if (full)
-        decode_chunk<R, GT, U, NL, false>(st, qh, kr, vr, ch + rg, lo, t1,
+        decode_chunk<R, GT, U, NL, false>(st, qh, ql, kr, vr, ch + rg, lo, t1,
                                           okmask, newtok);
       else
-        decode_chunk<R, GT, U, NL, true>(st, qh, kr, vr, ch + rg, lo, t1,
+        decode_chunk<R, GT, U, NL, true>(st, qh, ql, kr, vr, ch + rg, lo, t1,
                                          okmask, newtok);
     }
 
@@ -790,15 +842,7 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
       }
 #pragma unroll
       for (int g = 0; g < GT; ++g) {
-        float d = 0.f;
-#pragma unroll
-        for (int j = 0; j < NL; ++j) {
-          d = __builtin_amdgcn_fdot2(qh[g][j][0], as_h2(nk[j].x), d, false);
-          d = __builtin_amdgcn_fdot2(qh[g][j][1], as_h2(nk[j].y), d, false);
-          d = __builtin_amdgcn_fdot2(qh[g][j][2], as_h2(nk[j].z), d, false);
-          d = __builtin_amdgcn_fdot2(qh[g][j][3], as_h2(nk[j].w), d, false);
-        }
-        d = row_group_sum<R>(d);
+        const float d = row_group_sum<R>(qk_dot<NL>(qh[g], ql[g], nk));
         if (rg == 0) {
           const float mx = fmaxf(st.m[g], d);
           const float corr = __builtin_amdgcn_exp2f(st.m[g] - mx);
