@@ -317,17 +317,19 @@ __global__ void __launch_bounds__(
       }
       const float xs[8] = {x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        // hi: the f32 product rounded to f16; lo: the residual of the exact
-        // product (fma). The empty asm pins the f32 product, so every use of
-        // hi sees one rounding (the compiler would otherwise also fuse the
-        // product into an f16 conversion, a different rounding, for some
-        // uses).
-        float v = xs[e] * a.qscale;
-        asm volatile("" : "+v"(v));
-        const _Float16 h = (_Float16)v;
-        qf[kc][e] = h;
-        ql[kc][e] = (_Float16)__builtin_fmaf(xs[e], a.qscale, -(float)h);
+      for (int e = 0; e < 8; e += 2) {
+        // hi: the f32 product rounded toward zero to f16 (one intrinsic,
+        // so every use sees the same value; a plain conversion may be fused
+        // with the product and rounded differently at different uses); lo:
+        // the residual of the exact product (fma), rounded to f16.
+        const h2 hp = __builtin_bit_cast(
+            h2, __builtin_amdgcn_cvt_pkrtz(xs[e] * a.qscale,
+                                           xs[e + 1] * a.qscale));
+        qf[kc][e] = hp[0];
+        qf[kc][e + 1] = hp[1];
+        ql[kc][e] = (_Float16)__builtin_fmaf(xs[e], a.qscale, -(float)hp[0]);
+        ql[kc][e + 1] =
+            (_Float16)__builtin_fmaf(xs[e + 1], a.qscale, -(float)hp[1]);
       }
     }
   }

@@ -498,19 +498,15 @@ __device__ __forceinline__ float qk_dot(const h2 (&qh)[NL][4],
   return d;
 }
 
-// Splits x*sc into f16 hi + lo: hi = the f32 product rounded to f16 and
-// lo = the residual of the exact product (fma) rounded to f16. The empty
-// asm pins the f32 product, so every use of hi sees one rounding (the
-// compiler would otherwise also fuse the product into an f16 conversion, a
-// different rounding, for some uses).
+// Splits x*sc into f16 hi + lo: hi = the f32 product rounded toward zero to
+// f16 (one intrinsic, so every use sees the same value; a plain conversion
+// may be fused with the product and rounded differently at different uses)
+// and lo = the residual of the exact product (fma) rounded to f16.
 __device__ __forceinline__ void split_f16(float x0, float x1, float sc, h2 &hi,
                                           h2 &lo) {
-  float p0 = x0 * sc, p1 = x1 * sc;
-  asm volatile("" : "+v"(p0), "+v"(p1));
-  const _Float16 a = (_Float16)p0, b = (_Float16)p1;
-  hi = h2{a, b};
-  lo = h2{(_Float16)__builtin_fmaf(x0, sc, -(float)a),
-          (_Float16)__builtin_fmaf(x1, sc, -(float)b)};
+  hi = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(x0 * sc, x1 * sc));
+  lo = h2{(_Float16)__builtin_fmaf(x0, sc, -(float)hi[0]),
+          (_Float16)__builtin_fmaf(x1, sc, -(float)hi[1])};
 }
 
 // Online-softmax state of one row group for GT query heads: running max m
