@@ -131,6 +131,24 @@ int rvkv_paged_decode(const rvkv_pool *pool, uint32_t layer, const float *q,
                       uint32_t max_ctx_len, float scale, int32_t window,
                       float *out, void *ws, size_t ws_bytes);
 
+/* rvkv_paged_decode without a workspace argument and without any device
+ * allocation. No counterpart in the reference: it is for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). The split-sequence partials go to a static 8 MiB
+ * array of device memory that each GPU holds for the life of the process;
+ * a shape whose rvkv_decode_workspace_bytes exceeds 8 MiB is rejected with
+ * RVKV_EUNSUPPORTED (only reachable at head_dim 256 with > 4 query heads per
+ * KV head). Every call on one GPU shares that GPU's array, so calls
+ * that overlap on one GPU (several streams, several threads) race; calls
+ * queued on one stream do not. Same arguments, rules and results as
+ * rvkv_paged_decode otherwise. */
+int rvkv_paged_decode_noalloc(const rvkv_pool *pool, uint32_t layer,
+                              const float *q, const uint32_t *block_tables,
+                              const uint32_t *ctx_lens, uint32_t batch,
+                              uint32_t max_blocks, uint32_t n_heads,
+                              uint32_t max_ctx_len, float scale,
+                              int32_t window, float *out);
+
 /* Workspace bytes rvkv_paged_decode needs for this batch shape. */
 size_t rvkv_decode_workspace_bytes(const rvkv_pool *pool, uint32_t batch,
                                    uint32_t n_heads, uint32_t max_ctx_len);

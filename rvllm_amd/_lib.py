@@ -31,6 +31,8 @@ SIGNATURES = {
     "rvkv_gather": (_int, [_P, _u32, _P, _u32, _u32, _u32, _P, _P, _int]),
     "rvkv_paged_decode": (_int, [_P, _u32, _P, _P, _P, _u32, _u32, _u32, _u32,
                                  _f32, _i32, _P, _P, _sz]),
+    "rvkv_paged_decode_noalloc": (_int, [_P, _u32, _P, _P, _P, _u32, _u32,
+                                         _u32, _u32, _f32, _i32, _P]),
     "rvkv_decode_workspace_bytes": (_sz, [_P, _u32, _u32, _u32]),
     "rvkv_decode_partition_tokens": (_u32, [_P, _u32, _u32, _u32]),
     "rvkv_decode_plan_create": (_int, [_P, _P, _u32, _u32, _i32,

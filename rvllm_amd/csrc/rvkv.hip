@@ -16,6 +16,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <algorithm>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -1614,6 +1615,53 @@ int plan_check_args(const char *op, const rvkv_pool *pool,
 
 }  // namespace
 
+// Decode partials of rvkv_paged_decode_noalloc: one array per GPU, for the
+// life of the process. Host code never uses this name as an address (it
+// is a host-side stand-in); scratch_device_ptr() returns the device's copy.
+// 8 MiB holds the partials of every uniform decode up to head_dim 256 with
+// up to 4 query heads per KV head (at most ~1024*G partial rows, each
+// (head_dim + 2) floats), any batch.
+constexpr size_t kScratchBytes = (size_t)8 << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices];
+
+// Device `dev`'s copy of `scratch`, looked up once per device (with that
+// device current; the caller's current device is restored).
+int scratch_device_ptr(const char *op, int dev, void **out) {
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(RVKV_EUNSUPPORTED, op, "device index too large");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    int cur = 0;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess) return hip_fail(op, e);
+    if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess)
+      return hip_fail(op, e);
+    void *ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (cur != dev) (void)hipSetDevice(cur);
+    if (e != hipSuccess) return hip_fail(op, e);
+    if (!ptr) return fail(RVKV_EHIP, op, "scratch has no device address");
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return RVKV_OK;
+}
+
+int paged_decode_ws(const char *op, const rvkv_pool *pool, uint32_t layer,
+                    const float *q, const uint32_t *block_tables,
+                    const uint32_t *ctx_lens, uint32_t batch,
+                    uint32_t max_blocks, uint32_t n_heads,
+                    uint32_t max_ctx_len, float scale, int32_t window,
+                    float *out, void *ws, size_t ws_bytes, bool no_alloc);
+
+}  // namespace
+
 extern "C" {
 
 int rvkv_paged_decode(const rvkv_pool *pool, uint32_t layer, const float *q,
@@ -1621,7 +1669,32 @@ int rvkv_paged_decode(const rvkv_pool *pool, uint32_t layer, const float *q,
                       uint32_t batch, uint32_t max_blocks, uint32_t n_heads,
                       uint32_t max_ctx_len, float scale, int32_t window,
                       float *out, void *ws, size_t ws_bytes) {
-  const char *op = "paged_decode";
+  return paged_decode_ws("paged_decode", pool, layer, q, block_tables,
+                         ctx_lens, batch, max_blocks, n_heads, max_ctx_len,
+                         scale, window, out, ws, ws_bytes, false);
+}
+
+int rvkv_paged_decode_noalloc(const rvkv_pool *pool, uint32_t layer,
+                              const float *q, const uint32_t *block_tables,
+                              const uint32_t *ctx_lens, uint32_t batch,
+                              uint32_t max_blocks, uint32_t n_heads,
+                              uint32_t max_ctx_len, float scale,
+                              int32_t window, float *out) {
+  return paged_decode_ws("paged_decode_noalloc", pool, layer, q,
+                         block_tables, ctx_lens, batch, max_blocks, n_heads,
+                         max_ctx_len, scale, window, out, nullptr, 0, true);
+}
+
+}  // extern "C"
+
+namespace {
+
+int paged_decode_ws(const char *op, const rvkv_pool *pool, uint32_t layer,
+                    const float *q, const uint32_t *block_tables,
+                    const uint32_t *ctx_lens, uint32_t batch,
+                    uint32_t max_blocks, uint32_t n_heads,
+                    uint32_t max_ctx_len, float scale, int32_t window,
+                    float *out, void *ws, size_t ws_bytes, bool no_alloc) {
   if (pool && batch == 0) return RVKV_OK;
   DecodeArgs a;
   uint32_t gt;
@@ -1632,6 +1705,17 @@ int rvkv_paged_decode(const rvkv_pool *pool, uint32_t layer, const float *q,
   if (batch > 65535) return fail(RVKV_EUNSUPPORTED, op, "batch too large");
   if (max_ctx_len == 0) max_ctx_len = 1;
   const WsLayout w = ws_layout(pool, batch, n_heads, max_ctx_len);
+  if (no_alloc && w.bytes > 0) {
+    // The partials go to this device's static scratch array: no
+    // allocation, and nothing in it needs clearing (every partial the
+    // reduction reads is written by this call's first launch).
+    if (w.bytes > kScratchBytes)
+      return fail(RVKV_EUNSUPPORTED, op,
+                  "decode partials exceed the 8 MiB scratch; use "
+                  "rvkv_paged_decode with a workspace");
+    if ((rc = scratch_device_ptr(op, pool->device, &ws))) return rc;
+    ws_bytes = kScratchBytes;
+  }
   if ((rc = check_ws(op, ws, ws_bytes, w.bytes))) return rc;
   a.ws_acc = w.n_parts > 1 ? (float *)((char *)ws + w.acc_off) : nullptr;
   a.ws_ml = w.n_parts > 1 ? (float *)((char *)ws + w.ml_off) : nullptr;
@@ -1642,6 +1726,10 @@ int rvkv_paged_decode(const rvkv_pool *pool, uint32_t layer, const float *q,
   return launch_decode_pair(op, a, pool->head_dim, gt, grid,
                             dim3(n_heads, batch), w.n_parts > 1, pool->stream);
 }
+
+}  // namespace
+
+extern "C" {
 
 int rvkv_decode_plan_create(const rvkv_pool *pool,
                             const uint32_t *ctx_lens_host, uint32_t batch,
