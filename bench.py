@@ -35,7 +35,9 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--config", default="qwen3-0.6b")
+    p.add_argument("--config", default=None,
+                   help="workload (default: qwen3-0.6b; gemma-3-270m for "
+                   "--churn; qwen2.5-0.5b for --cow)")
     p.add_argument("--batch", type=int, default=0,
                    help="override the number of sequences (uniform configs)")
     p.add_argument("--ctx", type=int, default=0,
@@ -89,7 +91,11 @@ def parse():
     p.add_argument("--copy-calibration", action="store_true",
                    help="only time a plain 2 GiB device-to-device copy (the "
                         "achievable-bandwidth and PMC-counter reference)")
-    return p.parse_args()
+    a = p.parse_args()
+    if a.config is None:
+        a.config = ("gemma-3-270m" if a.churn else
+                    "qwen2.5-0.5b" if a.cow else "qwen3-0.6b")
+    return a
 
 
 def copy_calibration(torch, steps):
@@ -580,9 +586,7 @@ def run_cow(args, torch, W):
     one rvkv_copy_blocks covers every layer, K and V. Algorithmic bytes:
     each copied block read and written, all layers, K and V."""
     from rvllm_amd.kv_storage import HipKvStorage
-    # (The default config has no sharers; its pairs come from Qwen2.5.)
-    name = ("qwen2.5-0.5b" if args.config == "llama-3.2-1b" and
-            not args.cow_blocks else args.config)
+    name = args.config
     db = build_workload(W, name, args.batch, args.ctx)
     c = db.cfg
     st = HipKvStorage(c.n_layers, db.num_blocks, c.block_size, c.n_kv_heads,

@@ -145,6 +145,10 @@ class ChurnDriver:
             self.decode_bytes(lens) + append_bytes(self.batch, c)
             + append_bytes(n_prompt_tok, c))
         self.last = (tables.copy(), lens.copy(), blocks.copy(), offs.copy())
+        # This step's prompt slots (rows pk/pv[:n] went there), for checks.
+        self.last_prompt = (
+            hb["pb"][:n_prompt_tok].numpy().view(np.uint32).copy(),
+            hb["po"][:n_prompt_tok].numpy().view(np.uint32).copy())
         self.step_index += 1
 
     def _layers(self, db, n_prompt_tok) -> None:

@@ -743,6 +743,67 @@ def test_churn_driver_parity():
         drv.bm.num_blocks_of(int(s)) for s in drv.running) == drv.num_blocks
 
 
+def test_churn_full_scale_gemma():
+    """configs[4] at its real scale: gemma-3-270m shape (18 layers, 4 q / 1
+    KV head, head_dim 256, block_size 16), 1024 sequences at 1024 tokens
+    over the 81 920-block pool with a seeded-shuffled free list, 10 % churn
+    with 64-token prompts, a few engine steps. Checks, on the last step:
+    block accounting (every block free or owned by exactly one running
+    sequence); in two layers, every block's checksum unchanged except the
+    blocks this step wrote, and in those the written rows (prompt rows and
+    decode appends) bit-exact and every other row unchanged; 16 sampled
+    sequences' decode output against the oracle (2e-3)."""
+    from rvllm_amd.engine_sim import ChurnDriver
+    cfg = W.CONFIGS["gemma-3-270m"]
+    drv = ChurnDriver(cfg, 1024, 1024, prompt_len=64, churn=0.1, steps=200)
+    assert drv.num_blocks == 81920
+    all_ids = dev_u32(np.arange(drv.num_blocks))
+    check_layers = (0, cfg.n_layers - 1)
+    for _ in range(3):
+        drv.step()
+    torch.cuda.synchronize()
+    before = {(l, w): drv.st.block_checksums(l, w, all_ids).cpu().numpy()
+              for l in check_layers for w in (0, 1)}
+    drv.step()  # the checked step
+    torch.cuda.synchronize()
+    tables, lens, blocks, offs = drv.last
+    pb, po = drv.last_prompt
+    assert len(pb) == drv.n_churn * 64
+    # accounting
+    owned = np.concatenate([drv.bm.table(int(s)) for s in drv.running])
+    assert len(np.unique(owned)) == len(owned)
+    assert drv.bm.available() + len(owned) == drv.num_blocks
+    written = np.unique(np.concatenate([blocks, pb]))
+    others = np.setdiff1d(np.arange(drv.num_blocks), written)
+    for layer in check_layers:
+        for which, src_new, src_prompt in ((0, drv.nk, drv.pk),
+                                           (1, drv.nv, drv.pv)):
+            after = drv.st.block_checksums(layer, which,
+                                           all_ids).cpu().numpy()
+            assert np.array_equal(after[others],
+                                  before[(layer, which)][others])
+            rows = drv.st.read_blocks(layer, which, dev_u32(written)) \
+                .cpu().numpy().view(np.uint16)
+            at = {int(b): i for i, b in enumerate(written)}
+            want_dec = orc.f32_to_f16_bits(src_new[layer].cpu().numpy())
+            got_dec = rows[[at[int(b)] for b in blocks], offs]
+            assert np.array_equal(got_dec, want_dec)
+            want_pr = orc.f32_to_f16_bits(src_prompt.cpu().numpy()[:len(pb)])
+            got_pr = rows[[at[int(b)] for b in pb], po]
+            assert np.array_equal(got_pr, want_pr)
+    sample = list(range(0, 1024, 64))
+    layer = cfg.n_layers - 1
+    bs = cfg.block_size
+    cache, padded, mb = oracle_subset(
+        drv.st, layer, [tables[b, :-(-int(lens[b]) // bs)] for b in sample],
+        lens[sample])
+    want = orc.paged_decode_f64(cache, drv.q[layer].cpu().numpy()[sample],
+                                padded.reshape(-1), mb, lens[sample])
+    got = drv.out[layer].cpu().numpy()[sample]
+    assert np.abs(got - want).max() < ATOL
+    drv.st.close()
+
+
 # ---- full-size append / gather (size-independent checks) -------------------
 def test_full_size_gather_llama_layer():
     """One full Llama-3.2-1B layer (8192 blocks, 64 x 2048): the padded
