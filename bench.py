@@ -986,9 +986,11 @@ def main():
                            tables, ctx, max_ctx, plan=plan, out=out[layer],
                            ws=ws)
 
+    host_tables = db.padded_tables()
+
     def step():
         if plan is not None:
-            plan.update(db.ctx_lens)
+            plan.update(db.ctx_lens, host_tables)
         for layer in range(L):
             if args.unfused:
                 st.write_tokens(layer, sb, so, nk[layer], nv[layer])

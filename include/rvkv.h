@@ -182,6 +182,16 @@ int rvkv_decode_plan_create(const rvkv_pool *pool,
  * upload. The plan keeps a pointer to the pool: destroy it first. */
 int rvkv_decode_plan_update(rvkv_decode_plan *plan,
                             const uint32_t *ctx_lens_host, uint32_t batch);
+/* rvkv_decode_plan_update with the host copy of this step's padded block
+ * tables ([batch, max_blocks], what GatherPlan::new takes besides the read
+ * counts, src/kv_storage.rs:50-75): items of sequences that share prefix
+ * blocks are then ordered back to back, so those blocks are read from HBM
+ * about once per XCD instead of once per sharer. Results are the same as
+ * without tables; tables_host NULL is rvkv_decode_plan_update. */
+int rvkv_decode_plan_update_tables(rvkv_decode_plan *plan,
+                                   const uint32_t *ctx_lens_host,
+                                   const uint32_t *tables_host,
+                                   uint32_t max_blocks, uint32_t batch);
 /* Waits for the pool's stream (queued decodes may read the plan), frees. */
 void rvkv_decode_plan_destroy(rvkv_decode_plan *plan);
 /* Device scratch rvkv_paged_decode_planned needs (0 if nothing is split). */

@@ -38,6 +38,7 @@ SIGNATURES = {
     "rvkv_decode_plan_create": (_int, [_P, _P, _u32, _u32, _i32,
                                        ctypes.POINTER(_P)]),
     "rvkv_decode_plan_update": (_int, [_P, _P, _u32]),
+    "rvkv_decode_plan_update_tables": (_int, [_P, _P, _P, _u32, _u32]),
     "rvkv_decode_plan_destroy": (None, [_P]),
     "rvkv_decode_plan_workspace_bytes": (_sz, [_P]),
     "rvkv_decode_plan_items": (_u32, [_P]),

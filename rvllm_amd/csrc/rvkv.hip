@@ -460,10 +460,16 @@ __device__ __forceinline__ float row_group_sum(float x) {
   if constexpr (R >= 4) x += dpp<0x4E>(x);  // quad_perm [2,3,0,1]: lane ^ 2
   if constexpr (R >= 8) x += dpp<0x141>(x);  // row_half_mirror: 8-lane total
   if constexpr (R >= 16) x += dpp<0x140>(x);  // row_mirror: 16-lane total
-  if constexpr (R >= 32)
-    x += __builtin_bit_cast(
-        float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x),
-                                           0x401F));  // lane ^ 16
+  if constexpr (R >= 32) {
+    // lane ^ 16: v_permlane16_swap of x with itself leaves rows (0, 2) of x
+    // in element 0 and rows (1, 3) in element 1 of every lane, in the VALU
+    // (no LDS round trip as for a swizzle).
+    const auto r = __builtin_amdgcn_permlane16_swap(
+        __builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+        false, false);
+    const uint32_t r0 = r[0], r1 = r[1];
+    x = __uint_as_float(r0) + __uint_as_float(r1);
+  }
   return x;
 }
 
@@ -613,7 +619,7 @@ __device__ __forceinline__ void decode_chunk(SoftmaxState<GT, NL> &st,
 // through LDS. A workgroup covering the whole context writes the
 // normalised output; otherwise it writes its partial (m, l, acc) and the
 // reduction kernel merges the partitions.
-template <int HD, int GT, int U, int NL>
+template <int HD, int GT, int U, int NL, bool DB>
 __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
   constexpr int R = HD / (8 * NL);  // lanes per K/V row
   constexpr int RPL = 64 / R;       // rows (tokens) per wave-wide load
@@ -647,7 +653,11 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
   }
   const uint32_t h0 = kvh * a.group + sub * GT;
   const uint32_t ng = min((uint32_t)GT, a.group - sub * GT);
-  const uint32_t *table = a.tables + (size_t)b * a.max_blocks;
+  // Block ids are wave-uniform: read through the constant address space so
+  // they are scalar loads into SGPRs (a plain pointer may be reloaded with
+  // vector loads, since the kernel also stores to global memory).
+  typedef const __attribute__((address_space(4))) uint32_t cu32;
+  cu32 *table = (cu32 *)(uintptr_t)(a.tables + (size_t)b * a.max_blocks);
   const uint32_t first = t0 + (uint32_t)wave * TC;  // this wave's 1st chunk
 
   // The first block ids depend only on the partition: their scalar loads go
@@ -750,22 +760,28 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
     }
 
     const char *zero_v = reinterpret_cast<const char *>(g_zero_rows) + lane_off;
-    for (uint32_t ch = start; ch < t1; ch += stride) {
-      uint4 kr[U][NL], vr[U][NL];
-      uint32_t okmask = 0;
+    // Issues one chunk's K/V loads into (kr, vr) from block ids `cid`;
+    // reports its readable-block mask and whether it is full (no key
+    // masked). A chunk at or past t1 (the double-buffered loop's look-ahead)
+    // loads zero rows instead, which stay in the cache.
+    auto issue = [&](uint4 (&kr)[U][NL], uint4 (&vr)[U][NL],
+                     const uint32_t (&cid)[U], uint32_t ch, uint32_t &okmask,
+                     bool &full) {
+      okmask = 0;
 #pragma unroll
       for (int u = 0; u < U; ++u)
-        okmask |= (uint32_t)(ids[u] < a.num_blocks) << u;
+        okmask |= (uint32_t)(cid[u] < a.num_blocks) << u;
       // The chunk holding this step's appended key takes the masked path,
       // which leaves that key out.
       const bool has_new = newtok >= ch && newtok < ch + TC;
-      const bool full = !has_new && ch >= lo && ch + TC <= t1 &&
-                        okmask == (1u << U) - 1u;
+      full = !has_new && ch >= lo && ch + TC <= t1 &&
+             okmask == (1u << U) - 1u;
+      const bool past = ch >= t1;  // (wave-uniform)
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const uint32_t tb = ch + u * RPL;  // first token of this load
         const bool ok = (okmask >> u) & 1u;
-        const uint64_t uoff = (uint64_t)(ok ? ids[u] : 0u) * blk_bytes +
+        const uint64_t uoff = (uint64_t)(ok ? cid[u] : 0u) * blk_bytes +
                               (uint64_t)(tb & bs_mask) * (HD * 2);
         const char *kp = kbase + uoff + lane_off;
         const char *vp = vbase + uoff + lane_off;
@@ -773,6 +789,7 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
           const uint32_t tok = tb + rg;
           const bool valid = ok && tok >= lo && tok < t1 && tok != newtok;
           vp = valid ? vp : zero_v;
+          kp = past ? zero_v : kp;
         }
 #pragma unroll
         for (int j = 0; j < NL; ++j) {
@@ -780,17 +797,55 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
           vr[u][j] = *reinterpret_cast<const uint4 *>(vp + j * R * 16);
         }
       }
-      // Block ids of this wave's next chunk: scalar loads one chunk ahead.
+    };
+    auto fetch_ids = [&](uint32_t (&cid)[U], uint32_t ch) {
 #pragma unroll
       for (int u = 0; u < U; ++u)
-        ids[u] = table[min((ch + stride + u * RPL) >> a.bs_log2, last_blk)];
-
+        cid[u] = table[min((ch + u * RPL) >> a.bs_log2, last_blk)];
+    };
+    auto consume = [&](uint4 (&kr)[U][NL], uint4 (&vr)[U][NL], uint32_t ch,
+                       uint32_t okmask, bool full) {
       if (full)
         decode_chunk<R, GT, U, NL, false>(st, qh, ql, kr, vr, ch + rg, lo, t1,
                                           okmask, newtok);
       else
         decode_chunk<R, GT, U, NL, true>(st, qh, ql, kr, vr, ch + rg, lo, t1,
                                          okmask, newtok);
+    };
+    if constexpr (DB) {
+      // Two chunks in flight per wave: register sets A and B alternate, so
+      // set B's loads are out while set A is computed and vice versa. Every
+      // load is issued unconditionally (look-ahead past t1 reads zero rows)
+      // so the waits before each compute count only the other set's loads.
+      uint4 kA[U][NL], vA[U][NL], kB[U][NL], vB[U][NL];
+      uint32_t idsB[U], okA, okB;
+      bool fullA, fullB;
+      issue(kA, vA, ids, start, okA, fullA);
+      fetch_ids(idsB, start + stride);
+      fetch_ids(ids, start + 2 * stride);
+      for (uint32_t ch = start;;) {
+        const uint32_t chB = ch + stride;
+        issue(kB, vB, idsB, chB, okB, fullB);
+        fetch_ids(idsB, chB + 2 * stride);
+        consume(kA, vA, ch, okA, fullA);
+        if (chB >= t1) break;
+        const uint32_t chA = chB + stride;
+        issue(kA, vA, ids, chA, okA, fullA);
+        fetch_ids(ids, chA + 2 * stride);
+        consume(kB, vB, chB, okB, fullB);
+        if (chA >= t1) break;
+        ch = chA;
+      }
+    } else {
+      for (uint32_t ch = start; ch < t1; ch += stride) {
+        uint4 kr[U][NL], vr[U][NL];
+        uint32_t okmask;
+        bool full;
+        issue(kr, vr, ids, ch, okmask, full);
+        // Block ids of this wave's next chunk: scalar loads one chunk ahead.
+        fetch_ids(ids, ch + stride);
+        consume(kr, vr, ch, okmask, full);
+      }
     }
 
     if (newtok != 0xFFFFFFFFu && wave == 0) {
@@ -1112,12 +1167,16 @@ uint32_t partition_tokens(const rvkv_pool *p, uint32_t batch, uint32_t n_heads,
 }
 
 // Wavefronts per decode workgroup: four (the waves of a workgroup split its
-// context) unless the grid alone already has >= 2048 workgroups (8 per CU);
-// RVKV_DECODE_WAVES overrides.
-uint32_t decode_waves(uint64_t workgroups) {
+// context) unless the grid alone already has >= 2048 workgroups (8 per CU),
+// and two when workgroups average under 192 context tokens (short items:
+// fewer waves each doing more chunks beat more waves each paying the
+// start-up and merge; measured on the churn workload's final steps, 33.3 ->
+// 27.2 us). RVKV_DECODE_WAVES overrides.
+uint32_t decode_waves(uint64_t workgroups, uint32_t avg_tokens) {
   static const uint32_t forced = env_u32("RVKV_DECODE_WAVES");
   if (forced == 1 || forced == 2 || forced == 4) return forced;
-  return workgroups >= 2048 ? 1 : 4;
+  if (workgroups >= 2048) return 1;
+  return avg_tokens < 192 ? 2 : 4;
 }
 
 struct WsLayout {
@@ -1141,19 +1200,25 @@ WsLayout ws_layout(const rvkv_pool *p, uint32_t batch, uint32_t n_heads,
 template <int HD, int GT>
 void launch_decode(const DecodeArgs &a, dim3 grid, hipStream_t st) {
   static const uint32_t forced_u = env_u32("RVKV_DECODE_UNROLL");
-  const uint32_t W = decode_waves((uint64_t)grid.x * grid.y * grid.z);
+  const uint32_t W =
+      decode_waves((uint64_t)grid.x * grid.y * grid.z, a.avg_tokens);
   // Eight loads per chunk pay off for 512-byte rows and for large groups
   // in single-wave workgroups; otherwise four keep more waves resident.
   const bool u8 = forced_u ? forced_u == 8
                            : ((HD >= 256 && a.avg_tokens >= 512) ||
                               (GT >= 5 && W == 1));
   const size_t lds = (size_t)W * GT * (HD + 2) * sizeof(float);
-  if (u8)
-    hipLaunchKernelGGL((decode_part_kernel<HD, GT, 8, 1>), grid, dim3(64 * W),
-                       lds, st, a);
+  static const uint32_t forced_db = env_u32("RVKV_DECODE_DB");
+  const bool db = forced_db == 1;
+  if (db)
+    hipLaunchKernelGGL((decode_part_kernel<HD, GT, 4, 1, true>), grid,
+                       dim3(64 * W), lds, st, a);
+  else if (u8)
+    hipLaunchKernelGGL((decode_part_kernel<HD, GT, 8, 1, false>), grid,
+                       dim3(64 * W), lds, st, a);
   else
-    hipLaunchKernelGGL((decode_part_kernel<HD, GT, 4, 1>), grid, dim3(64 * W),
-                       lds, st, a);
+    hipLaunchKernelGGL((decode_part_kernel<HD, GT, 4, 1, false>), grid,
+                       dim3(64 * W), lds, st, a);
 }
 
 template <int HD>
@@ -1495,7 +1560,8 @@ int planned_mfma(const char *op, const rvkv_pool *pool,
 // the stream; the pinned staging buffer is reused once the previous upload
 // has completed.
 int plan_build(rvkv_decode_plan *pl, const uint32_t *ctx_lens_host,
-               uint32_t batch) {
+               uint32_t batch, const uint32_t *tables_host = nullptr,
+               uint32_t max_blocks = 0) {
   const char *op = "decode_plan";
   const rvkv_pool *pool = pl->pool;
   uint32_t n_sub, gt;
@@ -1556,11 +1622,54 @@ int plan_build(rvkv_decode_plan *pl, const uint32_t *ctx_lens_host,
     reds.push_back(make_uint4(b, slots, k, 0));
     slots += k;
   }
-  // Longest items first: the short tail fills in behind them.
-  std::stable_sort(items.begin(), items.end(),
-                   [](const uint4 &x, const uint4 &y) {
-                     return (x.z - x.y) > (y.z - y.y);
-                   });
+  // Longest items first: the short tail fills in behind them. With the
+  // block tables, items of one length are further ordered by the first
+  // block they read, so the items of sequences that share prefix blocks
+  // run back to back: consecutive workgroups go round-robin over the XCDs,
+  // and each XCD's sharers then find those blocks in its L2 instead of
+  // reading them from HBM once per sharer.
+  if (tables_host) {
+    // Items whose first block also starts another item form a group, placed
+    // by its longest member; inside a group, longest first.
+    const uint32_t lg = ilog2(pool->block_size);
+    std::vector<uint32_t> fb(items.size());
+    std::vector<std::pair<uint32_t, uint32_t>> by_block(items.size());
+    for (size_t i = 0; i < items.size(); ++i) {
+      const uint32_t bi = items[i].y >> lg;
+      fb[i] = bi < max_blocks ? tables_host[(size_t)items[i].x * max_blocks + bi]
+                              : 0xFFFFFFFFu;
+      by_block[i] = {fb[i], items[i].z - items[i].y};
+    }
+    std::sort(by_block.begin(), by_block.end());
+    std::vector<uint32_t> key(items.size());  // the group's longest item
+    std::vector<uint32_t> grouped(items.size());
+    for (size_t i = 0; i < items.size(); ++i) {
+      const auto lo_it = std::lower_bound(
+          by_block.begin(), by_block.end(), std::make_pair(fb[i], 0u));
+      const auto hi_it = std::upper_bound(
+          by_block.begin(), by_block.end(),
+          std::make_pair(fb[i], 0xFFFFFFFFu));
+      grouped[i] = (hi_it - lo_it) > 1;
+      key[i] = (hi_it - 1)->second;
+    }
+    std::vector<uint32_t> order(items.size());
+    for (size_t i = 0; i < order.size(); ++i) order[i] = (uint32_t)i;
+    std::stable_sort(order.begin(), order.end(), [&](uint32_t x, uint32_t y) {
+      const uint32_t lx = grouped[x] ? key[x] : items[x].z - items[x].y;
+      const uint32_t ly = grouped[y] ? key[y] : items[y].z - items[y].y;
+      if (lx != ly) return lx > ly;
+      if (fb[x] != fb[y]) return fb[x] < fb[y];
+      return (items[x].z - items[x].y) > (items[y].z - items[y].y);
+    });
+    std::vector<uint4> sorted(items.size());
+    for (size_t i = 0; i < order.size(); ++i) sorted[i] = items[order[i]];
+    items.swap(sorted);
+  } else {
+    std::stable_sort(items.begin(), items.end(),
+                     [](const uint4 &x, const uint4 &y) {
+                       return (x.z - x.y) > (y.z - y.y);
+                     });
+  }
   const size_t need = items.size() + reds.size();
   hipError_t e = hipSuccess;
   if (pl->uploaded) e = hipEventSynchronize(pl->uploaded);
@@ -1756,12 +1865,22 @@ int rvkv_decode_plan_create(const rvkv_pool *pool,
 
 int rvkv_decode_plan_update(rvkv_decode_plan *plan,
                             const uint32_t *ctx_lens_host, uint32_t batch) {
+  return rvkv_decode_plan_update_tables(plan, ctx_lens_host, nullptr, 0,
+                                        batch);
+}
+
+int rvkv_decode_plan_update_tables(rvkv_decode_plan *plan,
+                                   const uint32_t *ctx_lens_host,
+                                   const uint32_t *tables_host,
+                                   uint32_t max_blocks, uint32_t batch) {
   const char *op = "decode_plan";
   if (!plan) return fail(RVKV_EINVAL, op, "plan is NULL");
   int rc = plan_check_args(op, plan->pool, ctx_lens_host, batch,
                            plan->n_heads);
   if (rc) return rc;
-  return plan_build(plan, ctx_lens_host, batch);
+  if (tables_host && max_blocks == 0)
+    return fail(RVKV_EINVAL, op, "max_blocks must be positive with tables");
+  return plan_build(plan, ctx_lens_host, batch, tables_host, max_blocks);
 }
 
 void rvkv_decode_plan_destroy(rvkv_decode_plan *plan) {

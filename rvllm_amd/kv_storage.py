@@ -99,12 +99,24 @@ class HipDecodePlan:
             self.ws = torch.empty(self.workspace_bytes + (1 << 20),
                                   dtype=torch.uint8, device=self._device)
 
-    def update(self, ctx_lens) -> None:
-        """rvkv_decode_plan_update: this step's context lengths."""
+    def update(self, ctx_lens, tables=None) -> None:
+        """rvkv_decode_plan_update: this step's context lengths; with the
+        host copy of the padded block tables ([batch, max_blocks]), items
+        of sequences sharing prefix blocks are ordered back to back
+        (rvkv_decode_plan_update_tables)."""
         import numpy as np
         lens = np.ascontiguousarray(np.asarray(ctx_lens, dtype=np.uint32))
-        check(self._L.rvkv_decode_plan_update(
-            self._plan, lens.ctypes.data_as(ctypes.c_void_p), lens.size))
+        if tables is None:
+            check(self._L.rvkv_decode_plan_update(
+                self._plan, lens.ctypes.data_as(ctypes.c_void_p), lens.size))
+        else:
+            tab = np.ascontiguousarray(np.asarray(tables, dtype=np.uint32))
+            _need(tab.ndim == 2 and tab.shape[0] == lens.size,
+                  "decode_plan: tables must be [batch, max_blocks]")
+            check(self._L.rvkv_decode_plan_update_tables(
+                self._plan, lens.ctypes.data_as(ctypes.c_void_p),
+                tab.ctypes.data_as(ctypes.c_void_p), tab.shape[1],
+                lens.size))
         self.batch = int(lens.size)
         self.ctx_lens_host = lens
         self._sync()

@@ -618,6 +618,49 @@ def test_decode_masked_slots_hold_inf(G, hd):
         put_inf(last_b[keep], last_o[keep])
 
 
+@pytest.mark.parametrize("G", [2, 7])
+def test_planned_decode_shared_prefix_order(G):
+    """A plan updated with the host block tables orders the items of
+    prefix sharers back to back; the outputs are bitwise those of the plan
+    built from the lengths alone, and match the oracle. G 7: matrix-core
+    decode."""
+    from rvllm_amd.kv_storage import HipDecodePlan
+    bs, nkv, hd = 32, 2, 64
+    rng = np.random.default_rng(G)
+    n, n_pref = 40, 12
+    lens = rng.integers(40, 3000, n).astype(np.uint32)
+    prefix = rng.permutation(200)[:32].astype(np.uint32)  # 1024 tokens
+    free = list(range(200, 200 + 4000))
+    tables = []
+    for b in range(n):
+        nb = -(-int(lens[b]) // bs)
+        t = []
+        for i in range(nb):
+            if b < n_pref and i < len(prefix) and (i + 1) * bs <= lens[b]:
+                t.append(int(prefix[i]))
+            else:
+                t.append(free.pop(rng.integers(len(free))))
+        tables.append(np.array(t, np.uint32))
+    num_blocks = 200 + 4000
+    cfg = W.Config("pfx", 9, 1, G * nkv, nkv, hd, bs, n)
+    db = W.DecodeBatch(cfg, num_blocks, lens, tables,
+                       np.zeros(n, np.uint32), np.zeros(n, np.uint32))
+    st = HipKvStorage(1, num_blocks, bs, nkv, hd)
+    fill_layer(st, 0, seed=G)
+    q = torch.randn(n, G * nkv, hd, device="cuda")
+    tab = dev_u32(db.padded_tables())
+    ctx = dev_u32(lens)
+    plan = HipDecodePlan(st, lens, G * nkv)
+    a = st.paged_decode_planned(0, plan, q, tab, ctx).clone()
+    plan.update(lens, db.padded_tables())
+    b = st.paged_decode_planned(0, plan, q, tab, ctx)
+    assert torch.equal(a, b)
+    cache, padded, mb = oracle_subset(st, 0, tables, lens)
+    want = orc.paged_decode_f64(cache, q.cpu().numpy(), padded.reshape(-1),
+                                mb, lens)
+    assert np.abs(b.cpu().numpy() - want).max() < ATOL
+
+
 def test_planned_decode_update_reuses_plan():
     """update() with new lengths (a decode step later, batch change) gives
     the same results as a freshly built plan."""
