@@ -123,8 +123,10 @@ int rvkv_gather(const rvkv_pool *pool, uint32_t layer,
  * ws: device scratch of at least rvkv_decode_workspace_bytes(...) bytes,
  * 256-byte aligned; contents need no initialisation.
  * A sequence with ctx_len 0 gets an all-zero output row.
- * Supported: head_dim in {32, 64, 128, 256}, block_size a power of two
- * >= 512/head_dim, n_heads a multiple of n_kv_heads. */
+ * Supported: head_dim <= 256 (32, 64, 128 and 256 on the full-speed path;
+ * any other value reads rows element by element), block_size a power of
+ * two >= 512/HD where HD is head_dim rounded up to 32, 64, 128 or 256,
+ * n_heads a multiple of n_kv_heads. */
 int rvkv_paged_decode(const rvkv_pool *pool, uint32_t layer, const float *q,
                       const uint32_t *block_tables, const uint32_t *ctx_lens,
                       uint32_t batch, uint32_t max_blocks, uint32_t n_heads,

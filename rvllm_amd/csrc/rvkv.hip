@@ -436,6 +436,7 @@ struct DecodeArgs {
   uint32_t head_stride;   // elements per (block, head) tile
   uint32_t max_blocks, num_blocks, n_kv, n_heads, group, n_sub;
   uint32_t bs_log2, part_tokens, n_parts, ctx_cap;
+  uint32_t hd;  // the cache's head_dim (the kernels' HD is it rounded up)
   float qscale;
   int32_t window;
   // Host-side launch hint (not read by the kernels): average context
@@ -478,6 +479,54 @@ constexpr float kNegBig = -1.0e30f;  // finite "minus infinity" for m
 // Zero bytes covering one wave-wide load (64 lanes x 16 B, two loads per
 // row at most): the V source of masked keys.
 __device__ __align__(16) uint4 g_zero_rows[128];
+
+// Eight f16 of a row at byte address p whose first element is e0 of a
+// row of hd elements (RAGGED rows: any head_dim, 2-byte aligned): elements
+// at or past hd read as zero.
+__device__ __forceinline__ uint4 load_row8(const char *p, uint32_t e0,
+                                           uint32_t hd) {
+  const uint16_t *q = reinterpret_cast<const uint16_t *>(p);
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t lo = e0 + 2 * i < hd ? q[2 * i] : 0u;
+    const uint32_t hi = e0 + 2 * i + 1 < hd ? q[2 * i + 1] : 0u;
+    w[i] = lo | (hi << 16);
+  }
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+// The appended row's elements e0..e0+7 (f32 source rounded to f16
+// nearest-even, or f16 bits), zero past hd.
+__device__ __forceinline__ uint4 new_row8(const void *src, bool f32,
+                                          size_t row, uint32_t e0,
+                                          uint32_t hd) {
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint16_t v[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const uint32_t e = e0 + 2 * i + k;
+      if (e >= hd) {
+        v[k] = 0;
+      } else if (f32) {
+        v[k] = __builtin_bit_cast(
+            uint16_t, (_Float16) static_cast<const float *>(src)[row + e]);
+      } else {
+        v[k] = static_cast<const uint16_t *>(src)[row + e];
+      }
+    }
+    w[i] = (uint32_t)v[0] | ((uint32_t)v[1] << 16);
+  }
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+__device__ __forceinline__ void store_row8(uint16_t *p, uint4 x, uint32_t e0,
+                                           uint32_t hd) {
+  const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    if (e0 + i < hd) p[i] = (uint16_t)(w[i / 2] >> (16 * (i & 1)));
+}
 
 // q.k over the lane's NL*8 elements. q is carried as an f16 pair (hi, lo)
 // with hi + lo = q to ~2^-22 relative, so the score keeps q's f32 precision
@@ -619,7 +668,7 @@ __device__ __forceinline__ void decode_chunk(SoftmaxState<GT, NL> &st,
 // through LDS. A workgroup covering the whole context writes the
 // normalised output; otherwise it writes its partial (m, l, acc) and the
 // reduction kernel merges the partitions.
-template <int HD, int GT, int U, int NL, bool DB>
+template <int HD, int GT, int U, int NL, bool RAGGED>
 __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
   constexpr int R = HD / (8 * NL);  // lanes per K/V row
   constexpr int RPL = 64 / R;       // rows (tokens) per wave-wide load
@@ -668,6 +717,9 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
   for (int u = 0; u < U; ++u)
     ids[u] = table[min((first + u * RPL) >> a.bs_log2, mb1)];
 
+  // Row length in elements: HD, or (RAGGED) the cache's head_dim, whose
+  // lanes past its end hold zeros.
+  const uint32_t hdr = RAGGED ? a.hd : HD;
   // q rows of the GT heads (this lane's elements) are loaded up front too.
   float4 qraw[GT][NL][2];
 #pragma unroll
@@ -675,10 +727,19 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
     const uint32_t hg = h0 + ((uint32_t)g < ng ? g : 0);
 #pragma unroll
     for (int j = 0; j < NL; ++j) {
-      const float4 *qp = reinterpret_cast<const float4 *>(
-          a.q + ((size_t)b * a.n_heads + hg) * HD + (j * R + c) * 8);
-      qraw[g][j][0] = qp[0];
-      qraw[g][j][1] = qp[1];
+      const uint32_t e0 = (j * R + c) * 8;
+      const float *qe = a.q + ((size_t)b * a.n_heads + hg) * hdr + e0;
+      if constexpr (RAGGED) {
+        float x[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[i] = e0 + i < hdr ? qe[i] : 0.f;
+        qraw[g][j][0] = make_float4(x[0], x[1], x[2], x[3]);
+        qraw[g][j][1] = make_float4(x[4], x[5], x[6], x[7]);
+      } else {
+        const float4 *qp = reinterpret_cast<const float4 *>(qe);
+        qraw[g][j][0] = qp[0];
+        qraw[g][j][1] = qp[1];
+      }
     }
   }
 
@@ -697,10 +758,17 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
       for (uint32_t g = 0; g < ng; ++g)
 #pragma unroll
         for (int j = 0; j < NL; ++j) {
-          float4 *o = reinterpret_cast<float4 *>(
-              a.out + ((size_t)b * a.n_heads + h0 + g) * HD + (j * R + c) * 8);
-          o[0] = make_float4(0.f, 0.f, 0.f, 0.f);
-          o[1] = make_float4(0.f, 0.f, 0.f, 0.f);
+          const uint32_t e0 = (j * R + c) * 8;
+          float *oe = a.out + ((size_t)b * a.n_heads + h0 + g) * hdr + e0;
+          if constexpr (RAGGED) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+              if (e0 + i < hdr) oe[i] = 0.f;
+          } else {
+            float4 *o = reinterpret_cast<float4 *>(oe);
+            o[0] = make_float4(0.f, 0.f, 0.f, 0.f);
+            o[1] = make_float4(0.f, 0.f, 0.f, 0.f);
+          }
         }
     return;
   }
@@ -750,7 +818,7 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
                         (size_t)kvh * a.head_stride * 2;
     const char *vbase = reinterpret_cast<const char *>(a.vc) +
                         (size_t)kvh * a.head_stride * 2;
-    const uint32_t lane_off = (uint32_t)(rg * HD * 2 + c * 16);
+    const uint32_t lane_off = (uint32_t)(rg * hdr * 2 + c * 16);
     const uint64_t blk_bytes = a.block_stride * 2;
     const uint32_t stride = (uint32_t)W * TC;
     if (skip != 0 || last_blk < ((first + TC - 1) >> a.bs_log2)) {
@@ -782,7 +850,7 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
         const uint32_t tb = ch + u * RPL;  // first token of this load
         const bool ok = (okmask >> u) & 1u;
         const uint64_t uoff = (uint64_t)(ok ? cid[u] : 0u) * blk_bytes +
-                              (uint64_t)(tb & bs_mask) * (HD * 2);
+                              (uint64_t)(tb & bs_mask) * (hdr * 2);
         const char *kp = kbase + uoff + lane_off;
         const char *vp = vbase + uoff + lane_off;
         if (!full) {  // (wave-uniform)
@@ -793,8 +861,13 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
         }
 #pragma unroll
         for (int j = 0; j < NL; ++j) {
-          kr[u][j] = *reinterpret_cast<const uint4 *>(kp + j * R * 16);
-          vr[u][j] = *reinterpret_cast<const uint4 *>(vp + j * R * 16);
+          if constexpr (RAGGED) {
+            kr[u][j] = load_row8(kp + j * R * 16, (j * R + c) * 8, hdr);
+            vr[u][j] = load_row8(vp + j * R * 16, (j * R + c) * 8, hdr);
+          } else {
+            kr[u][j] = *reinterpret_cast<const uint4 *>(kp + j * R * 16);
+            vr[u][j] = *reinterpret_cast<const uint4 *>(vp + j * R * 16);
+          }
         }
       }
     };
@@ -812,31 +885,7 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
         decode_chunk<R, GT, U, NL, true>(st, qh, ql, kr, vr, ch + rg, lo, t1,
                                          okmask, newtok);
     };
-    if constexpr (DB) {
-      // Two chunks in flight per wave: register sets A and B alternate, so
-      // set B's loads are out while set A is computed and vice versa. Every
-      // load is issued unconditionally (look-ahead past t1 reads zero rows)
-      // so the waits before each compute count only the other set's loads.
-      uint4 kA[U][NL], vA[U][NL], kB[U][NL], vB[U][NL];
-      uint32_t idsB[U], okA, okB;
-      bool fullA, fullB;
-      issue(kA, vA, ids, start, okA, fullA);
-      fetch_ids(idsB, start + stride);
-      fetch_ids(ids, start + 2 * stride);
-      for (uint32_t ch = start;;) {
-        const uint32_t chB = ch + stride;
-        issue(kB, vB, idsB, chB, okB, fullB);
-        fetch_ids(idsB, chB + 2 * stride);
-        consume(kA, vA, ch, okA, fullA);
-        if (chB >= t1) break;
-        const uint32_t chA = chB + stride;
-        issue(kA, vA, ids, chA, okA, fullA);
-        fetch_ids(ids, chA + 2 * stride);
-        consume(kB, vB, chB, okB, fullB);
-        if (chA >= t1) break;
-        ch = chA;
-      }
-    } else {
+    {
       for (uint32_t ch = start; ch < t1; ch += stride) {
         uint4 kr[U][NL], vr[U][NL];
         uint32_t okmask;
@@ -853,11 +902,14 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
       // (sub-group 0, row group 0), and add it to row group 0's softmax
       // state as one more key.
       uint4 nk[NL], nv[NL];
-      const size_t src = ((size_t)b * a.n_kv + kvh) * HD;
+      const size_t src = ((size_t)b * a.n_kv + kvh) * hdr;
 #pragma unroll
       for (int j = 0; j < NL; ++j) {
         const uint32_t e0 = (j * R + c) * 8;
-        if (a.new_f32) {
+        if (RAGGED) {
+          nk[j] = new_row8(a.new_k, a.new_f32, src, e0, hdr);
+          nv[j] = new_row8(a.new_v, a.new_f32, src, e0, hdr);
+        } else if (a.new_f32) {
           const float4 *kp = reinterpret_cast<const float4 *>(
               static_cast<const float *>(a.new_k) + src + e0);
           const float4 *vp = reinterpret_cast<const float4 *>(
@@ -882,13 +934,19 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
         const uint32_t blk = a.new_blk[b], off = a.new_off[b];
         if (blk < a.num_blocks && off < a.block_size) {
           const size_t dst =
-              ((size_t)blk * a.n_kv + kvh) * a.head_stride + (size_t)off * HD;
+              ((size_t)blk * a.n_kv + kvh) * a.head_stride + (size_t)off * hdr;
           uint16_t *kc = const_cast<uint16_t *>(a.kc);
           uint16_t *vc = const_cast<uint16_t *>(a.vc);
 #pragma unroll
           for (int j = 0; j < NL; ++j) {
-            *reinterpret_cast<uint4 *>(kc + dst + (j * R + c) * 8) = nk[j];
-            *reinterpret_cast<uint4 *>(vc + dst + (j * R + c) * 8) = nv[j];
+            const uint32_t e0 = (j * R + c) * 8;
+            if constexpr (RAGGED) {
+              store_row8(kc + dst + e0, nk[j], e0, hdr);
+              store_row8(vc + dst + e0, nv[j], e0, hdr);
+            } else {
+              *reinterpret_cast<uint4 *>(kc + dst + e0) = nk[j];
+              *reinterpret_cast<uint4 *>(vc + dst + e0) = nv[j];
+            }
           }
         }
       }
@@ -970,7 +1028,8 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
       x += r[2 + d] * wt;
     }
     if (slot == kNoSlot) {
-      a.out[((size_t)b * a.n_heads + h0 + g) * HD + d] = x / L;
+      if (!RAGGED || (uint32_t)d < hdr)
+        a.out[((size_t)b * a.n_heads + h0 + g) * hdr + d] = x / L;
     } else {
       const size_t idx = (size_t)slot * a.n_heads + h0 + g;
       a.ws_acc[idx * HD + d] = x;
@@ -1043,7 +1102,7 @@ __global__ void __launch_bounds__(64) decode_reduce_kernel(DecodeArgs a) {
 #pragma unroll
     for (int e = 0; e < EPL; ++e) {
       const int d = lane * EPL + e;
-      if (d < HD) a.out[hrow * HD + d] = acc[e] * inv;
+      if ((uint32_t)d < a.hd) a.out[hrow * a.hd + d] = acc[e] * inv;
     }
     return;
   }
@@ -1108,7 +1167,7 @@ __global__ void __launch_bounds__(64) decode_reduce_kernel(DecodeArgs a) {
 #pragma unroll
   for (int e = 0; e < EPL; ++e) {
     const int d = lane * EPL + e;
-    if (d < HD) a.out[hrow * HD + d] = acc[e] * inv;
+    if ((uint32_t)d < a.hd) a.out[hrow * a.hd + d] = acc[e] * inv;
   }
 }
 
@@ -1123,6 +1182,15 @@ bool hd_supported(uint32_t hd) {
   for (int x : kSupportedHd)
     if ((uint32_t)x == hd) return true;
   return false;
+}
+
+// The decode kernels' HD for a cache head_dim: the smallest of 32, 64, 128,
+// 256 that holds it (0 past 256). Rows shorter than HD read element by
+// element, their missing lanes as zeros.
+uint32_t decode_hd(uint32_t hd) {
+  for (int x : kSupportedHd)
+    if (hd <= (uint32_t)x) return (uint32_t)x;
+  return 0;
 }
 
 uint32_t ilog2(uint32_t x) {
@@ -1192,7 +1260,7 @@ WsLayout ws_layout(const rvkv_pool *p, uint32_t batch, uint32_t n_heads,
   if (w.n_parts <= 1) return w;  // direct write, no workspace
   const size_t slots = (size_t)batch * n_heads * w.n_parts;
   w.acc_off = 0;
-  w.ml_off = (slots * p->head_dim * 4 + 255) & ~(size_t)255;
+  w.ml_off = (slots * decode_hd(p->head_dim) * 4 + 255) & ~(size_t)255;
   w.bytes = w.ml_off + ((slots * 2 * 4 + 255) & ~(size_t)255);
   return w;
 }
@@ -1208,9 +1276,7 @@ void launch_decode(const DecodeArgs &a, dim3 grid, hipStream_t st) {
                            : ((HD >= 256 && a.avg_tokens >= 512) ||
                               (GT >= 5 && W == 1));
   const size_t lds = (size_t)W * GT * (HD + 2) * sizeof(float);
-  static const uint32_t forced_db = env_u32("RVKV_DECODE_DB");
-  const bool db = forced_db == 1;
-  if (db)
+  if (a.hd != HD)  // a head_dim below HD: rows read element by element
     hipLaunchKernelGGL((decode_part_kernel<HD, GT, 4, 1, true>), grid,
                        dim3(64 * W), lds, st, a);
   else if (u8)
@@ -1428,14 +1494,14 @@ int prepare_decode(const char *op, const rvkv_pool *pool, uint32_t layer,
   if (n_heads == 0 || n_heads % pool->n_kv != 0)
     return fail(RVKV_EINVAL, op,
                 "n_heads must be a positive multiple of n_kv_heads");
-  const uint32_t hd = pool->head_dim;
-  if (!hd_supported(hd))
-    return fail(RVKV_EUNSUPPORTED, op,
-                "head_dim must be one of 32, 64, 128, 256");
+  const uint32_t hdp = decode_hd(pool->head_dim);
+  if (hdp == 0)
+    return fail(RVKV_EUNSUPPORTED, op, "head_dim must be at most 256");
   const uint32_t bs = pool->block_size;
-  if ((bs & (bs - 1)) != 0 || bs < 512 / hd)
+  if ((bs & (bs - 1)) != 0 || bs < 512 / hdp)
     return fail(RVKV_EUNSUPPORTED, op,
-                "block_size must be a power of two >= 512 / head_dim");
+                "block_size must be a power of two >= 512 / head_dim "
+                "(head_dim rounded up to 32, 64, 128 or 256)");
   if (!q || !block_tables || !ctx_lens || !out)
     return fail(RVKV_EINVAL, op, "NULL q/block_tables/ctx_lens/out");
   if ((uintptr_t)q % 16 || (uintptr_t)out % 16)
@@ -1455,7 +1521,8 @@ int prepare_decode(const char *op, const rvkv_pool *pool, uint32_t layer,
   a->tables = block_tables;
   a->ctx_lens = ctx_lens;
   a->block_stride = pool->block_elems;
-  a->head_stride = bs * hd;
+  a->head_stride = bs * pool->head_dim;
+  a->hd = pool->head_dim;
   a->block_size = bs;
   a->max_blocks = max_blocks;
   a->num_blocks = pool->num_blocks;
@@ -1551,7 +1618,8 @@ int planned_mfma(const char *op, const rvkv_pool *pool,
       scale, plan->window, a.items, plan->n_items, a.ws_acc, a.ws_ml, a.out,
       a.new_k, a.new_v, a.new_blk, a.new_off, a.new_f32);
   if (rc || plan->n_reds == 0) return rc;
-  return launch_reduce(op, a, pool->head_dim, dim3(plan->n_heads, plan->n_reds),
+  return launch_reduce(op, a, decode_hd(pool->head_dim),
+                       dim3(plan->n_heads, plan->n_reds),
                        pool->stream);
 }
 
@@ -1704,7 +1772,7 @@ int plan_build(rvkv_decode_plan *pl, const uint32_t *ctx_lens_host,
   pl->n_slots = slots;
   const size_t ent = (size_t)slots * pl->n_heads;
   pl->acc_off = 0;
-  pl->ml_off = (ent * pool->head_dim * 4 + 255) & ~(size_t)255;
+  pl->ml_off = (ent * decode_hd(pool->head_dim) * 4 + 255) & ~(size_t)255;
   pl->ws_bytes = slots ? pl->ml_off + ((ent * 2 * 4 + 255) & ~(size_t)255) : 0;
   return RVKV_OK;
 }
@@ -1832,7 +1900,7 @@ int paged_decode_ws(const char *op, const rvkv_pool *pool, uint32_t layer,
   a.n_parts = w.n_parts;
   a.avg_tokens = a.part_tokens < max_ctx_len ? a.part_tokens : max_ctx_len;
   const dim3 grid(w.n_parts, pool->n_kv * a.n_sub, batch);
-  return launch_decode_pair(op, a, pool->head_dim, gt, grid,
+  return launch_decode_pair(op, a, decode_hd(pool->head_dim), gt, grid,
                             dim3(n_heads, batch), w.n_parts > 1, pool->stream);
 }
 
@@ -1928,7 +1996,7 @@ int rvkv_paged_decode_planned(const rvkv_pool *pool,
   if (rvkv_detail::mfma_decode_wanted(pool, plan->n_heads))
     return planned_mfma(op, pool, plan, layer, a, max_blocks, scale);
   const dim3 grid(plan->n_items, pool->n_kv * a.n_sub, 1);
-  return launch_decode_pair(op, a, pool->head_dim, gt, grid,
+  return launch_decode_pair(op, a, decode_hd(pool->head_dim), gt, grid,
                             dim3(plan->n_heads, plan->n_reds ? plan->n_reds : 1),
                             plan->n_reds > 0, pool->stream);
 }
@@ -1982,7 +2050,7 @@ int rvkv_decode_step(rvkv_pool *pool, const rvkv_decode_plan *plan,
       return planned_mfma(op, pool, plan, layer, a, max_blocks, scale);
     const dim3 grid(plan->n_items, pool->n_kv * a.n_sub, 1);
     return launch_decode_pair(
-        op, a, pool->head_dim, gt, grid,
+        op, a, decode_hd(pool->head_dim), gt, grid,
         dim3(plan->n_heads, plan->n_reds ? plan->n_reds : 1),
         plan->n_reds > 0, pool->stream);
   }
@@ -1996,7 +2064,7 @@ int rvkv_decode_step(rvkv_pool *pool, const rvkv_decode_plan *plan,
   a.n_parts = w.n_parts;
   a.avg_tokens = a.part_tokens < max_ctx_len ? a.part_tokens : max_ctx_len;
   const dim3 grid(w.n_parts, pool->n_kv * a.n_sub, batch);
-  return launch_decode_pair(op, a, pool->head_dim, gt, grid,
+  return launch_decode_pair(op, a, decode_hd(pool->head_dim), gt, grid,
                             dim3(n_heads, batch), w.n_parts > 1, pool->stream);
 }
 

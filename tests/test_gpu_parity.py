@@ -276,7 +276,7 @@ def _decode_vs_oracle(st, layer, db, q, window=0, sample=None):
     return err
 
 
-@pytest.mark.parametrize("case", [0, 1, 2, 4])
+@pytest.mark.parametrize("case", [0, 1, 2, 3, 4, 5])
 def test_decode_metal_cases(golden, case):
     """attn_decode cases of src/metal/ops.rs:684-691 at q_len 1 (the decode
     kernel), xorshift data stored as f16, ragged ctx - 2b, reversed block
@@ -302,7 +302,7 @@ def test_decode_metal_cases(golden, case):
     want = orc.paged_decode_f64(ref, q.cpu().numpy(), c["block_idx"],
                                 c["max_blocks"], ctx)
     assert np.abs(out - want).max() < ATOL
-    if case in (0, 1):  # q_len 1 in the reference too: the golden applies
+    if case in (0, 1, 5):  # q_len 1 in the reference too: the golden applies
         exp = np.array(golden["metal_attn_decode"][case]["expected"],
                        np.float32).reshape(B, H, D)
         # golden is over the f32 cache; f16 storage adds <= ~1e-3
@@ -310,11 +310,47 @@ def test_decode_metal_cases(golden, case):
 
 
 def test_decode_unsupported_head_dims_raise():
-    for hd in (6, 200):
+    for hd in (264, 512):
         st = HipKvStorage(1, 4, 16, 1, hd)
         q = torch.zeros(1, 2, hd, device="cuda")
         with pytest.raises(RvkvError, match="paged_decode: head_dim"):
             st.paged_decode(0, q, dev_u32([[0]]), dev_u32([4]), 4)
+
+
+@pytest.mark.parametrize("hd,G", [(6, 2), (40, 3), (80, 4), (96, 1),
+                                  (200, 2), (136, 8)])
+def test_decode_any_head_dim(hd, G):
+    """head_dim that is not 32/64/128/256 (rows read element by element,
+    the missing lanes as zeros): uniform, planned (split sequences) and the
+    fused step against the oracle, the fused step's cache bits equal to
+    rvkv_append's."""
+    from rvllm_amd.kv_storage import HipDecodePlan
+    bs, nkv = 16, 2
+    lens = np.array([1, 37, 700, 3000, 16], np.uint32)
+    cfg = W.Config("anyhd", 9, 1, G * nkv, nkv, hd, bs, len(lens))
+    db = W.ragged_batch(cfg, lens, seed=hd, extra_blocks=3)
+    st = HipKvStorage(1, db.num_blocks, bs, nkv, hd)
+    fill_layer(st, 0, seed=hd)
+    q = torch.randn(len(lens), G * nkv, hd, device="cuda")
+    assert _decode_vs_oracle(st, 0, db, q) < ATOL
+    assert _decode_vs_oracle(st, 0, db, q, window=100) < ATOL
+    err, plan, _ = _planned_vs_oracle(st, 0, db, q)
+    assert err < ATOL
+    # fused step == append + decode
+    nk = torch.randn(len(lens), nkv, hd, device="cuda")
+    nv = torch.randn(len(lens), nkv, hd, device="cuda")
+    sb, so = dev_u32(db.slot_block), dev_u32(db.slot_off)
+    tab, ctx = dev_u32(db.padded_tables()), dev_u32(lens)
+    st2 = HipKvStorage(1, db.num_blocks, bs, nkv, hd)
+    fill_layer(st2, 0, seed=hd)
+    got = st.decode_step(0, nk, nv, sb, so, q, tab, ctx, int(lens.max()),
+                         plan=plan)
+    st2.write_tokens(0, sb, so, nk, nv)
+    want = st2.paged_decode(0, q, tab, ctx, int(lens.max()))
+    ids = dev_u32(np.arange(db.num_blocks))
+    for w in (0, 1):
+        assert torch.equal(st.read_blocks(0, w, ids), st2.read_blocks(0, w, ids))
+    assert (got - want).abs().max().item() < 5e-4
 
 
 def test_decode_edge_cases():
