@@ -1065,7 +1065,9 @@ def main():
         "data": "synthetic: K/V ~ N(0,1)*scale f16, q ~ N(0,1) f32, seeded "
                 "random-permutation block tables",
         "config": {
-            "workload": f"{c.name}: {c.description}; {L} layers, "
+            "workload": f"{c.name}: {c.description.split(',')[0]}"
+                        f"{'' if not (args.batch or args.ctx) else ' (resized)'}; "
+                        f"{L} layers, "
                         f"{c.n_heads} q / {c.n_kv_heads} kv heads, head_dim "
                         f"{c.head_dim}, block_size {c.block_size}, "
                         f"{B} seqs, max ctx {max_ctx}",
