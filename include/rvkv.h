@@ -65,8 +65,13 @@ const char *rvkv_last_error(void);
  * Replaces CudaKvStorage::new (src/cuda/kv_storage.rs:77-100) /
  * KvStorage::new (src/kv_storage.rs:84-104): zeroed K and V storage for
  * n_layers attention layers. One device allocation for all layers; 64-bit
- * offsets throughout. cache_dtype must be RVKV_F16. The pool binds to the
- * current HIP device and to `stream`. */
+ * offsets throughout. cache_dtype RVKV_F16 (the fast path) or RVKV_F32
+ * (the reference's own cell type): an f32 pool supports append (f32 rows
+ * copied, f16 rows widened exactly), gather into F32 only, copy_blocks,
+ * read_blocks, block_checksums, paged decode (uniform, planned, decode_step,
+ * no-alloc) at head_dim 32/64/128/256; paged_prefill and attn_prep return
+ * RVKV_EUNSUPPORTED on it. The pool binds to the current HIP device and to
+ * `stream`. */
 int rvkv_pool_create(uint32_t n_layers, uint32_t num_blocks,
                      uint32_t block_size, uint32_t n_kv_heads,
                      uint32_t head_dim, rvkv_dtype cache_dtype,
@@ -98,7 +103,8 @@ int rvkv_append(rvkv_pool *pool, uint32_t layer, const void *k, const void *v,
  * block_idx: device u32[batch*max_blocks], each sequence's block table padded
  * to max_blocks (rvllm's GatherPlan convention, src/kv_storage.rs:59-67).
  * out_k, out_v: device [batch, n_kv_heads, ctx_len, head_dim] of out_dtype
- * (F32 = the reference's output type; F16 = raw cache bits).
+ * (F32 = the reference's output type; F16 = raw cache bits, f16 pools
+ * only: an f32 pool gathers into F32, bit for bit).
  * ctx_len must not exceed max_blocks*block_size. */
 int rvkv_gather(const rvkv_pool *pool, uint32_t layer,
                 const uint32_t *block_idx, uint32_t batch, uint32_t max_blocks,

@@ -81,8 +81,9 @@ def lib() -> ctypes.CDLL:
                                       u32]
         L.orc_block_checksums.argtypes = [P, u32, u32, u32, P, u32, P]
         L.orc_decode_step.restype = ctypes.c_int
-        L.orc_decode_step.argtypes = [P, P, u32, u32, u32, u32, P, P, P, P, P,
-                                      u32, P, u32, u32, P, P, u32]
+        L.orc_decode_step.argtypes = [P, P, ctypes.c_int, u32, u32, u32, u32,
+                                      P, P, P, P, P, u32, P, u32, u32, P, P,
+                                      u32]
         L.orc_rope_cos_sin.argtypes = [f32, P, u32, P, u32, P, P]
         L.orc_rms_norm.argtypes = [P, P, u32, u32, f32, P]
         L.orc_rope_apply.argtypes = [P, P, P, u32, u32, P]
@@ -185,11 +186,13 @@ class KvCache:
                                   self.hd, _p(src), _p(dst), src.size)
 
     def checksums(self, which: int, blocks) -> np.ndarray:
-        assert self.dtype == F16
+        """FNV-1a 64 of each block's logical little-endian bytes (an f32
+        cell hashes as its two 16-bit halves, low first)."""
         blocks = _u32(blocks)
         out = np.empty(blocks.size, np.uint64)
-        cache = self.k if which == 0 else self.v
-        lib().orc_block_checksums(_p(cache), self.bs, self.n_kv, self.hd,
+        cache = (self.k if which == 0 else self.v).view(np.uint16)
+        words = self.hd * (1 if self.dtype == F16 else 2)
+        lib().orc_block_checksums(_p(cache), self.bs, self.n_kv, words,
                                   _p(blocks), blocks.size, _p(out))
         return out
 
@@ -282,14 +285,14 @@ def decode_step(cache: KvCache, slot_block, slot_off, new_k, new_v,
     """One decode step of one layer as rvllm's CPU path runs it
     (src/model.rs:628-644): append, padded gather, mask, gqa_attention.
     Mutates ``cache``; returns out [batch, n_heads, hd]."""
-    assert cache.dtype == F16
     q = _f32(q)
     batch, n_heads, hd = q.shape
     sb, so = _u32(slot_block), _u32(slot_off)
     nk, nv = _f32(new_k), _f32(new_v)
     bi, rn = _u32(block_idx), _u32(read_num_tokens)
     out = np.empty_like(q)
-    rc = lib().orc_decode_step(_p(cache.k), _p(cache.v), cache.num_blocks,
+    rc = lib().orc_decode_step(_p(cache.k), _p(cache.v), cache.dtype,
+                               cache.num_blocks,
                                cache.bs, cache.n_kv, cache.hd, _p(sb), _p(so),
                                _p(nk), _p(nv), _p(bi), max_blocks, _p(rn),
                                batch, n_heads, _p(q), _p(out), n_threads)

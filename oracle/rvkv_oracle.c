@@ -404,8 +404,9 @@ void orc_copy_blocks(void *cache, int dtype, uint32_t bs, uint32_t n_kv,
             blk);
 }
 
-/* 64-bit FNV-1a over the logical f16 bytes of each listed block (the
- * checksum rvkv_block_checksums computes on the device). */
+/* 64-bit FNV-1a over the logical bytes of each listed block, read as 16-bit
+ * words (hd counts words: two per f32 cell) - the checksum
+ * rvkv_block_checksums computes on the device. */
 void orc_block_checksums(const uint16_t *cache, uint32_t bs, uint32_t n_kv,
                          uint32_t hd, const uint32_t *blocks, uint32_t n,
                          uint64_t *out) {
@@ -428,9 +429,10 @@ void orc_block_checksums(const uint16_t *cache, uint32_t bs, uint32_t n_kv,
  * split over (sequence, KV head) across n_threads pthreads; each does the
  * gather of its slice (a padded [ctx_len, hd] K and V in f32) and the
  * attention of its group of query heads against it, so the arithmetic is the
- * reference's, parallelised. Cache: logical layout, f16 cells. */
+ * reference's, parallelised. Cache: logical layout, f16 or f32 cells. */
 typedef struct {
-  const uint16_t *ck, *cv;
+  const void *ck, *cv;
+  int dtype;
   uint32_t bs, n_kv, hd, n_heads, max_blocks, ctx_len, batch;
   const uint32_t *block_idx, *read_num_tokens;
   const float *q;
@@ -458,8 +460,8 @@ static void *orc_worker(void *arg) {
       size_t blk = J->block_idx[(size_t)b * J->max_blocks + p / J->bs];
       size_t src = ((blk * J->bs + p % J->bs) * J->n_kv + h) * J->hd;
       for (uint32_t d = 0; d < J->hd; ++d) {
-        k[(size_t)p * J->hd + d] = orc_f16_to_f32(J->ck[src + d]);
-        v[(size_t)p * J->hd + d] = orc_f16_to_f32(J->cv[src + d]);
+        k[(size_t)p * J->hd + d] = cell_get(J->ck, J->dtype, src + d);
+        v[(size_t)p * J->hd + d] = cell_get(J->cv, J->dtype, src + d);
       }
     }
     uint32_t pos = J->read_num_tokens[b] ? J->read_num_tokens[b] - 1 : 0;
@@ -480,7 +482,7 @@ static void *orc_worker(void *arg) {
 
 /* Appends one f32 row per sequence (src/kv_storage.rs:116-150), then runs
  * the padded-gather attention above. Returns 0 or -1 on a bad slot. */
-int orc_decode_step(uint16_t *cache_k, uint16_t *cache_v, uint32_t num_blocks,
+int orc_decode_step(void *cache_k, void *cache_v, int dtype, uint32_t num_blocks,
                     uint32_t bs, uint32_t n_kv, uint32_t hd,
                     const uint32_t *slot_block, const uint32_t *slot_off,
                     const float *new_k, const float *new_v,
@@ -488,7 +490,7 @@ int orc_decode_step(uint16_t *cache_k, uint16_t *cache_v, uint32_t num_blocks,
                     const uint32_t *read_num_tokens, uint32_t batch,
                     uint32_t n_heads, const float *q, float *out,
                     uint32_t n_threads) {
-  if (orc_write_tokens(cache_k, cache_v, ORC_F16, num_blocks, bs, n_kv, hd,
+  if (orc_write_tokens(cache_k, cache_v, dtype, num_blocks, bs, n_kv, hd,
                        slot_block, slot_off, batch, new_k, new_v))
     return -1;
   uint32_t ctx_len = 0;
@@ -497,6 +499,7 @@ int orc_decode_step(uint16_t *cache_k, uint16_t *cache_v, uint32_t num_blocks,
   orc_job J;
   J.ck = cache_k;
   J.cv = cache_v;
+  J.dtype = dtype;
   J.bs = bs;
   J.n_kv = n_kv;
   J.hd = hd;

@@ -10,17 +10,25 @@
 
 // Physical cache layout, per layer and per K/V tensor, f16:
 //   [num_blocks][n_kv_heads][block_size][head_dim]
+// Cells are f16 (elem_bytes 2) or f32 (elem_bytes 4, rvllm's own cache
+// dtype). The byte-moving kernels (append of same-typed rows, gather, copy,
+// inspection) see an f32 cell as two 16-bit words: the *16 sizes below count
+// 16-bit words, the *_elems ones cells.
 struct rvkv_pool {
   uint32_t n_layers, num_blocks, block_size, n_kv, head_dim;
+  uint32_t elem_bytes;   // 2 or 4
+  uint32_t hd16;         // head_dim * elem_bytes / 2
   hipStream_t stream;
   int device;
   uint16_t *base;        // 2 * n_layers tensors
   size_t tensor_elems;   // num_blocks * n_kv * block_size * head_dim
   size_t block_elems;    // n_kv * block_size * head_dim
+  size_t tensor16, block16;
 
   uint16_t *tensor(uint32_t layer, uint32_t which) const {
-    return base + ((size_t)layer * 2 + which) * tensor_elems;
+    return base + ((size_t)layer * 2 + which) * tensor16;
   }
+  bool f32() const { return elem_bytes == 4; }
 };
 
 namespace rvkv_detail {

@@ -871,6 +871,8 @@ int rvkv_paged_prefill(rvkv_pool *pool, uint32_t layer, const float *q,
     return fail(RVKV_EINVAL, op,
                 "n_heads must be a positive multiple of n_kv_heads");
   const uint32_t hd = pool->head_dim, bs = pool->block_size;
+  if (pool->f32())
+    return fail(RVKV_EUNSUPPORTED, op, "needs an f16 cache");
   if (hd != 32 && hd != 64 && hd != 128 && hd != 256)
     return fail(RVKV_EUNSUPPORTED, op, "head_dim must be 32, 64, 128 or 256");
   if (bs < 8 || (bs & (bs - 1)) != 0)
@@ -940,7 +942,8 @@ namespace rvkv_detail {
 bool mfma_decode_wanted(const rvkv_pool *pool, uint32_t n_heads) {
   static const char *env = getenv("RVKV_DECODE_MFMA");
   const uint32_t group = pool->n_kv ? n_heads / pool->n_kv : 0;
-  const bool shape_ok = pool->head_dim == 64 && group >= 1 && group <= 32 &&
+  const bool shape_ok = !pool->f32() && pool->head_dim == 64 && group >= 1 &&
+                        group <= 32 &&
                         pool->block_elems * 2 < 0x100000000ull &&
                         pool->block_size >= 8 &&
                         (pool->block_size & (pool->block_size - 1)) == 0 &&

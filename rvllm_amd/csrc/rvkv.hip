@@ -120,6 +120,28 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+// f16 rows appended to an f32 cache: every f16 value is exact in f32.
+__global__ void __launch_bounds__(256)
+    append_widen_kernel(const uint16_t *__restrict__ k,
+                        const uint16_t *__restrict__ v,
+                        const uint32_t *__restrict__ slot_block,
+                        const uint32_t *__restrict__ slot_off,
+                        float *__restrict__ kc, float *__restrict__ vc,
+                        uint32_t n_tokens, uint32_t n_kv, uint32_t hd,
+                        uint32_t bs, uint32_t num_blocks) {
+  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const uint64_t per_token = (uint64_t)n_kv * hd;
+  if (i >= n_tokens * per_token) return;
+  const uint32_t token = (uint32_t)(i / per_token);
+  const uint32_t j = (uint32_t)(i - token * per_token);  // head * hd + d
+  const uint32_t blk = slot_block[token], off = slot_off[token];
+  if (blk >= num_blocks || off >= bs) return;
+  const uint32_t head = j / hd, d = j - head * hd;
+  const size_t dst = (((size_t)blk * n_kv + head) * bs + off) * hd + d;
+  kc[dst] = (float)__builtin_bit_cast(_Float16, k[i]);
+  vc[dst] = (float)__builtin_bit_cast(_Float16, v[i]);
+}
+
 // ---------------------------------------------------------------------------
 // Block-table gather into rvllm's padded [batch, n_kv, ctx_len, hd].
 // Replaces kv_gather.cu. One thread per VW output elements.
@@ -437,6 +459,7 @@ struct DecodeArgs {
   uint32_t max_blocks, num_blocks, n_kv, n_heads, group, n_sub;
   uint32_t bs_log2, part_tokens, n_parts, ctx_cap;
   uint32_t hd;  // the cache's head_dim (the kernels' HD is it rounded up)
+  uint32_t f32cache;  // cells are f32 (decode_f32_kernel) instead of f16
   float qscale;
   int32_t window;
   // Host-side launch hint (not read by the kernels): average context
@@ -1041,6 +1064,210 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
   }
 }
 
+// Decode over an f32 cache (rvllm's own cache dtype): the layout, work
+// split, partials and merges of decode_part_kernel, with f32 cells and f32
+// arithmetic throughout (q.k and p.v as f32 fmas, probabilities in f32).
+// A lane loads 4 cells (16 bytes) per row and load, NL loads per row: R =
+// HD / (4 NL) lanes per row, RPL = 64 / R rows per wave-wide load. Masked
+// keys load zero rows, as in the f16 kernel.
+template <int HD, int GT>
+__global__ void __launch_bounds__(256) decode_f32_kernel(DecodeArgs a) {
+  constexpr int NL = HD >= 256 ? 2 : 1;
+  constexpr int R = HD / (4 * NL);
+  constexpr int RPL = 64 / R;
+  constexpr int U = 4;
+  constexpr int TC = U * RPL;
+  static_assert(R >= 2 && R <= 32, "row must span 2..32 lanes");
+  extern __shared__ float lds[];  // [W][GT][HD + 2]
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int W = blockDim.x >> 6;
+  const int rg = lane / R, c = lane % R;
+  const uint32_t kvh = blockIdx.y / a.n_sub;
+  const uint32_t sub = blockIdx.y - kvh * a.n_sub;
+  uint32_t b, t0, tend, slot;
+  if (a.items) {
+    const uint4 it = a.items[blockIdx.x];
+    b = it.x;
+    t0 = it.y;
+    tend = it.z;
+    slot = it.w;
+  } else {
+    b = blockIdx.z;
+    t0 = blockIdx.x * a.part_tokens;
+    tend = t0 + a.part_tokens;
+    slot = a.n_parts > 1 ? b * a.n_parts + blockIdx.x : kNoSlot;
+  }
+  const uint32_t h0 = kvh * a.group + sub * GT;
+  const uint32_t ng = min((uint32_t)GT, a.group - sub * GT);
+  typedef const __attribute__((address_space(4))) uint32_t cu32;
+  cu32 *table = (cu32 *)(uintptr_t)(a.tables + (size_t)b * a.max_blocks);
+
+  float4 q[GT][NL];
+#pragma unroll
+  for (int g = 0; g < GT; ++g) {
+    const uint32_t hg = h0 + ((uint32_t)g < ng ? g : 0);
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+      float4 x = *reinterpret_cast<const float4 *>(
+          a.q + ((size_t)b * a.n_heads + hg) * HD + (j * R + c) * 4);
+      q[g][j] = make_float4(x.x * a.qscale, x.y * a.qscale, x.z * a.qscale,
+                            x.w * a.qscale);
+    }
+  }
+  uint32_t ctx = min(a.ctx_lens[b], a.ctx_cap);
+  const uint32_t lo =
+      (a.window > 0 && ctx > (uint32_t)a.window) ? ctx - (uint32_t)a.window : 0;
+  const uint32_t t1 = min(tend, ctx);
+  if (!a.items && ctx <= a.part_tokens) slot = kNoSlot;
+  if (t0 >= t1) {
+    if (ctx == 0 && t0 == 0 && wave == 0 && rg == 0)
+      for (uint32_t g = 0; g < ng; ++g)
+#pragma unroll
+        for (int j = 0; j < NL; ++j)
+          *reinterpret_cast<float4 *>(a.out + ((size_t)b * a.n_heads + h0 + g) *
+                                                  HD + (j * R + c) * 4) =
+              make_float4(0.f, 0.f, 0.f, 0.f);
+    return;
+  }
+
+  float m[GT], l[GT], acc[GT][NL * 4];
+#pragma unroll
+  for (int g = 0; g < GT; ++g) {
+    m[g] = kNegBig;
+    l[g] = 0.f;
+#pragma unroll
+    for (int e = 0; e < NL * 4; ++e) acc[g][e] = 0.f;
+  }
+  const uint32_t first = t0 + (uint32_t)wave * TC;
+  const uint32_t stride = (uint32_t)W * TC;
+  const uint32_t skip = lo > t0 ? (lo - t0) / stride * stride : 0;
+  const uint32_t bs_mask = (1u << a.bs_log2) - 1u;
+  const uint32_t last_blk = (ctx - 1) >> a.bs_log2;
+  const char *kbase =
+      reinterpret_cast<const char *>(a.kc) + (size_t)kvh * a.head_stride * 4;
+  const char *vbase =
+      reinterpret_cast<const char *>(a.vc) + (size_t)kvh * a.head_stride * 4;
+  const uint32_t lane_off = (uint32_t)(rg * HD * 4 + c * 16);
+  const char *zero_v = reinterpret_cast<const char *>(g_zero_rows) + lane_off;
+  const uint64_t blk_bytes = a.block_stride * 4;
+  for (uint32_t ch = first + skip; ch < t1; ch += stride) {
+    float4 kr[U][NL], vr[U][NL];
+    bool valid[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t tb = ch + u * RPL;
+      const uint32_t id = table[min(tb >> a.bs_log2, last_blk)];
+      const uint32_t tok = tb + rg;
+      valid[u] = id < a.num_blocks && tok >= lo && tok < t1;
+      const char *row = (uint64_t)(id < a.num_blocks ? id : 0u) * blk_bytes +
+                        (uint64_t)(tb & bs_mask) * (HD * 4) + lane_off + kbase;
+      const char *kp = valid[u] ? row : zero_v;
+      const char *vp = valid[u] ? row - kbase + vbase : zero_v;
+#pragma unroll
+      for (int j = 0; j < NL; ++j) {
+        kr[u][j] = *reinterpret_cast<const float4 *>(kp + j * R * 16);
+        vr[u][j] = *reinterpret_cast<const float4 *>(vp + j * R * 16);
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+      float s[U];
+      float mx = m[g];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        float d = 0.f;
+#pragma unroll
+        for (int j = 0; j < NL; ++j) {
+          d = __builtin_fmaf(q[g][j].x, kr[u][j].x, d);
+          d = __builtin_fmaf(q[g][j].y, kr[u][j].y, d);
+          d = __builtin_fmaf(q[g][j].z, kr[u][j].z, d);
+          d = __builtin_fmaf(q[g][j].w, kr[u][j].w, d);
+        }
+        d = row_group_sum<R>(d);
+        s[u] = valid[u] ? d : -__builtin_inff();
+        mx = fmaxf(mx, s[u]);
+      }
+      const float corr = __builtin_amdgcn_exp2f(m[g] - mx);
+      m[g] = mx;
+      l[g] *= corr;
+#pragma unroll
+      for (int e = 0; e < NL * 4; ++e) acc[g][e] *= corr;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const float pu = __builtin_amdgcn_exp2f(s[u] - mx);
+        l[g] += pu;
+#pragma unroll
+        for (int j = 0; j < NL; ++j) {
+          acc[g][j * 4 + 0] = __builtin_fmaf(pu, vr[u][j].x, acc[g][j * 4 + 0]);
+          acc[g][j * 4 + 1] = __builtin_fmaf(pu, vr[u][j].y, acc[g][j * 4 + 1]);
+          acc[g][j * 4 + 2] = __builtin_fmaf(pu, vr[u][j].z, acc[g][j * 4 + 2]);
+          acc[g][j * 4 + 3] = __builtin_fmaf(pu, vr[u][j].w, acc[g][j * 4 + 3]);
+        }
+      }
+    }
+  }
+  // Merge the row groups of the wave, then the waves through LDS.
+#pragma unroll
+  for (int g = 0; g < GT; ++g) {
+#pragma unroll
+    for (int off = R; off < 64; off <<= 1) {
+      const float mo = __shfl_xor(m[g], off);
+      const float lo_ = __shfl_xor(l[g], off);
+      const float mx = fmaxf(m[g], mo);
+      const float ws = __builtin_amdgcn_exp2f(m[g] - mx);
+      const float wo = __builtin_amdgcn_exp2f(mo - mx);
+      l[g] = l[g] * ws + lo_ * wo;
+#pragma unroll
+      for (int e = 0; e < NL * 4; ++e) {
+        const float ao = __shfl_xor(acc[g][e], off);
+        acc[g][e] = acc[g][e] * ws + ao * wo;
+      }
+      m[g] = mx;
+    }
+  }
+  constexpr int ROW = HD + 2;
+  if (rg == 0) {
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+      float *r = lds + ((size_t)wave * GT + g) * ROW;
+      if (c == 0) {
+        r[0] = m[g];
+        r[1] = l[g];
+      }
+#pragma unroll
+      for (int j = 0; j < NL; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[2 + (j * R + c) * 4 + e] = acc[g][j * 4 + e];
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < GT * HD; i += blockDim.x) {
+    const int g = i / HD, d = i - g * HD;
+    if ((uint32_t)g >= ng) break;
+    float M = kNegBig;
+    for (int w = 0; w < W; ++w) M = fmaxf(M, lds[((size_t)w * GT + g) * ROW]);
+    float L = 0.f, x = 0.f;
+    for (int w = 0; w < W; ++w) {
+      const float *r = lds + ((size_t)w * GT + g) * ROW;
+      const float wt = __builtin_amdgcn_exp2f(r[0] - M);
+      L += r[1] * wt;
+      x += r[2 + d] * wt;
+    }
+    if (slot == kNoSlot) {
+      a.out[((size_t)b * a.n_heads + h0 + g) * HD + d] = L > 0.f ? x / L : 0.f;
+    } else {
+      const size_t idx = (size_t)slot * a.n_heads + h0 + g;
+      a.ws_acc[idx * HD + d] = x;
+      if (d == 0) {
+        a.ws_ml[idx * 2] = M;
+        a.ws_ml[idx * 2 + 1] = L;
+      }
+    }
+  }
+}
+
 // Reduction pass (only for sequences split over several partitions): one
 // wave per (sequence, query head) merges its partitions: M = max m_i,
 // out = sum_i 2^(m_i - M) acc_i / sum_i 2^(m_i - M) l_i. Partitions that saw
@@ -1276,7 +1503,10 @@ void launch_decode(const DecodeArgs &a, dim3 grid, hipStream_t st) {
                            : ((HD >= 256 && a.avg_tokens >= 512) ||
                               (GT >= 5 && W == 1));
   const size_t lds = (size_t)W * GT * (HD + 2) * sizeof(float);
-  if (a.hd != HD)  // a head_dim below HD: rows read element by element
+  if (a.f32cache)
+    hipLaunchKernelGGL((decode_f32_kernel<HD, GT>), grid, dim3(64 * W), lds, st,
+                       a);
+  else if (a.hd != HD)  // a head_dim below HD: rows read element by element
     hipLaunchKernelGGL((decode_part_kernel<HD, GT, 4, 1, true>), grid,
                        dim3(64 * W), lds, st, a);
   else if (u8)
@@ -1323,23 +1553,27 @@ int rvkv_pool_create(uint32_t n_layers, uint32_t num_blocks,
     return fail(RVKV_EINVAL, op,
                 "n_layers/num_blocks/block_size/n_kv_heads/head_dim must be "
                 "positive");
-  if (cache_dtype != RVKV_F16)
-    return fail(RVKV_EUNSUPPORTED, op, "only an f16 cache is supported");
+  if (cache_dtype != RVKV_F16 && cache_dtype != RVKV_F32)
+    return fail(RVKV_EINVAL, op, "cache dtype must be F16 or F32");
   rvkv_pool *p = new rvkv_pool();
   p->n_layers = n_layers;
   p->num_blocks = num_blocks;
   p->block_size = block_size;
   p->n_kv = n_kv_heads;
   p->head_dim = head_dim;
+  p->elem_bytes = cache_dtype == RVKV_F32 ? 4 : 2;
+  p->hd16 = head_dim * p->elem_bytes / 2;
   p->stream = static_cast<hipStream_t>(stream);
   p->block_elems = (size_t)n_kv_heads * block_size * head_dim;
   p->tensor_elems = p->block_elems * num_blocks;
+  p->block16 = p->block_elems * p->elem_bytes / 2;
+  p->tensor16 = p->tensor_elems * p->elem_bytes / 2;
   hipError_t e = hipGetDevice(&p->device);
   if (e != hipSuccess) {
     delete p;
     return hip_fail(op, e);
   }
-  const size_t bytes = p->tensor_elems * 2 * 2 * n_layers;
+  const size_t bytes = p->tensor16 * 2 * 2 * n_layers;
   e = hipMalloc(&p->base, bytes);
   if (e != hipSuccess) {
     delete p;
@@ -1364,7 +1598,7 @@ void rvkv_pool_destroy(rvkv_pool *pool) {
 }
 
 size_t rvkv_pool_bytes(const rvkv_pool *pool) {
-  return pool ? pool->tensor_elems * 4 * pool->n_layers : 0;
+  return pool ? pool->tensor16 * 4 * pool->n_layers : 0;
 }
 
 int rvkv_pool_set_stream(rvkv_pool *pool, rvkv_stream stream) {
@@ -1385,16 +1619,35 @@ int rvkv_append(rvkv_pool *pool, uint32_t layer, const void *k, const void *v,
     return fail(RVKV_EINVAL, op, "NULL k/v/block_ids/offsets");
   if (src_dtype != RVKV_F16 && src_dtype != RVKV_F32)
     return fail(RVKV_EINVAL, op, "src dtype must be F16 or F32");
-  const uint32_t hd = pool->head_dim;
+  uint16_t *kc = pool->tensor(layer, 0), *vc = pool->tensor(layer, 1);
+  if (pool->f32() && src_dtype == RVKV_F16) {
+    // f16 rows into an f32 cache: widened exactly, one thread per cell.
+    const uint64_t cells = (uint64_t)n_tokens * pool->n_kv * pool->head_dim;
+    hipLaunchKernelGGL(append_widen_kernel, dim3(grid_1d(cells, 256)),
+                       dim3(256), 0, pool->stream,
+                       static_cast<const uint16_t *>(k),
+                       static_cast<const uint16_t *>(v), slot_block, slot_off,
+                       reinterpret_cast<float *>(kc),
+                       reinterpret_cast<float *>(vc), n_tokens, pool->n_kv,
+                       pool->head_dim, pool->block_size, pool->num_blocks);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? RVKV_OK : hip_fail(op, e);
+  }
+  // f32 rows into an f32 cache are copied bit for bit: the same kernel as
+  // an f16 copy, over 16-bit words (hd16 of them per row).
+  const bool f32_copy = pool->f32();
+  if (f32_copy) src_dtype = RVKV_F16;
+  const uint32_t hd = pool->hd16;
   const bool v8 = hd % 8 == 0;
   if (v8 && src_dtype == RVKV_F32 &&
       ((uintptr_t)k % 16 || (uintptr_t)v % 16))
     return fail(RVKV_EINVAL, op, "f32 k/v must be 16-byte aligned");
   if (v8 && src_dtype == RVKV_F16 && ((uintptr_t)k % 16 || (uintptr_t)v % 16))
-    return fail(RVKV_EINVAL, op, "f16 k/v must be 16-byte aligned");
+    return fail(RVKV_EINVAL, op,
+                f32_copy ? "f32 k/v must be 16-byte aligned"
+                         : "f16 k/v must be 16-byte aligned");
   const uint64_t threads = (uint64_t)n_tokens * pool->n_kv * (v8 ? hd / 8 : hd);
   const dim3 grid(grid_1d(threads, 256));
-  uint16_t *kc = pool->tensor(layer, 0), *vc = pool->tensor(layer, 1);
   if (v8) {
     if (src_dtype == RVKV_F32)
       hipLaunchKernelGGL((append_kernel<8, true>), grid, dim3(256), 0,
@@ -1441,7 +1694,14 @@ int rvkv_gather(const rvkv_pool *pool, uint32_t layer,
     return fail(RVKV_EINVAL, op, "NULL block_idx/out_k/out_v");
   if (out_dtype != RVKV_F16 && out_dtype != RVKV_F32)
     return fail(RVKV_EINVAL, op, "out dtype must be F16 or F32");
-  const uint32_t hd = pool->head_dim;
+  if (pool->f32()) {
+    // An f32 cache gathers into f32 only, bit for bit: the raw-copy kernel
+    // over 16-bit words.
+    if (out_dtype != RVKV_F32)
+      return fail(RVKV_EUNSUPPORTED, op, "an f32 cache gathers into F32 only");
+    out_dtype = RVKV_F16;
+  }
+  const uint32_t hd = pool->hd16;
   const bool v8 = hd % 8 == 0 && (uintptr_t)out_k % 16 == 0 &&
                   (uintptr_t)out_v % 16 == 0;
   const uint64_t rows = (uint64_t)batch * pool->n_kv * ctx_len;
@@ -1497,6 +1757,9 @@ int prepare_decode(const char *op, const rvkv_pool *pool, uint32_t layer,
   const uint32_t hdp = decode_hd(pool->head_dim);
   if (hdp == 0)
     return fail(RVKV_EUNSUPPORTED, op, "head_dim must be at most 256");
+  if (pool->f32() && hdp != pool->head_dim)
+    return fail(RVKV_EUNSUPPORTED, op,
+                "an f32 cache needs head_dim 32, 64, 128 or 256");
   const uint32_t bs = pool->block_size;
   if ((bs & (bs - 1)) != 0 || bs < 512 / hdp)
     return fail(RVKV_EUNSUPPORTED, op,
@@ -1523,6 +1786,7 @@ int prepare_decode(const char *op, const rvkv_pool *pool, uint32_t layer,
   a->block_stride = pool->block_elems;
   a->head_stride = bs * pool->head_dim;
   a->hd = pool->head_dim;
+  a->f32cache = pool->f32() ? 1u : 0u;
   a->block_size = bs;
   a->max_blocks = max_blocks;
   a->num_blocks = pool->num_blocks;
@@ -2030,11 +2294,18 @@ int rvkv_decode_step(rvkv_pool *pool, const rvkv_decode_plan *plan,
                           plan ? plan->max_ctx : max_ctx_len, scale, window,
                           out, &a, &gt);
   if (rc) return rc;
-  a.new_k = k;
-  a.new_v = v;
-  a.new_blk = slot_block;
-  a.new_off = slot_off;
-  a.new_f32 = src_dtype == RVKV_F32;
+  if (pool->f32()) {
+    // f32 cache: the append and the decode as two launches on the stream.
+    if ((rc = rvkv_append(pool, layer, k, v, src_dtype, slot_block, slot_off,
+                          batch)))
+      return rc;
+  } else {
+    a.new_k = k;
+    a.new_v = v;
+    a.new_blk = slot_block;
+    a.new_off = slot_off;
+    a.new_f32 = src_dtype == RVKV_F32;
+  }
   if (plan) {
     if (plan->n_kv != pool->n_kv || plan->head_dim != pool->head_dim)
       return fail(RVKV_EINVAL, op, "plan was built for another pool shape");
@@ -2146,6 +2417,7 @@ int attn_prep_check(rvkv_pool *pool, uint32_t layer, uint32_t rows,
   if (!hd_supported(pool->head_dim))
     return fail(RVKV_EUNSUPPORTED, op,
                 "head_dim must be one of 32, 64, 128, 256");
+  if (pool->f32()) return fail(RVKV_EUNSUPPORTED, op, "needs an f16 cache");
   return 1;
 }
 
@@ -2201,7 +2473,7 @@ int rvkv_copy_blocks(rvkv_pool *pool, const uint32_t *src, const uint32_t *dst,
   if (n == 0) return RVKV_OK;
   if (!src || !dst) return fail(RVKV_EINVAL, op, "NULL src/dst");
   if (n > 65535) return fail(RVKV_EUNSUPPORTED, op, "at most 65535 pairs per call");
-  const size_t bytes = pool->block_elems * 2;
+  const size_t bytes = pool->block16 * 2;
   const bool w16 = bytes % 16 == 0;
   const size_t words = w16 ? bytes / 16 : bytes / 2;
   uint32_t gx = grid_1d(words, 256);
@@ -2209,12 +2481,12 @@ int rvkv_copy_blocks(rvkv_pool *pool, const uint32_t *src, const uint32_t *dst,
   const dim3 grid(gx, n, 2 * pool->n_layers);
   if (w16)
     hipLaunchKernelGGL(copy_blocks_kernel<uint4>, grid, dim3(256), 0,
-                       pool->stream, pool->base, src, dst, pool->tensor_elems,
-                       pool->block_elems, pool->num_blocks);
+                       pool->stream, pool->base, src, dst, pool->tensor16,
+                       pool->block16, pool->num_blocks);
   else
     hipLaunchKernelGGL(copy_blocks_kernel<uint16_t>, grid, dim3(256), 0,
-                       pool->stream, pool->base, src, dst, pool->tensor_elems,
-                       pool->block_elems, pool->num_blocks);
+                       pool->stream, pool->base, src, dst, pool->tensor16,
+                       pool->block16, pool->num_blocks);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? RVKV_OK : hip_fail(op, e);
 }
@@ -2227,11 +2499,11 @@ int rvkv_read_blocks(const rvkv_pool *pool, uint32_t layer, uint32_t which,
     return fail(RVKV_EINVAL, op, "layer or which out of range");
   if (n == 0) return RVKV_OK;
   if (!block_ids || !out) return fail(RVKV_EINVAL, op, "NULL block_ids/out");
-  const dim3 grid(grid_1d((uint64_t)pool->block_elems * n, 256));
+  const dim3 grid(grid_1d((uint64_t)pool->block16 * n, 256));
   hipLaunchKernelGGL(read_blocks_kernel, grid, dim3(256), 0, pool->stream,
                      pool->tensor(layer, which), block_ids, n,
                      static_cast<uint16_t *>(out), pool->block_size,
-                     pool->n_kv, pool->head_dim, pool->num_blocks);
+                     pool->n_kv, pool->hd16, pool->num_blocks);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? RVKV_OK : hip_fail(op, e);
 }
@@ -2247,7 +2519,7 @@ int rvkv_block_checksums(const rvkv_pool *pool, uint32_t layer,
   if (!block_ids || !out) return fail(RVKV_EINVAL, op, "NULL block_ids/out");
   hipLaunchKernelGGL(checksum_kernel, dim3(grid_1d(n, 64)), dim3(64), 0,
                      pool->stream, pool->tensor(layer, which), block_ids, n,
-                     out, pool->block_size, pool->n_kv, pool->head_dim,
+                     out, pool->block_size, pool->n_kv, pool->hd16,
                      pool->num_blocks);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? RVKV_OK : hip_fail(op, e);

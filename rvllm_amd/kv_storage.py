@@ -134,11 +134,14 @@ class HipDecodePlan:
 
 
 class HipKvStorage:
-    """CudaKvStorage (src/cuda/kv_storage.rs:65-164) on MI355X: one zeroed f16
-    pool for all layers' K and V, owned by librvkv."""
+    """CudaKvStorage (src/cuda/kv_storage.rs:65-164) on MI355X: one zeroed
+    pool for all layers' K and V, owned by librvkv. Cells are f16 (the
+    default) or, with dtype=torch.float32, f32 like rvllm's own cache (append,
+    gather, copy and decode; prefill attention and attn_prep need f16)."""
 
     def __init__(self, n_layers: int, num_blocks: int, block_size: int,
-                 n_kv_heads: int, head_dim: int, stream=None):
+                 n_kv_heads: int, head_dim: int, stream=None,
+                 dtype: torch.dtype = torch.float16):
         self._L = _lib.load()
         self.n_layers, self.num_blocks = n_layers, num_blocks
         self.block_size, self.n_kv_heads, self.head_dim = (block_size,
@@ -148,9 +151,12 @@ class HipKvStorage:
         if stream is None:
             stream = torch.cuda.current_stream(self.device)
         self.stream = stream
+        _need(dtype in _DT, "pool_create: cache dtype must be float16 or "
+              "float32")
+        self.dtype = dtype
         handle = ctypes.c_void_p()
         check(self._L.rvkv_pool_create(n_layers, num_blocks, block_size,
-                                       n_kv_heads, head_dim, RVKV_F16,
+                                       n_kv_heads, head_dim, _DT[dtype],
                                        ctypes.c_void_p(stream.cuda_stream),
                                        ctypes.byref(handle)))
         self._pool = handle
@@ -469,10 +475,11 @@ class HipKvStorage:
     # -- inspection ---------------------------------------------------------
     def read_blocks(self, layer: int, which: int,
                     block_ids: torch.Tensor) -> torch.Tensor:
-        """Logical [n, block_size, n_kv, hd] f16 contents of the blocks."""
+        """Logical [n, block_size, n_kv, hd] contents of the blocks, in the
+        cache's dtype."""
         n = block_ids.numel()
         out = torch.empty((n, self.block_size, self.n_kv_heads,
-                           self.head_dim), dtype=torch.float16,
+                           self.head_dim), dtype=self.dtype,
                           device=self.device)
         check(self._L.rvkv_read_blocks(self._pool, layer, which,
                                        _ptr(block_ids), n, _ptr(out)))
@@ -480,7 +487,8 @@ class HipKvStorage:
 
     def block_checksums(self, layer: int, which: int,
                         block_ids: torch.Tensor) -> torch.Tensor:
-        """FNV-1a 64 of each block's logical f16 bytes (int64 bits)."""
+        """FNV-1a 64 of each block's logical little-endian bytes (int64
+        bits)."""
         n = block_ids.numel()
         out = torch.empty(n, dtype=torch.int64, device=self.device)
         check(self._L.rvkv_block_checksums(self._pool, layer, which,

@@ -263,14 +263,17 @@ def test_paged_decode_f64_window_matches_masked_sdpa():
         assert np.max(np.abs(out - ref)) < 1e-5
 
 
-def test_decode_step_matches_f64():
+@pytest.mark.parametrize("dt", [orc.F16, orc.F32])
+def test_decode_step_matches_f64(dt):
     """orc_decode_step (append + padded gather + mask + gqa in f32, the CPU
-    baseline) against the float64 paged reference, multi-threaded."""
+    baseline) against the float64 paged reference, multi-threaded, over f16
+    cells and over the reference's f32 cells."""
     rng = np.random.default_rng(7)
     nb, bs, nkv, hd, H = 64, 16, 2, 64, 6
-    cache = orc.KvCache(nb, bs, nkv, hd, orc.F16)
-    cache.k[:] = orc.f32_to_f16_bits(rng.standard_normal(cache.k.shape))
-    cache.v[:] = orc.f32_to_f16_bits(rng.standard_normal(cache.v.shape))
+    cache = orc.KvCache(nb, bs, nkv, hd, dt)
+    cache.write_tokens(np.repeat(np.arange(nb), bs), np.tile(np.arange(bs), nb),
+                       rng.standard_normal((nb * bs, nkv, hd)),
+                       rng.standard_normal((nb * bs, nkv, hd)))
     ctx = np.array([33, 200, 17, 128], np.uint32)
     perm = rng.permutation(nb).astype(np.uint32)
     tables = [perm[i * 16:(i + 1) * 16] for i in range(4)]
@@ -280,7 +283,7 @@ def test_decode_step_matches_f64():
     nk = rng.standard_normal((4, nkv, hd)).astype(np.float32)
     nv = rng.standard_normal((4, nkv, hd)).astype(np.float32)
     q = rng.standard_normal((4, H, hd)).astype(np.float32)
-    ref_cache = orc.KvCache(nb, bs, nkv, hd, orc.F16)
+    ref_cache = orc.KvCache(nb, bs, nkv, hd, dt)
     ref_cache.k[:] = cache.k
     ref_cache.v[:] = cache.v
     ref_cache.write_tokens(sb, so, nk, nv)
@@ -319,6 +322,12 @@ def test_block_checksums_match_independent_fnv():
     got = c.checksums(0, [5, 0, 3])
     for i, b in enumerate([5, 0, 3]):
         assert int(got[i]) == _fnv1a64(c.k[b].astype("<u2").tobytes())
+    # f32 cells hash their little-endian bytes in logical order
+    f = orc.KvCache(5, 2, 3, 4, orc.F32)
+    f.v[:] = rng.standard_normal(f.v.shape).astype(np.float32)
+    got = f.checksums(1, [4, 1])
+    for i, b in enumerate([4, 1]):
+        assert int(got[i]) == _fnv1a64(f.v[b].astype("<f4").tobytes())
 
 
 # ---- RMS norm / RoPE / attention prep ---------------------------------
