@@ -878,6 +878,9 @@ def run_churn(args, torch, W):
             "avg_launch_ms": round(dec_ms, 5),
         },
     }
+    rc = read_ceiling(torch, dec_bytes, max(args.steps // 10, 3))
+    rc["frac"] = round(achieved / rc["GB/s"], 4)
+    res["roofline"]["stream_read_ceiling"] = rc
     print(json.dumps(res), flush=True)
 
 

@@ -812,10 +812,11 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
                               ? ctx - 1
                               : 0xFFFFFFFFu;
 
-  // Chunks start at multiples of TC inside the partition; the window's
-  // lower edge skips whole chunks below it.
-  const uint32_t skip = lo > t0 ? (lo - t0) / (TC * W) * (TC * W) : 0;
-  const uint32_t start = first + skip;
+  // Chunks are TC tokens from the partition start, taken round-robin by the
+  // W waves; the window's lower edge skips whole rounds below it.
+  const uint32_t base =
+      t0 + (lo > t0 ? (lo - t0) / (TC * W) * (TC * W) : 0);
+  const uint32_t start = base + (uint32_t)wave * TC;
   if (start < t1) {
     // q for the GT heads, this lane's elements, pre-scaled, as f16 hi/lo
     // pairs.
@@ -843,8 +844,7 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
                         (size_t)kvh * a.head_stride * 2;
     const uint32_t lane_off = (uint32_t)(rg * hdr * 2 + c * 16);
     const uint64_t blk_bytes = a.block_stride * 2;
-    const uint32_t stride = (uint32_t)W * TC;
-    if (skip != 0 || last_blk < ((first + TC - 1) >> a.bs_log2)) {
+    if (start != first || last_blk < ((first + TC - 1) >> a.bs_log2)) {
 #pragma unroll
       for (int u = 0; u < U; ++u)
         ids[u] = table[min((start + u * RPL) >> a.bs_log2, last_blk)];
@@ -908,16 +908,15 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
         decode_chunk<R, GT, U, NL, true>(st, qh, ql, kr, vr, ch + rg, lo, t1,
                                          okmask, newtok);
     };
-    {
-      for (uint32_t ch = start; ch < t1; ch += stride) {
-        uint4 kr[U][NL], vr[U][NL];
-        uint32_t okmask;
-        bool full;
-        issue(kr, vr, ids, ch, okmask, full);
-        // Block ids of this wave's next chunk: scalar loads one chunk ahead.
-        fetch_ids(ids, ch + stride);
-        consume(kr, vr, ch, okmask, full);
-      }
+    const uint32_t stride = (uint32_t)W * TC;
+    for (uint32_t ch = start; ch < t1; ch += stride) {
+      uint4 kr[U][NL], vr[U][NL];
+      uint32_t okmask;
+      bool full;
+      issue(kr, vr, ids, ch, okmask, full);
+      // Block ids of this wave's next chunk: scalar loads one chunk ahead.
+      fetch_ids(ids, ch + stride);
+      consume(kr, vr, ch, okmask, full);
     }
 
     if (newtok != 0xFFFFFFFFu && wave == 0) {
@@ -1019,43 +1018,59 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
     }
   }
 
-  // Merge the W waves through LDS: wave w stores [g][m, l, acc[HD]].
-  constexpr int ROW = HD + 2;
+  // Merge the W waves through LDS: wave w stores (m, l) of each head and
+  // its accumulator row; then every thread finishes 4 consecutive elements
+  // of one head's output at a time.
+  float *ml_s = lds;                                  // [W][GT][2]
+  float *acc_s = lds + ((W * GT * 2 + 3) & ~3);       // [W][GT][HD]
   if (rg == 0) {
 #pragma unroll
     for (int g = 0; g < GT; ++g) {
-      float *r = lds + ((size_t)wave * GT + g) * ROW;
       if (c == 0) {
-        r[0] = st.m[g];
-        r[1] = st.l[g];
+        ml_s[(wave * GT + g) * 2] = st.m[g];
+        ml_s[(wave * GT + g) * 2 + 1] = st.l[g];
       }
+      float4 *r = reinterpret_cast<float4 *>(acc_s + (size_t)(wave * GT + g) * HD);
 #pragma unroll
-      for (int j = 0; j < NL; ++j)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) r[2 + (j * R + c) * 8 + e] = st.acc[g][j * 8 + e];
+      for (int j = 0; j < NL; ++j) {
+        const float *x = &st.acc[g][j * 8];
+        r[(j * R + c) * 2] = make_float4(x[0], x[1], x[2], x[3]);
+        r[(j * R + c) * 2 + 1] = make_float4(x[4], x[5], x[6], x[7]);
+      }
     }
   }
   __syncthreads();
 
-  // Each thread finishes (g, d) elements of the GT x HD result.
-  for (int i = threadIdx.x; i < GT * HD; i += blockDim.x) {
-    const int g = i / HD, d = i - g * HD;
+  for (int i = threadIdx.x; i < GT * HD / 4; i += blockDim.x) {
+    const int g = i / (HD / 4), d = (i - g * (HD / 4)) * 4;
     if ((uint32_t)g >= ng) break;
     float M = kNegBig;
-    for (int w = 0; w < W; ++w) M = fmaxf(M, lds[((size_t)w * GT + g) * ROW]);
-    float L = 0.f, x = 0.f;
+    for (int w = 0; w < W; ++w) M = fmaxf(M, ml_s[(w * GT + g) * 2]);
+    float L = 0.f;
+    float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int w = 0; w < W; ++w) {
-      const float *r = lds + ((size_t)w * GT + g) * ROW;
-      const float wt = __builtin_amdgcn_exp2f(r[0] - M);
-      L += r[1] * wt;
-      x += r[2 + d] * wt;
+      const float wt = __builtin_amdgcn_exp2f(ml_s[(w * GT + g) * 2] - M);
+      L += ml_s[(w * GT + g) * 2 + 1] * wt;
+      const float4 v =
+          *reinterpret_cast<const float4 *>(acc_s + (size_t)(w * GT + g) * HD + d);
+      x.x += v.x * wt;
+      x.y += v.y * wt;
+      x.z += v.z * wt;
+      x.w += v.w * wt;
     }
     if (slot == kNoSlot) {
-      if (!RAGGED || (uint32_t)d < hdr)
-        a.out[((size_t)b * a.n_heads + h0 + g) * hdr + d] = x / L;
+      float *o = a.out + ((size_t)b * a.n_heads + h0 + g) * hdr + d;
+      const float y[4] = {x.x / L, x.y / L, x.z / L, x.w / L};
+      if (!RAGGED) {
+        *reinterpret_cast<float4 *>(o) = make_float4(y[0], y[1], y[2], y[3]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if ((uint32_t)(d + e) < hdr) o[e] = y[e];
+      }
     } else {
       const size_t idx = (size_t)slot * a.n_heads + h0 + g;
-      a.ws_acc[idx * HD + d] = x;
+      *reinterpret_cast<float4 *>(a.ws_acc + idx * HD + d) = x;
       if (d == 0) {
         a.ws_ml[idx * 2] = M;
         a.ws_ml[idx * 2 + 1] = L;
@@ -1469,7 +1484,7 @@ uint32_t partition_tokens(const rvkv_pool *p, uint32_t batch, uint32_t n_heads,
 // 27.2 us). RVKV_DECODE_WAVES overrides.
 uint32_t decode_waves(uint64_t workgroups, uint32_t avg_tokens) {
   static const uint32_t forced = env_u32("RVKV_DECODE_WAVES");
-  if (forced == 1 || forced == 2 || forced == 4) return forced;
+  if (forced >= 1 && forced <= 4) return forced;
   if (workgroups >= 2048) return 1;
   return avg_tokens < 192 ? 2 : 4;
 }
@@ -1502,7 +1517,10 @@ void launch_decode(const DecodeArgs &a, dim3 grid, hipStream_t st) {
   const bool u8 = forced_u ? forced_u == 8
                            : ((HD >= 256 && a.avg_tokens >= 512) ||
                               (GT >= 5 && W == 1));
-  const size_t lds = (size_t)W * GT * (HD + 2) * sizeof(float);
+  // (m, l) pairs rounded up to 16 bytes, then the accumulator rows; at
+  // least the f32 kernel's W * GT * (HD + 2) floats.
+  const size_t lds =
+      (((size_t)W * GT * 2 + 3) / 4 * 4 + (size_t)W * GT * HD) * sizeof(float);
   if (a.f32cache)
     hipLaunchKernelGGL((decode_f32_kernel<HD, GT>), grid, dim3(64 * W), lds, st,
                        a);
