@@ -853,8 +853,8 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
     const char *zero_v = reinterpret_cast<const char *>(g_zero_rows) + lane_off;
     // Issues one chunk's K/V loads into (kr, vr) from block ids `cid`;
     // reports its readable-block mask and whether it is full (no key
-    // masked). A chunk at or past t1 (the double-buffered loop's look-ahead)
-    // loads zero rows instead, which stay in the cache.
+    // masked). In a partial chunk, the rows of masked keys are loaded from
+    // the zero rows (in the cache) instead of HBM.
     auto issue = [&](uint4 (&kr)[U][NL], uint4 (&vr)[U][NL],
                      const uint32_t (&cid)[U], uint32_t ch, uint32_t &okmask,
                      bool &full) {
@@ -867,7 +867,6 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
       const bool has_new = newtok >= ch && newtok < ch + TC;
       full = !has_new && ch >= lo && ch + TC <= t1 &&
              okmask == (1u << U) - 1u;
-      const bool past = ch >= t1;  // (wave-uniform)
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const uint32_t tb = ch + u * RPL;  // first token of this load
@@ -877,10 +876,11 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
         const char *kp = kbase + uoff + lane_off;
         const char *vp = vbase + uoff + lane_off;
         if (!full) {  // (wave-uniform)
+          // Rows of masked keys are not read from the cache at all.
           const uint32_t tok = tb + rg;
           const bool valid = ok && tok >= lo && tok < t1 && tok != newtok;
           vp = valid ? vp : zero_v;
-          kp = past ? zero_v : kp;
+          kp = valid ? kp : zero_v;
         }
 #pragma unroll
         for (int j = 0; j < NL; ++j) {
