@@ -68,10 +68,9 @@ const char *rvkv_last_error(void);
  * offsets throughout. cache_dtype RVKV_F16 (the fast path) or RVKV_F32
  * (the reference's own cell type): an f32 pool supports append (f32 rows
  * copied, f16 rows widened exactly), gather into F32 only, copy_blocks,
- * read_blocks, block_checksums, paged decode (uniform, planned, decode_step,
- * no-alloc) at head_dim 32/64/128/256; paged_prefill and attn_prep return
- * RVKV_EUNSUPPORTED on it. The pool binds to the current HIP device and to
- * `stream`. */
+ * read_blocks, block_checksums, paged decode and paged prefill; attn_prep
+ * returns RVKV_EUNSUPPORTED on it. The pool binds to the current HIP device
+ * and to `stream`. */
 int rvkv_pool_create(uint32_t n_layers, uint32_t num_blocks,
                      uint32_t block_size, uint32_t n_kv_heads,
                      uint32_t head_dim, rvkv_dtype cache_dtype,
@@ -129,10 +128,12 @@ int rvkv_gather(const rvkv_pool *pool, uint32_t layer,
  * ws: device scratch of at least rvkv_decode_workspace_bytes(...) bytes,
  * 256-byte aligned; contents need no initialisation.
  * A sequence with ctx_len 0 gets an all-zero output row.
- * Supported: head_dim <= 256 (32, 64, 128 and 256 on the full-speed path;
- * any other value reads rows element by element), block_size a power of
- * two >= 512/HD where HD is head_dim rounded up to 32, 64, 128 or 256,
- * n_heads a multiple of n_kv_heads. */
+ * Supported: head_dim <= 1024, any block_size, n_heads a multiple of
+ * n_kv_heads. The tuned kernels take head_dim <= 256 (32, 64, 128 and 256
+ * at full speed; other values read rows element by element) with block_size
+ * a power of two >= 512/HD, HD being head_dim rounded up to 32, 64, 128 or
+ * 256 (an f32 pool: head_dim exactly 32, 64, 128 or 256); every other shape
+ * runs a generic kernel (f32 arithmetic, no workspace, slower). */
 int rvkv_paged_decode(const rvkv_pool *pool, uint32_t layer, const float *q,
                       const uint32_t *block_tables, const uint32_t *ctx_lens,
                       uint32_t batch, uint32_t max_blocks, uint32_t n_heads,
@@ -270,9 +271,11 @@ int rvkv_attn_prep(rvkv_pool *pool, uint32_t layer, const float *q_in,
  * token-major [batch * q_len, n_heads, head_dim] f32, 16-byte aligned;
  * block_tables [batch, max_blocks] u32; pos_offset, read_num_tokens [batch]
  * u32 (all device). Table entries >= num_blocks mark keys unreadable (they
- * get probability 0); a row that sees no key gets zeros. head_dim in {32,
- * 64, 128, 256}; block_size a power of two >= 8. Computed on the matrix cores in
- * f16 with f32 accumulation. Allocates nothing. */
+ * get probability 0); a row that sees no key gets zeros. With an f16 pool,
+ * head_dim in {32, 64, 128, 256} and block_size a power of two >= 8 it is
+ * computed on the matrix cores in f16 with f32 accumulation; any other
+ * head_dim <= 1024, block size or an f32 pool runs a generic kernel in f32
+ * arithmetic. Allocates nothing. */
 int rvkv_paged_prefill(rvkv_pool *pool, uint32_t layer, const float *q,
                        const uint32_t *block_tables,
                        const uint32_t *pos_offset,
@@ -302,7 +305,7 @@ int rvkv_copy_blocks(rvkv_pool *pool, const uint32_t *src,
 
 /* ---- inspection (test and integration support) --------------------------
  * Logical view of whole blocks: out is device [n, block_size, n_kv_heads,
- * head_dim] f16 for blocks block_ids[0..n) of (layer, which: 0 = K, 1 = V).
+ * head_dim] of the pool's cell type for blocks block_ids[0..n) of (layer, which: 0 = K, 1 = V).
  * The raw-cache view rvllm's tests read (src/cuda/ops.rs:1104-1114). */
 int rvkv_read_blocks(const rvkv_pool *pool, uint32_t layer, uint32_t which,
                      const uint32_t *block_ids, uint32_t n, void *out);

@@ -20,6 +20,7 @@ SOURCES = [
     os.path.join(HERE, "csrc", "rvkv.hip"),
     os.path.join(HERE, "csrc", "prefill.hip"),
     os.path.join(HERE, "csrc", "argmax.hip"),
+    os.path.join(HERE, "csrc", "generic.hip"),
     os.path.join(HERE, "csrc", "block_manager.cpp"),
     os.path.join(HERE, "csrc", "scheduler.cpp"),
 ]

@@ -47,4 +47,15 @@ int mfma_decode(const rvkv_pool *pool, uint32_t layer, const float *q,
                 const void *new_k = nullptr, const void *new_v = nullptr,
                 const uint32_t *new_blk = nullptr,
                 const uint32_t *new_off = nullptr, bool new_f32 = false);
+// Paged attention for shapes the tuned kernels do not take (generic.hip):
+// any head_dim <= 1024, any block size, f16 or f32 cells, f32 arithmetic.
+// pos_offset NULL: decode (one row per sequence at read_num - 1). Keys
+// per sequence are capped at min(ctx_cap, max_blocks * block_size).
+bool generic_head_dim_ok(uint32_t hd);
+int generic_attention(const char *op, const rvkv_pool *pool, uint32_t layer,
+                      const float *q, const uint32_t *tables,
+                      uint32_t max_blocks, const uint32_t *pos_offset,
+                      const uint32_t *read_num, uint32_t batch,
+                      uint32_t q_len, uint32_t n_heads, uint32_t ctx_cap,
+                      float scale, int32_t window, float *out);
 }  // namespace rvkv_detail

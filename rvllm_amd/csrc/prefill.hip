@@ -871,24 +871,24 @@ int rvkv_paged_prefill(rvkv_pool *pool, uint32_t layer, const float *q,
     return fail(RVKV_EINVAL, op,
                 "n_heads must be a positive multiple of n_kv_heads");
   const uint32_t hd = pool->head_dim, bs = pool->block_size;
-  if (pool->f32())
-    return fail(RVKV_EUNSUPPORTED, op, "needs an f16 cache");
-  if (hd != 32 && hd != 64 && hd != 128 && hd != 256)
-    return fail(RVKV_EUNSUPPORTED, op, "head_dim must be 32, 64, 128 or 256");
-  if (bs < 8 || (bs & (bs - 1)) != 0)
-    return fail(RVKV_EUNSUPPORTED, op,
-                "block_size must be a power of two >= 8");
   if ((uintptr_t)q % 16 || (uintptr_t)out % 16)
     return fail(RVKV_EINVAL, op, "q and out must be 16-byte aligned");
-  if ((uint64_t)max_blocks * bs > 0x80000000ull)
-    return fail(RVKV_EUNSUPPORTED, op, "max_blocks * block_size too large");
-  if (pool->block_elems * 2 >= 0x100000000ull)
-    return fail(RVKV_EUNSUPPORTED, op, "one block of all heads is >= 4 GiB");
+  if (!(scale > 0.f) || !std::isfinite(scale))
+    return fail(RVKV_EINVAL, op, "scale must be positive and finite");
+  // The matrix-core kernel takes f16 cells, head_dim 32/64/128/256 and
+  // power-of-two blocks of >= 8 tokens; every other shape (and an f32
+  // cache) runs the generic kernel.
+  if (pool->f32() || (hd != 32 && hd != 64 && hd != 128 && hd != 256) ||
+      bs < 8 || (bs & (bs - 1)) != 0 ||
+      (uint64_t)max_blocks * bs > 0x80000000ull ||
+      pool->block_elems * 2 >= 0x100000000ull)
+    return rvkv_detail::generic_attention(
+        op, pool, layer, q, block_tables, max_blocks, pos_offset,
+        read_num_tokens, batch, q_len, n_heads, 0xFFFFFFFFu, scale, window,
+        out);
   const uint64_t rows = (uint64_t)(n_heads / pool->n_kv) * q_len;
   if (rows > 0x7fffffffull)
     return fail(RVKV_EUNSUPPORTED, op, "q_len too large for one launch");
-  if (!(scale > 0.f) || !std::isfinite(scale))
-    return fail(RVKV_EINVAL, op, "scale must be positive and finite");
 
   PrefillArgs a{};
   a.q = q;

@@ -465,6 +465,8 @@ struct DecodeArgs {
   // Host-side launch hint (not read by the kernels): average context
   // tokens per workgroup.
   uint32_t avg_tokens;
+  // Host-side: the shape runs the generic kernel (generic.hip).
+  uint32_t generic;
 };
 
 constexpr uint32_t kNoSlot = 0xFFFFFFFFu;
@@ -1494,9 +1496,23 @@ struct WsLayout {
   uint32_t n_parts;
 };
 
+// Shapes the tuned decode kernels take: head_dim up to 256 (run at 32, 64,
+// 128 or 256, rounded up; an f32 cache needs it exact) and power-of-two
+// blocks of at least 512 / that many tokens. Every other shape runs the
+// generic kernel.
+bool decode_tuned(const rvkv_pool *p) {
+  const uint32_t hdp = decode_hd(p->head_dim), bs = p->block_size;
+  if (hdp == 0 || (p->f32() && hdp != p->head_dim)) return false;
+  return (bs & (bs - 1)) == 0 && bs >= 512 / hdp;
+}
+
 WsLayout ws_layout(const rvkv_pool *p, uint32_t batch, uint32_t n_heads,
                    uint32_t max_ctx) {
   WsLayout w{};
+  if (!decode_tuned(p)) {  // the generic kernel needs no workspace
+    w.n_parts = 1;
+    return w;
+  }
   const uint32_t P = partition_tokens(p, batch, n_heads, max_ctx);
   w.n_parts = div_up(max_ctx ? max_ctx : 1, P);
   if (w.n_parts <= 1) return w;  // direct write, no workspace
@@ -1772,17 +1788,10 @@ int prepare_decode(const char *op, const rvkv_pool *pool, uint32_t layer,
   if (n_heads == 0 || n_heads % pool->n_kv != 0)
     return fail(RVKV_EINVAL, op,
                 "n_heads must be a positive multiple of n_kv_heads");
-  const uint32_t hdp = decode_hd(pool->head_dim);
-  if (hdp == 0)
-    return fail(RVKV_EUNSUPPORTED, op, "head_dim must be at most 256");
-  if (pool->f32() && hdp != pool->head_dim)
-    return fail(RVKV_EUNSUPPORTED, op,
-                "an f32 cache needs head_dim 32, 64, 128 or 256");
+  const bool generic = !decode_tuned(pool);
+  if (generic && !rvkv_detail::generic_head_dim_ok(pool->head_dim))
+    return fail(RVKV_EUNSUPPORTED, op, "head_dim must be at most 1024");
   const uint32_t bs = pool->block_size;
-  if ((bs & (bs - 1)) != 0 || bs < 512 / hdp)
-    return fail(RVKV_EUNSUPPORTED, op,
-                "block_size must be a power of two >= 512 / head_dim "
-                "(head_dim rounded up to 32, 64, 128 or 256)");
   if (!q || !block_tables || !ctx_lens || !out)
     return fail(RVKV_EINVAL, op, "NULL q/block_tables/ctx_lens/out");
   if ((uintptr_t)q % 16 || (uintptr_t)out % 16)
@@ -1816,7 +1825,16 @@ int prepare_decode(const char *op, const rvkv_pool *pool, uint32_t layer,
   a->ctx_cap = (uint32_t)(cap64 < max_ctx_len ? cap64 : max_ctx_len);
   a->qscale = scale * 1.4426950408889634f;  // log2(e)
   a->window = window;
+  a->generic = generic ? 1u : 0u;
   return RVKV_OK;
+}
+
+// The generic kernel over the decode's arguments (one row per sequence).
+int decode_generic(const char *op, const rvkv_pool *pool, uint32_t layer,
+                   const DecodeArgs &a, uint32_t batch, float scale) {
+  return rvkv_detail::generic_attention(
+      op, pool, layer, a.q, a.tables, a.max_blocks, nullptr, a.ctx_lens,
+      batch, 1, a.n_heads, a.ctx_cap, scale, a.window, a.out);
 }
 
 int check_ws(const char *op, void *ws, size_t ws_bytes, size_t need) {
@@ -2055,7 +2073,9 @@ int plan_build(rvkv_decode_plan *pl, const uint32_t *ctx_lens_host,
   const size_t ent = (size_t)slots * pl->n_heads;
   pl->acc_off = 0;
   pl->ml_off = (ent * decode_hd(pool->head_dim) * 4 + 255) & ~(size_t)255;
-  pl->ws_bytes = slots ? pl->ml_off + ((ent * 2 * 4 + 255) & ~(size_t)255) : 0;
+  pl->ws_bytes = slots && decode_tuned(pool)
+                     ? pl->ml_off + ((ent * 2 * 4 + 255) & ~(size_t)255)
+                     : 0;
   return RVKV_OK;
 }
 
@@ -2162,6 +2182,7 @@ int paged_decode_ws(const char *op, const rvkv_pool *pool, uint32_t layer,
                           out, &a, &gt);
   if (rc) return rc;
   if (batch > 65535) return fail(RVKV_EUNSUPPORTED, op, "batch too large");
+  if (a.generic) return decode_generic(op, pool, layer, a, batch, scale);
   if (max_ctx_len == 0) max_ctx_len = 1;
   const WsLayout w = ws_layout(pool, batch, n_heads, max_ctx_len);
   if (no_alloc && w.bytes > 0) {
@@ -2267,6 +2288,7 @@ int rvkv_paged_decode_planned(const rvkv_pool *pool,
                           max_blocks, plan->n_heads, plan->max_ctx, scale,
                           plan->window, out, &a, &gt);
   if (rc) return rc;
+  if (a.generic) return decode_generic(op, pool, layer, a, plan->batch, scale);
   if ((rc = check_ws(op, ws, ws_bytes, plan->ws_bytes))) return rc;
   a.ws_acc = plan->n_slots ? (float *)((char *)ws + plan->acc_off) : nullptr;
   a.ws_ml = plan->n_slots ? (float *)((char *)ws + plan->ml_off) : nullptr;
@@ -2312,11 +2334,21 @@ int rvkv_decode_step(rvkv_pool *pool, const rvkv_decode_plan *plan,
                           plan ? plan->max_ctx : max_ctx_len, scale, window,
                           out, &a, &gt);
   if (rc) return rc;
-  if (pool->f32()) {
-    // f32 cache: the append and the decode as two launches on the stream.
+  if (pool->f32() || a.generic) {
+    // f32 cache or the generic kernel: the append and the decode as two
+    // launches on the stream.
     if ((rc = rvkv_append(pool, layer, k, v, src_dtype, slot_block, slot_off,
                           batch)))
       return rc;
+    if (a.generic) {
+      if (plan) {
+        if (plan->n_kv != pool->n_kv || plan->head_dim != pool->head_dim)
+          return fail(RVKV_EINVAL, op, "plan was built for another pool shape");
+      } else if (batch > 65535) {
+        return fail(RVKV_EUNSUPPORTED, op, "batch too large");
+      }
+      return decode_generic(op, pool, layer, a, batch, scale);
+    }
   } else {
     a.new_k = k;
     a.new_v = v;

@@ -309,14 +309,6 @@ def test_decode_metal_cases(golden, case):
         assert np.abs(out - exp).max() < ATOL
 
 
-def test_decode_unsupported_head_dims_raise():
-    for hd in (264, 512):
-        st = HipKvStorage(1, 4, 16, 1, hd)
-        q = torch.zeros(1, 2, hd, device="cuda")
-        with pytest.raises(RvkvError, match="paged_decode: head_dim"):
-            st.paged_decode(0, q, dev_u32([[0]]), dev_u32([4]), 4)
-
-
 @pytest.mark.parametrize("hd,G", [(6, 2), (40, 3), (80, 4), (96, 1),
                                   (200, 2), (136, 8)])
 def test_decode_any_head_dim(hd, G):
@@ -1106,10 +1098,11 @@ def test_attn_prep_then_decode_end_to_end(hd, H, KV):
 
 
 # ---- paged prefill / chunked-prefill attention -------------------------
-@pytest.mark.parametrize("case", [0, 1, 2, 4])
+@pytest.mark.parametrize("case", range(len(METAL_CASES)))
 def test_prefill_metal_cases(golden, case):
     """The attn_decode cases of src/metal/ops.rs:676-766 with their own
-    q_len (1, 1, 2, 3) through rvkv_paged_prefill: the Metal mask is
+    q_len (1, 1, 2, 2, 3, 1) through rvkv_paged_prefill (head_dim 6 and 200
+    on the generic kernel): the Metal mask is
     batch_mask with pos_offset = valid - q_len, read_num = valid. Against
     the oracle over the same f16 cache and against the f32-cache golden."""
     c = metal_case_inputs(case)
@@ -1285,14 +1278,6 @@ def test_prefill_edges(hd):
 
 
 def test_prefill_rejections():
-    st = HipKvStorage(1, 4, 16, 1, 48)
-    with pytest.raises(RvkvError, match="paged_prefill: head_dim"):
-        st.paged_prefill(0, torch.zeros(1, 2, 2, 48, device="cuda"),
-                         dev_u32([[0]]), dev_u32([0]), dev_u32([2]))
-    st = HipKvStorage(1, 4, 4, 1, 64)
-    with pytest.raises(RvkvError, match="paged_prefill: block_size"):
-        st.paged_prefill(0, torch.zeros(1, 2, 2, 64, device="cuda"),
-                         dev_u32([[0]]), dev_u32([0]), dev_u32([2]))
     st = HipKvStorage(1, 4, 16, 2, 64)
     with pytest.raises(RvkvError, match="paged_prefill: n_heads"):
         st.paged_prefill(0, torch.zeros(1, 2, 3, 64, device="cuda"),
