@@ -68,9 +68,8 @@ const char *rvkv_last_error(void);
  * offsets throughout. cache_dtype RVKV_F16 (the fast path) or RVKV_F32
  * (the reference's own cell type): an f32 pool supports append (f32 rows
  * copied, f16 rows widened exactly), gather into F32 only, copy_blocks,
- * read_blocks, block_checksums, paged decode and paged prefill; attn_prep
- * returns RVKV_EUNSUPPORTED on it. The pool binds to the current HIP device
- * and to `stream`. */
+ * read_blocks, block_checksums, attn_prep, paged decode and paged prefill.
+ * The pool binds to the current HIP device and to `stream`. */
 int rvkv_pool_create(uint32_t n_layers, uint32_t num_blocks,
                      uint32_t block_size, uint32_t n_kv_heads,
                      uint32_t head_dim, rvkv_dtype cache_dtype,
@@ -248,9 +247,11 @@ int rvkv_decode_step(rvkv_pool *pool, const rvkv_decode_plan *plan,
  * biases [heads*hd] or NULL; cos/sin [rows, hd/2] f32 (rope_cos_sin of each
  * row's position, src/model.rs:224-250, built once per forward).
  * The rotated q goes to q_out [rows, n_heads, hd] f32; k and v are rounded
- * to f16 (nearest-even) and written to (slot_block[i], slot_off[i]) of
- * `layer`, as rvkv_append would. head_dim in {32, 64, 128, 256}; every
- * float buffer 16-byte aligned (RVKV_EINVAL otherwise). Rows whose slot is
+ * to f16 (nearest-even; stored as they are in an f32 pool) and written to
+ * (slot_block[i], slot_off[i]) of `layer`, as rvkv_append would. head_dim
+ * even and <= 1024 (32, 64, 128 and 256 on the tuned kernel, others and f32
+ * pools on a generic one); every float buffer 16-byte aligned (RVKV_EINVAL
+ * otherwise). Rows whose slot is
  * out of range still produce q_out but write no k/v. */
 int rvkv_attn_prep(rvkv_pool *pool, uint32_t layer, const float *q_in,
                    const float *k_in, const float *v_in, uint32_t rows,

@@ -89,7 +89,8 @@ def lib() -> ctypes.CDLL:
         L.orc_rope_apply.argtypes = [P, P, P, u32, u32, P]
         L.orc_attn_prep.restype = ctypes.c_int
         L.orc_attn_prep.argtypes = [P, P, P, u32, u32, u32, u32, P, P, P, P,
-                                    P, f32, P, P, P, P, P, P, u32, u32, P]
+                                    P, f32, P, P, P, P, P, P, ctypes.c_int,
+                                    u32, u32, P]
         _lib = L
     return _lib
 
@@ -337,8 +338,7 @@ def attn_prep(cache: KvCache, q_in, k_in, v_in, cos, sin, slot_block,
               slot_off, q_bias=None, k_bias=None, v_bias=None, q_norm=None,
               k_norm=None, eps=1e-6):
     """The prep segment of Attention::forward (src/model.rs:600-626) plus
-    write_tokens: returns q_out, mutates the f16 cache."""
-    assert cache.dtype == F16
+    write_tokens: returns q_out, mutates the cache (f16 or f32 cells)."""
     q_in, k_in, v_in = _f32(q_in), _f32(k_in), _f32(v_in)
     rows, n_heads, hd = q_in.shape
     n_kv = k_in.shape[1]
@@ -350,7 +350,8 @@ def attn_prep(cache: KvCache, q_in, k_in, v_in, cos, sin, slot_block,
     rc = lib().orc_attn_prep(
         _p(q_in), _p(k_in), _p(v_in), rows, n_heads, n_kv, hd,
         *[None if a is None else _p(a) for a in opt], float(eps), _p(cos),
-        _p(sin), _p(sb), _p(so), _p(cache.k), _p(cache.v), cache.num_blocks,
+        _p(sin), _p(sb), _p(so), _p(cache.k), _p(cache.v), cache.dtype,
+        cache.num_blocks,
         cache.bs, _p(q_out))
     if rc:
         raise ValueError("attn_prep: slot out of range")

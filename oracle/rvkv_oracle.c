@@ -575,15 +575,15 @@ void orc_rope_apply(const float *x, const float *cos_t, const float *sin_t,
 /* The prep segment of Attention::forward (src/model.rs:600-626) for `rows`
  * tokens, then write_tokens of K/V (src/model.rs:628-639): q/k/v inputs are
  * the projection outputs [rows, heads, hd] (bias not yet added); q_out gets
- * the normed + rotated q; the f16 cache (logical layout) gets the normed +
- * rotated k and the biased v at each row's slot. NULL bias/norm = absent. */
+ * the normed + rotated q; the cache (logical layout, f16 or f32 cells)
+ * gets the normed + rotated k and the biased v at each row's slot. NULL bias/norm = absent. */
 int orc_attn_prep(const float *q_in, const float *k_in, const float *v_in,
                   uint32_t rows, uint32_t n_heads, uint32_t n_kv, uint32_t hd,
                   const float *q_bias, const float *k_bias, const float *v_bias,
                   const float *q_norm, const float *k_norm, float eps,
                   const float *cos_t, const float *sin_t,
                   const uint32_t *slot_block, const uint32_t *slot_off,
-                  uint16_t *cache_k, uint16_t *cache_v, uint32_t num_blocks,
+                  void *cache_k, void *cache_v, int dtype, uint32_t num_blocks,
                   uint32_t bs, float *q_out) {
   uint32_t half = hd / 2;
   float *buf = (float *)malloc((size_t)hd * 4 * 2);
@@ -605,7 +605,7 @@ int orc_attn_prep(const float *q_in, const float *k_in, const float *v_in,
           return -1;
         }
         size_t dst = (((size_t)slot_block[r] * bs + slot_off[r]) * n_kv + hh) * hd;
-        for (uint32_t d = 0; d < hd; ++d) cache_v[dst + d] = orc_f32_to_f16(buf[d]);
+        for (uint32_t d = 0; d < hd; ++d) cell_set(cache_v, dtype, dst + d, buf[d]);
         continue;
       }
       const float *w = is_q ? q_norm : k_norm;
@@ -622,7 +622,7 @@ int orc_attn_prep(const float *q_in, const float *k_in, const float *v_in,
           return -1;
         }
         size_t dst = (((size_t)slot_block[r] * bs + slot_off[r]) * n_kv + hh) * hd;
-        for (uint32_t d = 0; d < hd; ++d) cache_k[dst + d] = orc_f32_to_f16(nb[d]);
+        for (uint32_t d = 0; d < hd; ++d) cell_set(cache_k, dtype, dst + d, nb[d]);
       }
     }
   }

@@ -227,6 +227,7 @@ struct PrepArgs {
   uint16_t *kc, *vc;
   uint32_t rows, n_heads, n_kv, num_blocks, bs;
   uint32_t q_stride, kv_stride;  // elements between consecutive input rows
+  uint32_t hd;                   // (read by the generic kernel)
   float eps;
 };
 
@@ -332,6 +333,74 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(PrepArgs a) {
   } else if (slot_ok) {
     st8h(a.kc + dst + j, r0);
     st8h(a.kc + dst + j + HALF, r1);
+  }
+}
+
+// attn_prep for the shapes attn_prep_kernel does not take (an even head_dim
+// other than 32/64/128/256, or f32 cells): one wave per (row, head slot),
+// lane i owning the rotate-half pairs (p, p + hd/2) for p = i, i + 64, ...;
+// the same element arithmetic, the RMS sum reduced over the wave.
+template <typename Cell>
+__global__ void __launch_bounds__(64) attn_prep_generic_kernel(PrepArgs a) {
+#pragma clang fp contract(off)
+  const uint32_t n_slots = a.n_heads + 2 * a.n_kv;
+  const uint32_t item = blockIdx.x;
+  const uint32_t row = item / n_slots;
+  const uint32_t slot = item - row * n_slots;
+  const uint32_t HD = a.hd, HALF = HD / 2;
+  const uint32_t lane = threadIdx.x;
+  const bool is_q = slot < a.n_heads;
+  const bool is_v = slot >= a.n_heads + a.n_kv;
+  const uint32_t hh = is_q ? slot : (is_v ? slot - a.n_heads - a.n_kv
+                                          : slot - a.n_heads);
+  const float *src = is_q ? a.q_in + (size_t)row * a.q_stride + (size_t)hh * HD
+                          : (is_v ? a.v_in : a.k_in) +
+                                (size_t)row * a.kv_stride + (size_t)hh * HD;
+  const float *bias = is_q ? a.q_bias : (is_v ? a.v_bias : a.k_bias);
+  const float *bh = bias ? bias + (size_t)hh * HD : nullptr;
+  const uint32_t blk = a.slot_block[row], off = a.slot_off[row];
+  const bool slot_ok = blk < a.num_blocks && off < a.bs;
+  const size_t dst = (((size_t)blk * a.n_kv + hh) * a.bs + off) * HD;
+  Cell *kc = reinterpret_cast<Cell *>(a.kc);
+  Cell *vc = reinterpret_cast<Cell *>(a.vc);
+  const float *w = is_v ? nullptr : (is_q ? a.q_norm : a.k_norm);
+  float rms = 1.f;
+  if (w) {  // (uniform over the wave)
+    float ss = 0.f;
+    for (uint32_t p = lane; p < HALF; p += 64) {
+      const float x0 = bh ? src[p] + bh[p] : src[p];
+      const float x1 = bh ? src[p + HALF] + bh[p + HALF] : src[p + HALF];
+      ss = ss + (x0 * x0 + x1 * x1);
+    }
+    for (int o = 32; o >= 1; o >>= 1) ss = ss + __shfl_xor(ss, o);
+    rms = sqrtf(ss / (float)HD + a.eps);
+  }
+  for (uint32_t p = lane; p < HALF; p += 64) {
+    float x0 = bh ? src[p] + bh[p] : src[p];
+    float x1 = bh ? src[p + HALF] + bh[p + HALF] : src[p + HALF];
+    if (is_v) {
+      if (slot_ok) {
+        vc[dst + p] = (Cell)x0;
+        vc[dst + p + HALF] = (Cell)x1;
+      }
+      continue;
+    }
+    if (w) {
+      x0 = (x0 / rms) * w[p];
+      x1 = (x1 / rms) * w[p + HALF];
+    }
+    const float c = a.cos_t[(size_t)row * HALF + p];
+    const float sn = a.sin_t[(size_t)row * HALF + p];
+    const float r0 = x0 * c - x1 * sn;
+    const float r1 = x0 * sn + x1 * c;
+    if (is_q) {
+      float *o = a.q_out + ((size_t)row * a.n_heads + hh) * HD;
+      o[p] = r0;
+      o[p + HALF] = r1;
+    } else if (slot_ok) {
+      kc[dst + p] = (Cell)r0;
+      kc[dst + p + HALF] = (Cell)r1;
+    }
   }
 }
 
@@ -2428,6 +2497,7 @@ int attn_prep_impl(rvkv_pool *pool, uint32_t layer, const float *q_in,
   a.bs = pool->block_size;
   a.q_stride = q_stride;
   a.kv_stride = kv_stride;
+  a.hd = hd;
   a.eps = eps;
   for (const void *p : {(const void *)q_in, (const void *)k_in,
                         (const void *)v_in, (const void *)q_bias,
@@ -2440,6 +2510,19 @@ int attn_prep_impl(rvkv_pool *pool, uint32_t layer, const float *q_in,
   const uint64_t items = (uint64_t)rows * (n_heads + 2 * pool->n_kv);
   if (items > 0xffffffffull)
     return fail(RVKV_EUNSUPPORTED, op, "too many rows for one launch");
+  if (pool->f32() || !hd_supported(hd)) {
+    if (items > 0x7fffffffull)
+      return fail(RVKV_EUNSUPPORTED, op, "too many rows for one launch");
+    const dim3 grid((uint32_t)items);
+    if (pool->f32())
+      hipLaunchKernelGGL(attn_prep_generic_kernel<float>, grid, dim3(64), 0,
+                         pool->stream, a);
+    else
+      hipLaunchKernelGGL(attn_prep_generic_kernel<_Float16>, grid, dim3(64),
+                         0, pool->stream, a);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? RVKV_OK : hip_fail(op, e);
+  }
   const uint32_t per_block = 256 / (hd / 16);
   const dim3 grid((uint32_t)((items + per_block - 1) / per_block));
   switch (hd) {
@@ -2464,10 +2547,9 @@ int attn_prep_check(rvkv_pool *pool, uint32_t layer, uint32_t rows,
   if (n_heads == 0 || n_heads % pool->n_kv != 0)
     return fail(RVKV_EINVAL, op,
                 "n_heads must be a positive multiple of n_kv_heads");
-  if (!hd_supported(pool->head_dim))
+  if (pool->head_dim % 2 != 0 || pool->head_dim > 1024)
     return fail(RVKV_EUNSUPPORTED, op,
-                "head_dim must be one of 32, 64, 128, 256");
-  if (pool->f32()) return fail(RVKV_EUNSUPPORTED, op, "needs an f16 cache");
+                "head_dim must be even and at most 1024");
   return 1;
 }
 

@@ -226,9 +226,3 @@ def test_f32_smollm2_config():
                           _bits(ref.v))
 
 
-def test_f32_cache_rejections():
-    st = HipKvStorage(1, 8, 16, 2, 64, dtype=F32)
-    x = torch.zeros(1, 2, 64, device="cuda")
-    cs = torch.zeros(1, 32, device="cuda")
-    with pytest.raises(RvkvError, match="needs an f16 cache"):
-        st.attn_prep(0, x, x, x, cs, cs, dev_u32([0]), dev_u32([0]))

@@ -210,3 +210,72 @@ def test_head_dim_above_1024_raises():
     with pytest.raises(RvkvError, match="paged_prefill: head_dim"):
         st.paged_prefill(0, q.reshape(1, 1, 2, 1040), dev_u32([[0]]),
                          dev_u32([0]), dev_u32([1]))
+
+
+@pytest.mark.parametrize("hd,dtype,bias,norm", [
+    (48, torch.float16, True, True), (96, torch.float16, False, False),
+    (200, torch.float16, True, False), (6, torch.float16, False, True),
+    (64, torch.float32, True, True), (128, torch.float32, False, False),
+    (320, torch.float16, True, True), (512, torch.float32, False, True)])
+def test_generic_attn_prep(hd, dtype, bias, norm):
+    """rvkv_attn_prep on the generic kernel (head_dim other than
+    32/64/128/256, or an f32 pool) against the oracle's restatement of
+    src/model.rs:600-626 over the same cell type: without the RMS norm q and
+    the cache are bit-identical; with it the sum of squares is reduced in
+    another order (q to 2e-6 * (1 + |q|), f16 cells to one ulp, f32 cells to
+    2e-6 * (1 + |x|)). The fused-QKV entry point gives the same bits."""
+    rng = np.random.default_rng(hd + 2 * bias + norm)
+    rows, nb, bs, H, KV = 29, 20, 16, 6, 2
+    q = rng.standard_normal((rows, H, hd)).astype(np.float32)
+    k = rng.standard_normal((rows, KV, hd)).astype(np.float32)
+    v = rng.standard_normal((rows, KV, hd)).astype(np.float32)
+    opt = {}
+    if bias:
+        opt.update(q_bias=rng.standard_normal(H * hd).astype(np.float32),
+                   k_bias=rng.standard_normal(KV * hd).astype(np.float32),
+                   v_bias=rng.standard_normal(KV * hd).astype(np.float32))
+    if norm:
+        opt.update(q_norm=rng.standard_normal(hd).astype(np.float32),
+                   k_norm=rng.standard_normal(hd).astype(np.float32))
+    c, s = orc.rope_cos_sin(1e6, hd, rng.integers(0, 8192, rows))
+    slots = rng.permutation(nb * bs)[:rows]
+    sb, so = slots // bs, slots % bs
+    f32 = dtype == torch.float32
+    cache = orc.KvCache(nb, bs, KV, hd, orc.F32 if f32 else orc.F16)
+    want_q = orc.attn_prep(cache, q, k, v, c, s, sb, so, eps=1e-6, **opt)
+    st = HipKvStorage(1, nb, bs, KV, hd, dtype=dtype)
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    got_q = st.attn_prep(0, T(q), T(k), T(v), T(c), T(s), dev_u32(sb),
+                         dev_u32(so), eps=1e-6,
+                         **{n: T(a) for n, a in opt.items()}).cpu().numpy()
+    ids = dev_u32(np.arange(nb))
+    gk = st.read_blocks(0, 0, ids).cpu().numpy()
+    gv = st.read_blocks(0, 1, ids).cpu().numpy()
+    view = np.uint32 if f32 else np.uint16
+    ck, cv = cache.k.view(view), cache.v.view(view)
+    assert np.array_equal(gv.view(view), cv)  # v: bias + store only
+    if not norm:
+        assert np.array_equal(got_q, want_q)
+        assert np.array_equal(gk.view(view), ck)
+    else:
+        assert np.max(np.abs(got_q - want_q) / (1 + np.abs(want_q))) < 2e-6
+        if f32:
+            assert np.max(np.abs(gk - cache.k) / (1 + np.abs(cache.k))) < 2e-6
+        else:
+            ulp = np.abs(gk.view(np.uint16).astype(np.int32) -
+                         cache.k.astype(np.int32))
+            assert ulp.max() <= 1
+    # the fused [rows, (H + 2 KV) * hd] entry point: same bits
+    st2 = HipKvStorage(1, nb, bs, KV, hd, dtype=dtype)
+    qkv = np.concatenate([q.reshape(rows, -1), k.reshape(rows, -1),
+                          v.reshape(rows, -1)], axis=1)
+    fb = None
+    if bias:
+        fb = T(np.concatenate([opt["q_bias"], opt["k_bias"], opt["v_bias"]]))
+    q2 = st2.attn_prep_qkv(0, T(qkv), H, T(c), T(s), dev_u32(sb), dev_u32(so),
+                           bias=fb, q_norm=T(opt["q_norm"]) if norm else None,
+                           k_norm=T(opt["k_norm"]) if norm else None,
+                           eps=1e-6).cpu().numpy()
+    assert np.array_equal(q2, got_q)
+    assert torch.equal(st2.read_blocks(0, 0, ids), st.read_blocks(0, 0, ids))
+    assert torch.equal(st2.read_blocks(0, 1, ids), st.read_blocks(0, 1, ids))

@@ -1392,29 +1392,23 @@ def test_engine_fork_copy_on_write_on_gpu():
     assert be.calls > 5
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
 @pytest.mark.parametrize("hd,bias_on,qn_on,kn_on", [(64, True, True, True),
                                                     (128, False, False, False),
                                                     (6, True, False, True),
                                                     (2, False, True, False)])
-def test_attn_prep_qkv_metal_cases(hd, bias_on, qn_on, kn_on):
+def test_attn_prep_qkv_metal_cases(hd, bias_on, qn_on, kn_on, dtype):
     """attn_prep_matches_reference (src/metal/ops.rs:771-858) through the
     fused-QKV entry point: 6 q / 2 kv heads, 5 rows, xorshift values (seeds
     40-45), row r to (block r % 3 + 1, offset r % 4), eps 1e-5. The expected
     values are computed as that test computes them (rms in float64, the
     rotate-half in f32); q within its 1e-5, the f16 cache equal to the
-    expected f32 rounded to f16 (one ulp where the norm's sum order shows).
-    Head widths 6 and 2 are not supported here and must be rejected."""
+    expected f32 rounded to f16 (one ulp where the norm's sum order shows);
+    on an f32 pool (the reference's cells) v exactly and k within 1e-5.
+    Head widths 6 and 2 run the generic kernel."""
     from tests.golden.make_golden import values
     H, KV, rows, bs = 6, 2, 5, 4
     width = (H + 2 * KV) * hd
-    if hd % 32:
-        st = HipKvStorage(1, 4, bs, KV, hd)
-        with pytest.raises(RvkvError, match="attn_prep: head_dim"):
-            st.attn_prep_qkv(0, torch.zeros(rows, width, device="cuda"), H,
-                             torch.zeros(rows, hd // 2, device="cuda"),
-                             torch.zeros(rows, hd // 2, device="cuda"),
-                             dev_u32([0] * rows), dev_u32([0] * rows))
-        return
     half, eps = hd // 2, np.float32(1e-5)
     qkv = values(rows * width, 40).reshape(rows, width)
     bias, qn, kn = values(width, 41), values(hd, 42), values(hd, 43)
@@ -1445,7 +1439,7 @@ def test_attn_prep_qkv_metal_cases(hd, bias_on, qn_on, kn_on):
             want_k[blk[r], off[r], h] = rotate(r, head(r, H + h),
                                                kn if kn_on else None)
             want_v[blk[r], off[r], h] = head(r, H + KV + h)
-    st = HipKvStorage(1, 4, bs, KV, hd)
+    st = HipKvStorage(1, 4, bs, KV, hd, dtype=dtype)
     T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
     q = st.attn_prep_qkv(0, T(qkv), H, T(cos), T(sin), dev_u32(blk),
                          dev_u32(off), bias=T(bias) if bias_on else None,
@@ -1453,6 +1447,12 @@ def test_attn_prep_qkv_metal_cases(hd, bias_on, qn_on, kn_on):
                          k_norm=T(kn) if kn_on else None, eps=1e-5)
     assert np.abs(q.cpu().numpy() - want_q).max() < 1e-5
     ids = dev_u32(np.arange(4))
+    if dtype == torch.float32:
+        gk = st.read_blocks(0, 0, ids).cpu().numpy()
+        gv = st.read_blocks(0, 1, ids).cpu().numpy()
+        assert np.array_equal(gv, want_v)
+        assert np.abs(gk - want_k).max() < 1e-5
+        return
     gk, gv = bits(st.read_blocks(0, 0, ids)), bits(st.read_blocks(0, 1, ids))
     assert np.array_equal(gv, orc.f32_to_f16_bits(want_v))
     d = np.abs(gk.astype(np.int32) - orc.f32_to_f16_bits(want_k).astype(

@@ -402,6 +402,13 @@ def test_attn_prep_composes_the_pinned_parts():
             y = v[r, h] + vb[h * hd:(h + 1) * hd]
             assert np.array_equal(cache.v[sb[r], so[r], h],
                                   orc.f32_to_f16_bits(y))
+    # f32 cells (the reference's own): the same q, and cells whose f16
+    # rounding is exactly the f16 cache's
+    c32 = orc.KvCache(nb, bs, KV, hd, orc.F32)
+    qo32 = orc.attn_prep(c32, q, k, v, c, s, sb, so, qb, kb, vb, qn, kn, 1e-6)
+    assert np.array_equal(qo32, qo)
+    assert np.array_equal(orc.f32_to_f16_bits(c32.k), cache.k)
+    assert np.array_equal(orc.f32_to_f16_bits(c32.v), cache.v)
 
 
 # ---- paged prefill / chunked attention ----------------------------------
