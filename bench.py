@@ -45,6 +45,11 @@ def parse():
                    "qwen3, gemma); 0 = the config's own")
     p.add_argument("--no-cpu", action="store_true",
                    help="skip the CPU baseline leg")
+    p.add_argument("--f32-cache", dest="f32_cache", action="store_true",
+                   default=None,
+                   help="f32 cache cells, the reference's own (default for "
+                   "smollm2-360m, whose reference path is f32; else f16)")
+    p.add_argument("--f16-cache", dest="f32_cache", action="store_false")
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="wall-clock budget of the CPU baseline sample")
     p.add_argument("--plan", dest="plan", action="store_true", default=None,
@@ -236,9 +241,9 @@ def sample_batch(W, db, n_seq):
     return sub, np.asarray(ids, np.uint32)
 
 
-def cpu_baseline(orc, W, st, db, budget_s):
+def cpu_baseline(orc, W, st, db, budget_s, f32=False):
     """The oracle's restatement of rvllm's CPU decode path (append + padded
-    gather + batch_mask + gqa_attention, f32 math over the f16 cache) on the
+    gather + batch_mask + gqa_attention, f32 math over the cache) on the
     host cores: layer 0 of a bounded sample of the same workload (its first
     sequences, the cache blocks they read copied from the GPU pool),
     repeated within budget_s, on every core this process may run on, and a
@@ -249,7 +254,8 @@ def cpu_baseline(orc, W, st, db, budget_s):
     threads = len(os.sched_getaffinity(0))
     # About 1 s of multi-threaded work per repetition at ~10 GB/s; the
     # single-thread leg uses an eighth of that sample.
-    full_bytes = W.decode_bytes(db)
+    cell = 4 if f32 else 2
+    full_bytes = W.decode_bytes(db, cell)
     n_seq = db.batch
     while n_seq > 1 and full_bytes * n_seq / db.batch > 2e9:
         n_seq //= 2
@@ -258,12 +264,14 @@ def cpu_baseline(orc, W, st, db, budget_s):
     def prepare(n):
         sub, ids = sample_batch(W, db, n)
         cache = orc.KvCache(sub.num_blocks, c.block_size, c.n_kv_heads,
-                            c.head_dim, orc.F16)
+                            c.head_dim, orc.F32 if f32 else orc.F16)
         dev_ids = torch.from_numpy(ids.view(np.int32)).cuda()
-        cache.k[:] = st.read_blocks(0, 0, dev_ids).cpu().view(torch.int16) \
-            .numpy().view(np.uint16)
-        cache.v[:] = st.read_blocks(0, 1, dev_ids).cpu().view(torch.int16) \
-            .numpy().view(np.uint16)
+        for which, dst in ((0, cache.k), (1, cache.v)):
+            blocks = st.read_blocks(0, which, dev_ids).cpu()
+            if f32:
+                dst[:] = blocks.numpy()
+            else:
+                dst[:] = blocks.view(torch.int16).numpy().view(np.uint16)
         rng = W.Rng(c.seed + 99)
         nk = rng.normal((n, c.n_kv_heads, c.head_dim))
         nv = rng.normal((n, c.n_kv_heads, c.head_dim))
@@ -283,15 +291,18 @@ def cpu_baseline(orc, W, st, db, budget_s):
 
     sub, cache, nk, nv, q = prepare(n_seq)
     per_rep, reps = timed(sub, cache, nk, nv, q, threads, budget_s, 1000)
-    sub_bytes = W.decode_bytes(sub) + W.append_bytes(sub.batch, c)
+    sub_bytes = (W.decode_bytes(sub, cell) +
+                 W.append_bytes(sub.batch, c, cell_bytes=cell))
     gbs = sub_bytes / per_rep / 1e9
     n1 = max(1, n_seq // 8)
     sub1, cache1, nk1, nv1, q1 = prepare(n1)
     per_rep1, reps1 = timed(sub1, cache1, nk1, nv1, q1, 1,
                             min(3.0, budget_s / 4), 100)
-    sub1_bytes = W.decode_bytes(sub1) + W.append_bytes(sub1.batch, c)
+    sub1_bytes = (W.decode_bytes(sub1, cell) +
+                  W.append_bytes(sub1.batch, c, cell_bytes=cell))
     # Whole batch, all layers, at the sample's rate.
-    layer_bytes = W.decode_bytes(db) + W.append_bytes(db.batch, c)
+    layer_bytes = (W.decode_bytes(db, cell) +
+                   W.append_bytes(db.batch, c, cell_bytes=cell))
     layer_s = layer_bytes / (gbs * 1e9)
     return {
         "value": round(gbs, 3),
@@ -301,7 +312,9 @@ def cpu_baseline(orc, W, st, db, budget_s):
         "kind": "port",
         "sample": (f"oracle decode_step (rvllm CPU path restated in C: "
                    f"write_tokens + padded gather + batch_mask + "
-                   f"gqa_attention, f32) on layer 0 of the first {n_seq} of "
+                   f"gqa_attention, f32 math over "
+                   f"{'f32' if f32 else 'f16'} cells) on layer 0 of the "
+                   f"first {n_seq} of "
                    f"{db.batch} sequences of the same workload, "
                    f"{reps} repetitions of {per_rep * 1e3:.1f} ms on "
                    f"{threads} threads; tok/s extrapolated to {db.batch} "
@@ -923,8 +936,12 @@ def main():
         return
     db = build_workload(W, args.config, args.batch, args.ctx)
     c = db.cfg
+    f32 = (args.f32_cache if args.f32_cache is not None
+           else c.name == "smollm2-360m")
+    cell = 4 if f32 else 2
     st = HipKvStorage(c.n_layers, db.num_blocks, c.block_size, c.n_kv_heads,
-                      c.head_dim)
+                      c.head_dim,
+                      dtype=torch.float32 if f32 else torch.float16)
     fill_pool(torch, st, c.seed, c.value_scale)
 
     def u32(a):
@@ -1045,12 +1062,13 @@ def main():
     torch.cuda.synchronize()
     dec_ms = e0.elapsed_time(e1) / (args.steps * L)
 
-    traffic = measured_traffic(args.config, args.batch, args.unfused,
-                               args.ctx)
-    app_bytes = W.append_bytes(B, c)
-    # The fused launch also moves the appended rows (f32 in, f16 out).
-    dec_bytes = W.decode_bytes(db) + (0 if args.unfused else app_bytes)
-    step_bytes = L * (W.decode_bytes(db) + app_bytes)
+    traffic = None if f32 else measured_traffic(args.config, args.batch,
+                                                args.unfused, args.ctx)
+    app_bytes = W.append_bytes(B, c, cell_bytes=cell)
+    # The fused launch also moves the appended rows (f32 in, f16 out; an f32
+    # pool runs the append and the decode as two launches, timed together).
+    dec_bytes = W.decode_bytes(db, cell) + (0 if args.unfused else app_bytes)
+    step_bytes = L * (W.decode_bytes(db, cell) + app_bytes)
     achieved = dec_bytes / (dec_ms * 1e-3) / 1e9
     res = {
         "metric": METRIC,
@@ -1064,9 +1082,9 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16 KV, f32 accumulate",
-        "data": "synthetic: K/V ~ N(0,1)*scale f16, q ~ N(0,1) f32, seeded "
-                "random-permutation block tables",
+        "dtype": "f32 KV, f32 math" if f32 else "f16 KV, f32 accumulate",
+        "data": "synthetic: K/V ~ N(0,1)*scale (f16 values), q ~ N(0,1) "
+                "f32, seeded random-permutation block tables",
         "config": {
             "workload": f"{c.name}: {c.description.split(',')[0]}"
                         f"{'' if not (args.batch or args.ctx) else ' (resized)'}; "
@@ -1101,7 +1119,8 @@ def main():
     res["roofline"]["stream_read_ceiling"] = rc
     if not args.no_cpu:
         from oracle import oracle as orc
-        res["cpu_baseline"] = cpu_baseline(orc, W, st, db, args.cpu_seconds)
+        res["cpu_baseline"] = cpu_baseline(orc, W, st, db, args.cpu_seconds,
+                                             f32=f32)
     print(json.dumps(res), flush=True)
     st.close()
 

@@ -270,21 +270,24 @@ def qwen25_batch(batch: Optional[int] = None, seed: Optional[int] = None,
     return db
 
 
-def decode_bytes(db: DecodeBatch) -> int:
+def decode_bytes(db: DecodeBatch, cell_bytes: int = 2) -> int:
     """Algorithmic HBM bytes of one paged-decode launch (one layer): unique
-    K+V bytes read (f16) + q and out (f32) + block tables + ctx_lens."""
+    K+V bytes read (cell_bytes per element: 2 for f16, 4 for f32) + q and
+    out (f32) + block tables + ctx_lens."""
     c = db.cfg
-    kv = db.unique_kv_tokens() * c.n_kv_heads * c.head_dim * 2 * 2
+    kv = db.unique_kv_tokens() * c.n_kv_heads * c.head_dim * 2 * cell_bytes
     qo = db.batch * c.n_heads * c.head_dim * 4 * 2
     tables = 4 * sum(-(-int(n) // c.block_size) for n in db.ctx_lens)
     return kv + qo + tables + 4 * db.batch
 
 
-def append_bytes(n_tokens: int, cfg: Config, src_bytes: int = 4) -> int:
+def append_bytes(n_tokens: int, cfg: Config, src_bytes: int = 4,
+                 cell_bytes: int = 2) -> int:
     """Algorithmic bytes of one append launch: K+V rows read at src_bytes
-    per element, written as f16, plus 8 bytes of slot per token."""
-    return (n_tokens * cfg.n_kv_heads * cfg.head_dim * 2 * (src_bytes + 2)
-            + 8 * n_tokens)
+    per element, written at cell_bytes (f16: 2, f32: 4), plus 8 bytes of
+    slot per token."""
+    return (n_tokens * cfg.n_kv_heads * cfg.head_dim * 2 *
+            (src_bytes + cell_bytes) + 8 * n_tokens)
 
 
 def prep_bytes(n_tokens: int, cfg: Config) -> int:
