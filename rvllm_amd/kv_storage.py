@@ -136,8 +136,9 @@ class HipDecodePlan:
 class HipKvStorage:
     """CudaKvStorage (src/cuda/kv_storage.rs:65-164) on MI355X: one zeroed
     pool for all layers' K and V, owned by librvkv. Cells are f16 (the
-    default) or, with dtype=torch.float32, f32 like rvllm's own cache (append,
-    gather, copy and decode; prefill attention and attn_prep need f16)."""
+    default) or, with dtype=torch.float32, f32 like rvllm's own cache (every
+    operation; attention and attn_prep on an f32 pool run the generic
+    kernels)."""
 
     def __init__(self, n_layers: int, num_blocks: int, block_size: int,
                  n_kv_heads: int, head_dim: int, stream=None,
