@@ -59,6 +59,35 @@ def test_noalloc_decode_matches_workspace_decode():
         assert torch.equal(got, want), (i, (got - want).abs().max().item())
 
 
+@pytest.mark.parametrize("hd,bs,dtype", [(128, 16, torch.float32),
+                                          (96, 12, torch.float16)])
+def test_noalloc_decode_other_pools(hd, bs, dtype):
+    """An f32 pool (the f32 decode kernel, its partials in the scratch
+    array) and a shape on the generic kernel (no partials): bit-identical to
+    rvkv_paged_decode, two calls in a row, the second smaller."""
+    print(f"\n[gpu] noalloc other pools hd={hd} bs={bs} {dtype}", flush=True)
+    nkv, H = 2, 6
+    st = HipKvStorage(1, 1200, bs, nkv, hd, dtype=dtype)
+    g = torch.Generator(device="cuda").manual_seed(hd)
+    n = 1200 * bs
+    slots = torch.arange(n, device="cuda")
+    k = torch.randn((n, nkv, hd), generator=g, device="cuda")
+    st.write_tokens(0, (slots // bs).int(), (slots % bs).int(), k, k * 0.5)
+    for i, lens in enumerate([np.array([5000, 17, 900, 3], np.uint32),
+                              np.array([700, 40], np.uint32)]):
+        cfg = W.Config("na2", 9, 1, H, nkv, hd, bs, len(lens))
+        db = W.ragged_batch(cfg, lens, seed=i)
+        assert db.num_blocks <= 1200
+        max_ctx = int(lens.max())
+        tables, ctx = dev_u32(db.padded_tables()), dev_u32(lens)
+        q = torch.randn(len(lens), H, hd, device="cuda", generator=g)
+        want = st.paged_decode(0, q, tables, ctx, max_ctx)
+        got = _noalloc(st, q, tables, ctx, max_ctx)
+        torch.cuda.synchronize()
+        assert torch.isfinite(got).all()
+        assert torch.equal(got, want), (i, (got - want).abs().max().item())
+
+
 def test_noalloc_decode_rejects_oversized_partials():
     """A shape whose partials need more than the 8 MiB array (head_dim 256,
     8 query heads per KV head, 511 sequences split in two) is refused
