@@ -1131,7 +1131,10 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
     }
     if (slot == kNoSlot) {
       float *o = a.out + ((size_t)b * a.n_heads + h0 + g) * hdr + d;
-      const float y[4] = {x.x / L, x.y / L, x.z / L, x.w / L};
+      // (L is 0 only if every key in range sat behind an unreadable block
+      // id: zeros, as for a sequence with nothing to attend to.)
+      const float y[4] = {L > 0.f ? x.x / L : 0.f, L > 0.f ? x.y / L : 0.f,
+                          L > 0.f ? x.z / L : 0.f, L > 0.f ? x.w / L : 0.f};
       if (!RAGGED) {
         *reinterpret_cast<float4 *>(o) = make_float4(y[0], y[1], y[2], y[3]);
       } else {

@@ -376,6 +376,35 @@ def test_decode_edge_cases():
     assert torch.equal(out2[:7], out[:7])
 
 
+@pytest.mark.parametrize("hd,G", [(64, 4), (128, 2), (256, 4)])
+def test_decode_all_blocks_unreadable_gives_zeros(hd, G):
+    """Every table entry of one sequence past the pool: nothing readable to
+    attend to, so its output rows are zeros (not 0/0), through the uniform
+    and the planned path; the other sequences are unaffected."""
+    from rvllm_amd.kv_storage import HipDecodePlan
+    bs, nkv = 16, 2
+    lens = np.array([40, 700, 2100], np.uint32)
+    cfg = W.Config("unr", 9, 1, G * nkv, nkv, hd, bs, len(lens))
+    db = W.ragged_batch(cfg, lens, seed=hd)
+    st = HipKvStorage(1, db.num_blocks, bs, nkv, hd)
+    fill_layer(st, 0, seed=hd + 1)
+    q = torch.randn(len(lens), G * nkv, hd, device="cuda")
+    good = st.paged_decode(0, q, dev_u32(db.padded_tables()), dev_u32(lens),
+                           int(lens.max()))
+    for victim in (0, 2):
+        bad = db.padded_tables()
+        bad[victim, :] = 3_000_000_000
+        out = st.paged_decode(0, q, dev_u32(bad), dev_u32(lens),
+                              int(lens.max()))
+        plan = HipDecodePlan(st, lens, G * nkv)
+        outp = st.paged_decode_planned(0, plan, q, dev_u32(bad),
+                                       dev_u32(lens))
+        for o in (out, outp):
+            assert o[victim].eq(0).all()
+            others = [i for i in range(len(lens)) if i != victim]
+            assert torch.allclose(o[others], good[others], atol=ATOL, rtol=0)
+
+
 @pytest.mark.parametrize("max_ctx", [300, 5000])
 def test_decode_multi_partition_and_window(max_ctx):
     """Partition split + reduction pass (several partitions) and the
