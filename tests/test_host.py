@@ -237,3 +237,16 @@ def test_bench_cpu_sample_keeps_the_batch_shape():
     assert sub.unique_kv_tokens() == W.DecodeBatch(
         db.cfg, db.num_blocks, db.ctx_lens[:20], db.tables[:20],
         db.slot_block[:20], db.slot_off[:20]).unique_kv_tokens()
+
+
+def test_integration_sys_listing_matches_the_header():
+    """The Rust -sys listing a maintainer would copy declares exactly the
+    functions of include/rvkv.h, no more and no fewer."""
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    header = open(os.path.join(root, "include", "rvkv.h")).read()
+    header = re.sub(r"/\*.*?\*/", "", header, flags=re.S)
+    declared = set(re.findall(r"\b(rvkv_[a-z0-9_]+)\s*\(", header))
+    listing = open(os.path.join(root, "INTEGRATION.md")).read()
+    bound = set(re.findall(r"pub fn (rvkv_[a-z0-9_]+)", listing))
+    assert bound == declared, (sorted(bound - declared),
+                               sorted(declared - bound))
