@@ -52,6 +52,15 @@ __device__ __forceinline__ uint32_t as_u32(h2 x) {
   return __builtin_bit_cast(uint32_t, x);
 }
 
+// 16-byte load with the non-temporal hint: for K/V bytes a decode reads
+// once (a plain streaming read of a decode launch's size runs ~5 % faster
+// with it on this part).
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 load_nt16(const void *p) {
+  const u32x4v x = __builtin_nontemporal_load(static_cast<const u32x4v *>(p));
+  return make_uint4(x[0], x[1], x[2], x[3]);
+}
+
 }  // namespace
 
 
@@ -959,8 +968,8 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
             kr[u][j] = load_row8(kp + j * R * 16, (j * R + c) * 8, hdr);
             vr[u][j] = load_row8(vp + j * R * 16, (j * R + c) * 8, hdr);
           } else {
-            kr[u][j] = *reinterpret_cast<const uint4 *>(kp + j * R * 16);
-            vr[u][j] = *reinterpret_cast<const uint4 *>(vp + j * R * 16);
+            kr[u][j] = load_nt16(kp + j * R * 16);
+            vr[u][j] = load_nt16(vp + j * R * 16);
           }
         }
       }
@@ -1256,8 +1265,12 @@ __global__ void __launch_bounds__(256) decode_f32_kernel(DecodeArgs a) {
       const char *vp = valid[u] ? row - kbase + vbase : zero_v;
 #pragma unroll
       for (int j = 0; j < NL; ++j) {
-        kr[u][j] = *reinterpret_cast<const float4 *>(kp + j * R * 16);
-        vr[u][j] = *reinterpret_cast<const float4 *>(vp + j * R * 16);
+        const uint4 kb = load_nt16(kp + j * R * 16);
+        const uint4 vb = load_nt16(vp + j * R * 16);
+        kr[u][j] = make_float4(__uint_as_float(kb.x), __uint_as_float(kb.y),
+                               __uint_as_float(kb.z), __uint_as_float(kb.w));
+        vr[u][j] = make_float4(__uint_as_float(vb.x), __uint_as_float(vb.y),
+                               __uint_as_float(vb.z), __uint_as_float(vb.w));
       }
     }
 #pragma unroll
