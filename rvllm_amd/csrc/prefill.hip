@@ -52,6 +52,17 @@ namespace {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// A 16-byte K/V load; NT: with the non-temporal hint, for bytes read once
+// (the decode mode), where it reads ~5 % faster; prefill tiles are re-read
+// by a head's other query tiles through the L2 and load normally.
+template <bool NT>
+__device__ __forceinline__ u32x4 ld16(const char *p) {
+  if constexpr (NT)
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+  else
+    return *reinterpret_cast<const u32x4 *>(p);
+}
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef short v4s __attribute__((ext_vector_type(4)));
@@ -453,9 +464,9 @@ __global__ void __launch_bounds__(
 #pragma unroll
       for (int i = 0; i < CHK; ++i) {
         const uint64_t off = (uint64_t)kid[i] * blk_bytes + (t_off + k_off[i]);
-        kr[si][i] = *reinterpret_cast<const u32x4 *>(kbase + off);
+        kr[si][i] = ld16<WAVES == 1>(kbase + off);
         if constexpr (TRV)
-          vr[si][i] = *reinterpret_cast<const u32x4 *>(vbase + off);
+          vr[si][i] = ld16<WAVES == 1>(vbase + off);
       }
       if constexpr (!TRV) {
         if (v_lane) {
@@ -463,8 +474,8 @@ __global__ void __launch_bounds__(
           for (int j = 0; j < CHV; ++j) {
             const char *vp =
                 vbase + (uint64_t)vid[j] * blk_bytes + (t_off + v_off[j]);
-            vr0[si][j] = *reinterpret_cast<const u32x4 *>(vp);
-            vr1[si][j] = *reinterpret_cast<const u32x4 *>(vp + HD * 2);
+            vr0[si][j] = ld16<WAVES == 1>(vp);
+            vr1[si][j] = ld16<WAVES == 1>(vp + HD * 2);
           }
         }
       }
@@ -480,9 +491,9 @@ __global__ void __launch_bounds__(
       kbits[si] |= (uint32_t)(okb && kt + k_key[i] < k_end) << i;
       const uint64_t off =
           (uint64_t)(okb ? kid[i] : 0u) * blk_bytes + (t_off + k_off[i]);
-      kr[si][i] = *reinterpret_cast<const u32x4 *>(kbase + off);
+      kr[si][i] = ld16<WAVES == 1>(kbase + off);
       if constexpr (TRV)
-        vr[si][i] = *reinterpret_cast<const u32x4 *>(vbase + off);
+        vr[si][i] = ld16<WAVES == 1>(vbase + off);
     }
     if constexpr (!TRV) {
 #pragma unroll
@@ -494,8 +505,8 @@ __global__ void __launch_bounds__(
         const char *vp = vbase + (uint64_t)(okb ? vid[j] : 0u) * blk_bytes +
                          (t_off + v_off[j]);
         if (v_lane) {
-          vr0[si][j] = *reinterpret_cast<const u32x4 *>(vp);
-          vr1[si][j] = *reinterpret_cast<const u32x4 *>(vp + HD * 2);
+          vr0[si][j] = ld16<WAVES == 1>(vp);
+          vr1[si][j] = ld16<WAVES == 1>(vp + HD * 2);
         }
       }
     }
