@@ -127,7 +127,8 @@ def copy_calibration(torch, steps):
 
 def read_ceiling(torch, nbytes, steps):
     """The plain streaming-read rate at one launch's size: the read probe
-    (16-byte loads, 2048 contiguous slices, nothing written) timed with HIP
+    (16-byte non-temporal loads, 16384 contiguous slices, nothing written)
+    timed with HIP
     events over buffers of `nbytes`, rotated so at least 1.5 GiB separates
     two reads of one buffer (no MALL reuse, as for the layer launches)."""
     import ctypes

@@ -52,13 +52,29 @@ __device__ __forceinline__ uint32_t as_u32(h2 x) {
   return __builtin_bit_cast(uint32_t, x);
 }
 
-// 16-byte load with the non-temporal hint: for K/V bytes a decode reads
-// once (a plain streaming read of a decode launch's size runs ~5 % faster
-// with it on this part).
+// 16-byte loads and stores with the non-temporal hint, for bytes that are
+// read or written once (K/V streamed by a decode, rows moved by an append,
+// a gather or a copy): on this part a plain streaming read of a decode
+// launch's size runs ~5 % faster with it, a copy ~6 %. Stores use it only
+// where a wave writes whole contiguous runs (attn_prep and the f32 gather,
+// whose lanes write two separate halves, measured slower with it).
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+typedef float f32x4v __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 load_nt16(const void *p) {
   const u32x4v x = __builtin_nontemporal_load(static_cast<const u32x4v *>(p));
   return make_uint4(x[0], x[1], x[2], x[3]);
+}
+__device__ __forceinline__ float4 load_nt16f(const void *p) {
+  const f32x4v x = __builtin_nontemporal_load(static_cast<const f32x4v *>(p));
+  return make_float4(x[0], x[1], x[2], x[3]);
+}
+__device__ __forceinline__ void store_nt16(void *p, uint4 v) {
+  __builtin_nontemporal_store(u32x4v{v.x, v.y, v.z, v.w},
+                              static_cast<u32x4v *>(p));
+}
+__device__ __forceinline__ void store_nt16f(void *p, float4 v) {
+  __builtin_nontemporal_store(f32x4v{v.x, v.y, v.z, v.w},
+                              static_cast<f32x4v *>(p));
 }
 
 }  // namespace
@@ -98,7 +114,8 @@ __global__ void __launch_bounds__(256)
           static_cast<const float *>(k) + src);
       const float4 *vs = reinterpret_cast<const float4 *>(
           static_cast<const float *>(v) + src);
-      float4 k0 = ks[0], k1 = ks[1], v0 = vs[0], v1 = vs[1];
+      const float4 k0 = load_nt16f(ks), k1 = load_nt16f(ks + 1);
+      const float4 v0 = load_nt16f(vs), v1 = load_nt16f(vs + 1);
       // f32 -> f16 round-to-nearest-even (v_cvt_f16_f32, default mode).
       ko.x = as_u32(h2{(_Float16)k0.x, (_Float16)k0.y});
       ko.y = as_u32(h2{(_Float16)k0.z, (_Float16)k0.w});
@@ -109,13 +126,11 @@ __global__ void __launch_bounds__(256)
       vo.z = as_u32(h2{(_Float16)v1.x, (_Float16)v1.y});
       vo.w = as_u32(h2{(_Float16)v1.z, (_Float16)v1.w});
     } else {
-      ko = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(k) +
-                                            src);
-      vo = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(v) +
-                                            src);
+      ko = load_nt16(static_cast<const uint16_t *>(k) + src);
+      vo = load_nt16(static_cast<const uint16_t *>(v) + src);
     }
-    *reinterpret_cast<uint4 *>(kc + dst) = ko;
-    *reinterpret_cast<uint4 *>(vc + dst) = vo;
+    store_nt16(kc + dst, ko);
+    store_nt16(vc + dst, vo);
   } else {
     if constexpr (SRC_F32) {
       kc[dst] = __builtin_bit_cast(
@@ -179,6 +194,8 @@ __global__ void __launch_bounds__(256)
   const size_t src =
       (((size_t)(ok_blk ? blk : 0) * n_kv + head) * bs + pos % bs) * hd + d;
   if constexpr (VW == 8) {
+    // (plain loads: the padded layout re-reads a sequence's last block for
+    // every padding position, and those re-reads hit in L2)
     uint4 kr = ok_blk ? *reinterpret_cast<const uint4 *>(kc + src)
                       : make_uint4(0, 0, 0, 0);
     uint4 vr = ok_blk ? *reinterpret_cast<const uint4 *>(vc + src)
@@ -197,13 +214,16 @@ __global__ void __launch_bounds__(256)
         vo[2 * e] = (float)vh.x;
         vo[2 * e + 1] = (float)vh.y;
       }
+      // (plain stores: each lane writes two 16-byte halves of a 32-byte
+      // run, and non-temporal stores of such partial lines measured 37 %
+      // slower)
       reinterpret_cast<float4 *>(kf)[0] = make_float4(ko[0], ko[1], ko[2], ko[3]);
       reinterpret_cast<float4 *>(kf)[1] = make_float4(ko[4], ko[5], ko[6], ko[7]);
       reinterpret_cast<float4 *>(vf)[0] = make_float4(vo[0], vo[1], vo[2], vo[3]);
       reinterpret_cast<float4 *>(vf)[1] = make_float4(vo[4], vo[5], vo[6], vo[7]);
     } else {
-      *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(ok) + dst) = kr;
-      *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(ov) + dst) = vr;
+      store_nt16(static_cast<uint16_t *>(ok) + dst, kr);
+      store_nt16(static_cast<uint16_t *>(ov) + dst, vr);
     }
   } else {
     uint16_t kr = ok_blk ? kc[src] : 0, vr = ok_blk ? vc[src] : 0;
@@ -431,8 +451,12 @@ __global__ void __launch_bounds__(256)
   W *to = reinterpret_cast<W *>(t + (size_t)d * block_elems);
   const size_t words = block_elems * 2 / sizeof(W);
   for (size_t w = (size_t)blockIdx.x * blockDim.x + threadIdx.x; w < words;
-       w += (size_t)gridDim.x * blockDim.x)
-    to[w] = from[w];
+       w += (size_t)gridDim.x * blockDim.x) {
+    if constexpr (sizeof(W) == 16)
+      store_nt16(to + w, load_nt16(from + w));
+    else
+      to[w] = from[w];
+  }
 }
 
 // Logical [n, bs, n_kv, hd] view of listed blocks (test/inspection path).
