@@ -567,6 +567,8 @@ struct DecodeArgs {
   // Host-side launch hint (not read by the kernels): average context
   // tokens per workgroup.
   uint32_t avg_tokens;
+  // Host-side launch hint: tokens of the longest workgroup.
+  uint32_t max_tokens;
   // Host-side: the shape runs the generic kernel (generic.hip).
   uint32_t generic;
 };
@@ -1589,15 +1591,17 @@ uint32_t partition_tokens(const rvkv_pool *p, uint32_t batch, uint32_t n_heads,
 
 // Wavefronts per decode workgroup: four (the waves of a workgroup split its
 // context) unless the grid alone already has >= 2048 workgroups (8 per CU),
-// and two when workgroups average under 192 context tokens (short items:
-// fewer waves each doing more chunks beat more waves each paying the
-// start-up and merge; measured on the churn workload's final steps, 33.3 ->
-// 27.2 us). RVKV_DECODE_WAVES overrides.
-uint32_t decode_waves(uint64_t workgroups, uint32_t avg_tokens) {
+// and two when even the longest workgroup has under 192 context tokens
+// (short items: fewer waves each doing more chunks beat more waves each
+// paying the start-up and merge; churn's final launch 23.0 vs 26.2 us).
+// A launch that still holds some long items keeps four: its time is set by
+// them (churn's 200-step run 1.9 -> 2.4 TB/s against deciding on the
+// average). RVKV_DECODE_WAVES overrides.
+uint32_t decode_waves(uint64_t workgroups, uint32_t max_tokens) {
   static const uint32_t forced = env_u32("RVKV_DECODE_WAVES");
   if (forced >= 1 && forced <= 4) return forced;
   if (workgroups >= 2048) return 1;
-  return avg_tokens < 192 ? 2 : 4;
+  return max_tokens < 192 ? 2 : 4;
 }
 
 struct WsLayout {
@@ -1635,13 +1639,16 @@ WsLayout ws_layout(const rvkv_pool *p, uint32_t batch, uint32_t n_heads,
 template <int HD, int GT>
 void launch_decode(const DecodeArgs &a, dim3 grid, hipStream_t st) {
   static const uint32_t forced_u = env_u32("RVKV_DECODE_UNROLL");
-  const uint32_t W =
-      decode_waves((uint64_t)grid.x * grid.y * grid.z, a.avg_tokens);
-  // Eight loads per chunk pay off for 512-byte rows and for large groups
-  // in single-wave workgroups; otherwise four keep more waves resident.
-  const bool u8 = forced_u ? forced_u == 8
-                           : ((HD >= 256 && a.avg_tokens >= 512) ||
-                              (GT >= 5 && W == 1));
+  const uint64_t wgs = (uint64_t)grid.x * grid.y * grid.z;
+  const uint32_t W = decode_waves(wgs, a.max_tokens);
+  // Eight loads per chunk pay off for 512-byte rows, for large groups in
+  // single-wave workgroups, and for long items when every wave of the
+  // launch fits at two per SIMD (<= 2048 waves; Llama 64 x 2048: 63.0 ->
+  // 64.8 % of 8 TB/s); otherwise four keep more waves resident.
+  const bool u8 =
+      forced_u ? forced_u == 8
+               : ((HD >= 256 && a.avg_tokens >= 512) || (GT >= 5 && W == 1) ||
+                  (GT <= 4 && a.avg_tokens >= 512 && wgs * W <= 2048));
   // (m, l) pairs rounded up to 16 bytes, then the accumulator rows; at
   // least the f32 kernel's W * GT * (HD + 2) floats.
   const size_t lds =
@@ -2005,7 +2012,8 @@ struct rvkv_decode_plan {
   const rvkv_pool *pool;
   uint32_t batch, n_heads, n_kv, head_dim, max_ctx;
   int32_t window;
-  uint32_t part_tokens, n_items, n_reds, n_slots, avg_tokens = 0;
+  uint32_t part_tokens, n_items, n_reds, n_slots, avg_tokens = 0,
+      max_tokens = 0;
   uint4 *d_buf = nullptr;   // items, then reduction rows (device)
   uint4 *h_buf = nullptr;   // pinned staging copy of the same
   size_t cap = 0;           // entries both buffers hold
@@ -2176,6 +2184,9 @@ int plan_build(rvkv_decode_plan *pl, const uint32_t *ctx_lens_host,
   pl->max_ctx = max_ctx;
   pl->part_tokens = P;
   pl->avg_tokens = items.empty() ? 0u : (uint32_t)(total / items.size());
+  pl->max_tokens = 0;
+  for (const uint4 &it : items)
+    pl->max_tokens = std::max(pl->max_tokens, it.z > it.y ? it.z - it.y : 0u);
   pl->n_items = (uint32_t)items.size();
   pl->n_reds = (uint32_t)reds.size();
   pl->n_slots = slots;
@@ -2311,6 +2322,7 @@ int paged_decode_ws(const char *op, const rvkv_pool *pool, uint32_t layer,
   a.part_tokens = partition_tokens(pool, batch, n_heads, max_ctx_len);
   a.n_parts = w.n_parts;
   a.avg_tokens = a.part_tokens < max_ctx_len ? a.part_tokens : max_ctx_len;
+  a.max_tokens = a.avg_tokens;
   const dim3 grid(w.n_parts, pool->n_kv * a.n_sub, batch);
   return launch_decode_pair(op, a, decode_hd(pool->head_dim), gt, grid,
                             dim3(n_heads, batch), w.n_parts > 1, pool->stream);
@@ -2405,6 +2417,7 @@ int rvkv_paged_decode_planned(const rvkv_pool *pool,
   a.reds = plan->d_buf + plan->n_items;
   a.part_tokens = plan->part_tokens;
   a.avg_tokens = plan->avg_tokens;
+  a.max_tokens = plan->max_tokens;
   a.n_parts = 1;
   if (rvkv_detail::mfma_decode_wanted(pool, plan->n_heads))
     return planned_mfma(op, pool, plan, layer, a, max_blocks, scale);
@@ -2475,6 +2488,7 @@ int rvkv_decode_step(rvkv_pool *pool, const rvkv_decode_plan *plan,
     a.reds = plan->d_buf + plan->n_items;
     a.part_tokens = plan->part_tokens;
     a.avg_tokens = plan->avg_tokens;
+    a.max_tokens = plan->max_tokens;
     a.n_parts = 1;
     if (rvkv_detail::mfma_decode_wanted(pool, n_heads))
       return planned_mfma(op, pool, plan, layer, a, max_blocks, scale);
@@ -2493,6 +2507,7 @@ int rvkv_decode_step(rvkv_pool *pool, const rvkv_decode_plan *plan,
   a.part_tokens = partition_tokens(pool, batch, n_heads, max_ctx_len);
   a.n_parts = w.n_parts;
   a.avg_tokens = a.part_tokens < max_ctx_len ? a.part_tokens : max_ctx_len;
+  a.max_tokens = a.avg_tokens;
   const dim3 grid(w.n_parts, pool->n_kv * a.n_sub, batch);
   return launch_decode_pair(op, a, decode_hd(pool->head_dim), gt, grid,
                             dim3(n_heads, batch), w.n_parts > 1, pool->stream);
