@@ -483,14 +483,20 @@ __global__ void __launch_bounds__(
     }
     kbits[si] = 0;
     vbits[si] = 0;
+    // A chunk whose key is not read (past k_end, or an unreadable block)
+    // loads the lane's chunk-0 address again instead: that line is fetched
+    // anyway (or is block 0's), so the masked keys of a sequence's last
+    // block cost no HBM bytes. Its value is masked out at the LDS store.
+    const uint64_t off0 = (uint64_t)(kid[0] < a.num_blocks ? kid[0] : 0u) *
+                              blk_bytes + (t_off + k_off[0]);
 #pragma unroll
     for (int i = 0; i < CHK; ++i) {
       // The address checks its own block id: all_ok covers only the blocks
       // of keys below k_end, and the last tile may reach past them.
-      const bool okb = kid[i] < a.num_blocks;
-      kbits[si] |= (uint32_t)(okb && kt + k_key[i] < k_end) << i;
+      const bool use = kid[i] < a.num_blocks && kt + k_key[i] < k_end;
+      kbits[si] |= (uint32_t)use << i;
       const uint64_t off =
-          (uint64_t)(okb ? kid[i] : 0u) * blk_bytes + (t_off + k_off[i]);
+          use ? (uint64_t)kid[i] * blk_bytes + (t_off + k_off[i]) : off0;
       kr[si][i] = ld16<WAVES == 1>(kbase + off);
       if constexpr (TRV)
         vr[si][i] = ld16<WAVES == 1>(vbase + off);
@@ -502,8 +508,12 @@ __global__ void __launch_bounds__(
         const uint32_t tok = kt + v_key[j];
         vbits[si] |= (uint32_t)(okb && tok < k_end) << (2 * j);
         vbits[si] |= (uint32_t)(okb && tok + 1 < k_end) << (2 * j + 1);
-        const char *vp = vbase + (uint64_t)(okb ? vid[j] : 0u) * blk_bytes +
-                         (t_off + v_off[j]);
+        // (a pair wholly unread loads the lane's chunk-0 pair again)
+        const bool use = okb && tok < k_end;
+        const char *vp =
+            vbase + (use ? (uint64_t)vid[j] * blk_bytes + (t_off + v_off[j])
+                         : (uint64_t)(vid[0] < a.num_blocks ? vid[0] : 0u) *
+                                   blk_bytes + (t_off + v_off[0]));
         if (v_lane) {
           vr0[si][j] = ld16<WAVES == 1>(vp);
           vr1[si][j] = ld16<WAVES == 1>(vp + HD * 2);
