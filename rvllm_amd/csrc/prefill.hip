@@ -674,20 +674,32 @@ __global__ void __launch_bounds__(
     } else {
       // Register j of sub-tile t holds key kt + 8hl + c, c = 32t + 16(j/8)
       // + j%8 (a constant): valid for lo <= c < hi and a readable block.
+      // Each run of 8 registers gets a bit mask of its valid keys first
+      // (range bits, and with unreadable blocks the key flags' bits), then
+      // one select per register: no branches per key.
       const int32_t lo = (int32_t)(row_lo - kt) - 8 * hl;
       const int32_t hi = (int32_t)(row_hi - kt) - 8 * hl;
 #pragma unroll
       for (int t = 0; t < NT; ++t)
 #pragma unroll
         for (int g8 = 0; g8 < 2; ++g8) {
-          const uint32_t k0 = 32 * t + 16 * g8 + 8 * hl;
-          const uint64_t okw =
-              all_ok ? ~0ull : *reinterpret_cast<const uint64_t *>(kok + k0);
+          const int32_t c0 = 32 * t + 16 * g8;
+          const uint32_t a0 = (uint32_t)min(max(lo - c0, 0), 8);
+          const uint32_t a1 = (uint32_t)min(max(hi - c0, 0), 8);
+          // keys e in [a0, a1)
+          uint32_t vm = a1 > a0 ? ((1u << (a1 - a0)) - 1u) << a0 : 0u;
+          if (!all_ok) {  // (uniform) flags: one byte (0 or 1) per key
+            const uint32_t k0 = 32 * t + 16 * g8 + 8 * hl;
+            const uint2 fw = *reinterpret_cast<const uint2 *>(kok + k0);
+            // Bytes b0..b3 of a word (each 0 or 1) to bits 0..3: the product
+            // puts byte i's bit at 24 + i, with no carries into those bits.
+            const uint32_t f4l = ((fw.x & 0x01010101u) * 0x01020408u) >> 24;
+            const uint32_t f4h = ((fw.y & 0x01010101u) * 0x01020408u) >> 24;
+            vm &= f4l | (f4h << 4);
+          }
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            const int32_t c = 32 * t + 16 * g8 + e;
-            const bool valid = (all_ok || ((okw >> (8 * e)) & 1u)) &&
-                               c >= lo && c < hi;
+            const bool valid = (vm >> e) & 1u;
             const float x = valid ? s[t][8 * g8 + e] : -__builtin_inff();
             s[t][8 * g8 + e] = x;
             mx = fmaxf(mx, x);
