@@ -1265,7 +1265,7 @@ def test_prefill_full_prompt_from_empty():
     assert np.abs(out - want).max() < ATOL
 
 
-@pytest.mark.parametrize("hd", [64, 256])
+@pytest.mark.parametrize("hd", [64, 128, 256])
 def test_prefill_edges(hd):
     """Rows that see no key (read_num <= pos_offset) are zero; q_len 1
     agrees with the decode kernel; an out-of-range table entry is read as
@@ -1304,6 +1304,9 @@ def test_prefill_edges(hd):
     assert torch.isfinite(got).all()
     assert torch.equal(got[:2], good[:2])
     assert torch.equal(got[2, :176], good[2, :176])
+    # rows past the bad block see exactly keys 0..175: as if read_num = 176
+    cut = st.paged_prefill(0, qq, dev_u32(tables), z, dev_u32([192, 192, 176]))
+    assert (got[2, 176:] - cut[2, 176:]).abs().max().item() < 1e-6
 
 
 def test_prefill_rejections():
