@@ -1589,19 +1589,27 @@ uint32_t partition_tokens(const rvkv_pool *p, uint32_t batch, uint32_t n_heads,
   return P;
 }
 
+// Short items: even the longest workgroup has under 192 context tokens.
+bool short_items(uint64_t workgroups, uint32_t max_tokens) {
+  return workgroups < 2048 && max_tokens < 192;
+}
+
 // Wavefronts per decode workgroup: four (the waves of a workgroup split its
-// context) unless the grid alone already has >= 2048 workgroups (8 per CU),
-// and two when even the longest workgroup has under 192 context tokens
-// (short items: fewer waves each doing more chunks beat more waves each
-// paying the start-up and merge; churn's final launch 23.0 vs 26.2 us).
-// A launch that still holds some long items keeps four: its time is set by
-// them (churn's 200-step run 1.9 -> 2.4 TB/s against deciding on the
-// average). RVKV_DECODE_WAVES overrides.
-uint32_t decode_waves(uint64_t workgroups, uint32_t max_tokens) {
+// context) unless the grid alone already has >= 2048 workgroups (8 per CU).
+// Short items with groups of up to four heads keep four waves, each with
+// two loads per chunk (120 VGPRs at head_dim 256: every wave of churn's
+// 1024-workgroup launch resident at once); larger groups take two waves of
+// four loads (fewer waves each doing more chunks beat more waves each
+// paying the start-up and merge when not all fit: churn's final launch
+// 23.0 vs 26.2 us at four loads). A launch that still holds some long
+// items keeps four waves of four or eight loads: its time is set by them
+// (churn's 200-step run 1.9 -> 2.4 TB/s against deciding on the average).
+// RVKV_DECODE_WAVES overrides.
+uint32_t decode_waves(uint64_t workgroups, uint32_t max_tokens, int gt) {
   static const uint32_t forced = env_u32("RVKV_DECODE_WAVES");
   if (forced >= 1 && forced <= 4) return forced;
   if (workgroups >= 2048) return 1;
-  return max_tokens < 192 ? 2 : 4;
+  return short_items(workgroups, max_tokens) && gt > 4 ? 2 : 4;
 }
 
 struct WsLayout {
@@ -1640,15 +1648,19 @@ template <int HD, int GT>
 void launch_decode(const DecodeArgs &a, dim3 grid, hipStream_t st) {
   static const uint32_t forced_u = env_u32("RVKV_DECODE_UNROLL");
   const uint64_t wgs = (uint64_t)grid.x * grid.y * grid.z;
-  const uint32_t W = decode_waves(wgs, a.max_tokens);
+  const uint32_t W = decode_waves(wgs, a.max_tokens, GT);
   // Eight loads per chunk pay off for 512-byte rows, for large groups in
   // single-wave workgroups, and for long items when every wave of the
   // launch fits at two per SIMD (<= 2048 waves; Llama 64 x 2048: 63.0 ->
-  // 64.8 % of 8 TB/s); otherwise four keep more waves resident.
+  // 64.8 % of 8 TB/s); two for short items with groups of up to four
+  // (with four waves a workgroup, above); otherwise four keep more waves
+  // resident.
   const bool u8 =
       forced_u ? forced_u == 8
                : ((HD >= 256 && a.avg_tokens >= 512) || (GT >= 5 && W == 1) ||
                   (GT <= 4 && a.avg_tokens >= 512 && wgs * W <= 2048));
+  const bool u2 = forced_u ? forced_u == 2
+                           : GT <= 4 && short_items(wgs, a.max_tokens);
   // (m, l) pairs rounded up to 16 bytes, then the accumulator rows; at
   // least the f32 kernel's W * GT * (HD + 2) floats.
   const size_t lds =
@@ -1661,6 +1673,9 @@ void launch_decode(const DecodeArgs &a, dim3 grid, hipStream_t st) {
                        dim3(64 * W), lds, st, a);
   else if (u8)
     hipLaunchKernelGGL((decode_part_kernel<HD, GT, 8, 1, false>), grid,
+                       dim3(64 * W), lds, st, a);
+  else if (u2)
+    hipLaunchKernelGGL((decode_part_kernel<HD, GT, 2, 1, false>), grid,
                        dim3(64 * W), lds, st, a);
   else
     hipLaunchKernelGGL((decode_part_kernel<HD, GT, 4, 1, false>), grid,
