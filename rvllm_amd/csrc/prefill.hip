@@ -434,10 +434,27 @@ __global__ void __launch_bounds__(
   u32x4 vr0[DEPTH][CHV], vr1[DEPTH][CHV];
   uint32_t kbits[DEPTH], vbits[DEPTH];
 
+  // From head_dim 64 up, one wave-wide load covers 512 / head_dim <= 8
+  // keys, all in one block (blocks hold >= 8): a chunk's block id is
+  // wave-uniform and comes by a scalar load through the constant address
+  // space. A vector load would count in the same in-order queue as the K/V
+  // loads in flight, so waiting for the ids would wait for those too.
+  constexpr bool SCALAR_IDS = HD >= 64;
+  typedef const __attribute__((address_space(4))) uint32_t cu32;
+  cu32 *ctable = (cu32 *)(uintptr_t)table;
   auto fetch_ids = [&](uint32_t kt) {
     const uint32_t b0 = kt >> a.bs_log2, last = a.max_blocks - 1u;
+    if constexpr (SCALAR_IDS) {
 #pragma unroll
-    for (int i = 0; i < CHK; ++i) kid[i] = table[min(b0 + k_db[i], last)];
+      for (int i = 0; i < CHK; ++i) {
+        // the chunk's first key (lane 0's): lanes add lane / CPR < 512 / HD
+        const uint32_t key0 = (64u * wave + (uint32_t)(NTH * i)) / CPR;
+        kid[i] = ctable[min(b0 + (key0 >> a.bs_log2), last)];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < CHK; ++i) kid[i] = table[min(b0 + k_db[i], last)];
+    }
     if constexpr (!TRV) {
 #pragma unroll
       for (int j = 0; j < CHV; ++j) vid[j] = table[min(b0 + v_db[j], last)];
