@@ -133,10 +133,15 @@ template <int HD, int WAVES>
 struct Lds {
   static constexpr int BN = tile_keys<HD, WAVES>();
   static constexpr int KS = HD + 8;  // K row stride in halves (16 B pad)
+  // Row-major V stride: 32 halves of pad. The transposing reads of P.V
+  // (four keys x four dims per 16 lanes) met 0.33 bank conflicts per LDS
+  // access with 8, 16 or 24 halves of pad (Llama prefill, 17 M conflict
+  // cycles a launch) and none with 32.
+  static constexpr int VRS = HD + 32;
   static constexpr size_t k_bytes = (size_t)BN * KS * 2;
   static constexpr int VS = BN + 8;  // Vt row stride in halves (transposed)
   static constexpr size_t v_bytes =
-      v_rowmajor(HD) ? k_bytes : (size_t)HD * VS * 2;
+      v_rowmajor(HD) ? (size_t)BN * VRS * 2 : (size_t)HD * VS * 2;
   // Workgroups of several waves double-buffer the tile, so one barrier a
   // tile both publishes it and retires the buffer the next tile overwrites
   // (a one-wave workgroup orders its own LDS accesses).
@@ -225,7 +230,7 @@ __global__ void __launch_bounds__(
   static_assert(!SPLIT || (WAVES % 2 == 0 && WAVES > 1), "wave pairs");
   constexpr int kBM = block_rows<HD, WAVES>();
   using LD = Lds<HD, WAVES>;
-  constexpr int KS = LD::KS, VS = LD::VS, BN = LD::BN;
+  constexpr int KS = LD::KS, VS = LD::VS, BN = LD::BN, VRS = LD::VRS;
   constexpr bool TRV = v_rowmajor(HD);
   constexpr int NT = BN / 32;                 // 32-key sub-tiles per tile
   // This wave's share of the head dimension: all of it, or one half.
@@ -562,7 +567,7 @@ __global__ void __launch_bounds__(
       *reinterpret_cast<u32x4 *>(ks + key * KS + dc * 8) = kr[si][i];
       if constexpr (TRV) {
         const bool vok = tile_ok || ((kbits[si] >> i) & 1u);
-        *reinterpret_cast<u32x4 *>(vs + key * KS + dc * 8) =
+        *reinterpret_cast<u32x4 *>(vs + key * VRS + dc * 8) =
             vok ? vr[si][i] : u32x4{0u, 0u, 0u, 0u};
       }
       // Every loader of a key writes the same flag.
@@ -608,7 +613,7 @@ __global__ void __launch_bounds__(
         if (tid < CPR) {
           *reinterpret_cast<u32x4 *>(ks + r * KS + tid * 8) = new_kc;
           if constexpr (TRV)
-            *reinterpret_cast<u32x4 *>(vs + r * KS + tid * 8) = new_vc;
+            *reinterpret_cast<u32x4 *>(vs + r * VRS + tid * 8) = new_vc;
         }
         if constexpr (!TRV) {
           if (tid < HD) vs[tid * VS + r] = new_ve;
@@ -766,9 +771,9 @@ __global__ void __launch_bounds__(
           if constexpr (TRV) {
             // Two transposing reads of 4 keys each; the lane's address is
             // the (key, dim) its 16-lane group hands out.
-            const uint16_t *vp = vs + (32 * t + 16 * c + tr_key) * KS +
+            const uint16_t *vp = vs + (32 * t + 16 * c + tr_key) * VRS +
                                  (dh * DT + dt) * 32 + tr_dim;
-            const v4h lo = tr_read(vp), hi = tr_read(vp + 4 * KS);
+            const v4h lo = tr_read(vp), hi = tr_read(vp + 4 * VRS);
             vf = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
           } else {
             vf = *reinterpret_cast<const half8 *>(
