@@ -226,7 +226,10 @@ int rvkv_paged_decode_planned(const rvkv_pool *pool,
  * (as in the engine, src/engine.rs:446-451): the slot is the block-table slot
  * of position ctx_lens[b]-1. plan may be NULL (uniform partitioning, same
  * workspace as rvkv_paged_decode) or a plan built for this batch (then
- * batch/n_heads/window must match it and max_ctx_len is ignored). */
+ * batch/n_heads/window must match it and max_ctx_len is ignored). On an f32
+ * pool the rows are stored as f32 (F32 copied, F16 widened exactly), also in
+ * one launch; shapes that run the generic kernel take an append launch and
+ * then the decode. */
 int rvkv_decode_step(rvkv_pool *pool, const rvkv_decode_plan *plan,
                      uint32_t layer, const void *k, const void *v,
                      rvkv_dtype src_dtype, const uint32_t *slot_block,

@@ -1276,6 +1276,12 @@ __global__ void __launch_bounds__(256) decode_f32_kernel(DecodeArgs a) {
   const uint32_t lane_off = (uint32_t)(rg * HD * 4 + c * 16);
   const char *zero_v = reinterpret_cast<const char *>(g_zero_rows) + lane_off;
   const uint64_t blk_bytes = a.block_stride * 4;
+  // Fused append (rvkv_decode_step): position ctx - 1 holds the row appended
+  // this step; the workgroup whose range holds it skips that key in the
+  // loop, stores the row and folds it in from registers afterwards.
+  const uint32_t newtok = (a.new_k != nullptr && ctx - 1 >= t0 && ctx - 1 < t1)
+                              ? ctx - 1
+                              : 0xFFFFFFFFu;
   for (uint32_t ch = first + skip; ch < t1; ch += stride) {
     float4 kr[U][NL], vr[U][NL];
     bool valid[U];
@@ -1284,7 +1290,7 @@ __global__ void __launch_bounds__(256) decode_f32_kernel(DecodeArgs a) {
       const uint32_t tb = ch + u * RPL;
       const uint32_t id = table[min(tb >> a.bs_log2, last_blk)];
       const uint32_t tok = tb + rg;
-      valid[u] = id < a.num_blocks && tok >= lo && tok < t1;
+      valid[u] = id < a.num_blocks && tok >= lo && tok < t1 && tok != newtok;
       const char *row = (uint64_t)(id < a.num_blocks ? id : 0u) * blk_bytes +
                         (uint64_t)(tb & bs_mask) * (HD * 4) + lane_off + kbase;
       const char *kp = valid[u] ? row : zero_v;
@@ -1299,6 +1305,9 @@ __global__ void __launch_bounds__(256) decode_f32_kernel(DecodeArgs a) {
                                __uint_as_float(vb.z), __uint_as_float(vb.w));
       }
     }
+    // Keep the chunk's loads issued together ahead of the math (without
+    // this fence the scheduler may pair each load with its first use).
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int g = 0; g < GT; ++g) {
       float s[U];
@@ -1332,6 +1341,75 @@ __global__ void __launch_bounds__(256) decode_f32_kernel(DecodeArgs a) {
           acc[g][j * 4 + 1] = __builtin_fmaf(pu, vr[u][j].y, acc[g][j * 4 + 1]);
           acc[g][j * 4 + 2] = __builtin_fmaf(pu, vr[u][j].z, acc[g][j * 4 + 2]);
           acc[g][j * 4 + 3] = __builtin_fmaf(pu, vr[u][j].w, acc[g][j * 4 + 3]);
+        }
+      }
+    }
+  }
+  if (newtok != 0xFFFFFFFFu && wave == 0) {
+    // The appended row (f32 source copied, f16 widened exactly, as the
+    // append does): stored by sub-group 0's row group 0, and one more key
+    // of row group 0's softmax state.
+    float4 nk[NL], nv[NL];
+    const size_t src = ((size_t)b * a.n_kv + kvh) * HD;
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+      const uint32_t e0 = (j * R + c) * 4;
+      if (a.new_f32) {
+        nk[j] = *reinterpret_cast<const float4 *>(
+            static_cast<const float *>(a.new_k) + src + e0);
+        nv[j] = *reinterpret_cast<const float4 *>(
+            static_cast<const float *>(a.new_v) + src + e0);
+      } else {
+        const uint2 kh = *reinterpret_cast<const uint2 *>(
+            static_cast<const uint16_t *>(a.new_k) + src + e0);
+        const uint2 vh = *reinterpret_cast<const uint2 *>(
+            static_cast<const uint16_t *>(a.new_v) + src + e0);
+        const h2 k01 = as_h2(kh.x), k23 = as_h2(kh.y);
+        const h2 v01 = as_h2(vh.x), v23 = as_h2(vh.y);
+        nk[j] = make_float4((float)k01.x, (float)k01.y, (float)k23.x,
+                            (float)k23.y);
+        nv[j] = make_float4((float)v01.x, (float)v01.y, (float)v23.x,
+                            (float)v23.y);
+      }
+    }
+    if (sub == 0 && rg == 0) {
+      const uint32_t nb = a.new_blk[b], no = a.new_off[b];
+      if (nb < a.num_blocks && no < a.block_size) {
+        const size_t dst = (size_t)nb * a.block_stride +
+                           (size_t)kvh * a.head_stride + (size_t)no * HD;
+        float *kc = reinterpret_cast<float *>(const_cast<uint16_t *>(a.kc));
+        float *vc = reinterpret_cast<float *>(const_cast<uint16_t *>(a.vc));
+#pragma unroll
+        for (int j = 0; j < NL; ++j) {
+          const uint32_t e0 = (j * R + c) * 4;
+          *reinterpret_cast<float4 *>(kc + dst + e0) = nk[j];
+          *reinterpret_cast<float4 *>(vc + dst + e0) = nv[j];
+        }
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+      float d = 0.f;
+#pragma unroll
+      for (int j = 0; j < NL; ++j) {
+        d = __builtin_fmaf(q[g][j].x, nk[j].x, d);
+        d = __builtin_fmaf(q[g][j].y, nk[j].y, d);
+        d = __builtin_fmaf(q[g][j].z, nk[j].z, d);
+        d = __builtin_fmaf(q[g][j].w, nk[j].w, d);
+      }
+      d = row_group_sum<R>(d);
+      if (rg == 0) {
+        const float mx = fmaxf(m[g], d);
+        const float corr = __builtin_amdgcn_exp2f(m[g] - mx);
+        const float p = __builtin_amdgcn_exp2f(d - mx);
+        m[g] = mx;
+        l[g] = l[g] * corr + p;
+#pragma unroll
+        for (int j = 0; j < NL; ++j) {
+          acc[g][j * 4 + 0] = __builtin_fmaf(p, nv[j].x, acc[g][j * 4 + 0] * corr);
+          acc[g][j * 4 + 1] = __builtin_fmaf(p, nv[j].y, acc[g][j * 4 + 1] * corr);
+          acc[g][j * 4 + 2] = __builtin_fmaf(p, nv[j].z, acc[g][j * 4 + 2] * corr);
+          acc[g][j * 4 + 3] = __builtin_fmaf(p, nv[j].w, acc[g][j * 4 + 3] * corr);
         }
       }
     }
@@ -2471,9 +2549,9 @@ int rvkv_decode_step(rvkv_pool *pool, const rvkv_decode_plan *plan,
                           plan ? plan->max_ctx : max_ctx_len, scale, window,
                           out, &a, &gt);
   if (rc) return rc;
-  if (pool->f32() || a.generic) {
-    // f32 cache or the generic kernel: the append and the decode as two
-    // launches on the stream.
+  if (a.generic) {
+    // The generic kernel: the append and the decode as two launches on the
+    // stream.
     if ((rc = rvkv_append(pool, layer, k, v, src_dtype, slot_block, slot_off,
                           batch)))
       return rc;

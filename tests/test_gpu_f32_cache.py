@@ -144,8 +144,9 @@ def _f32_pool(bs, nkv, hd, lens, seed):
                                   (1, 64), (8, 128)])
 def test_f32_decode_vs_oracle(G, hd):
     """Uniform and planned decode (windows, an empty sequence, sequences
-    long enough to split) and the decode step (append, then decode) over an
-    f32 cache, against float64 attention over the same cells."""
+    long enough to split) and the decode step (the append fused into the
+    decode launch; f32 and f16 source rows) over an f32 cache, against
+    float64 attention over the same cells."""
     bs, nkv = 16, 2
     lens = np.array([1, 17, 300, 2500, 64, 5], np.uint32)
     db, st, ref = _f32_pool(bs, nkv, hd, lens, seed=G * 7 + hd)
@@ -189,6 +190,22 @@ def test_f32_decode_vs_oracle(G, hd):
         assert np.array_equal(_bits(st.read_blocks(0, 1, ids).cpu().numpy()),
                               _bits(ref.v))
         nk, nv = nv, nk
+    # f16 source rows: widened exactly into the f32 cells
+    nk16 = rng.standard_normal((len(lens), nkv, hd)).astype(np.float16)
+    nv16 = rng.standard_normal((len(lens), nkv, hd)).astype(np.float16)
+    got = st.decode_step(0, torch.from_numpy(nk16).cuda(),
+                         torch.from_numpy(nv16).cuda(), dev_u32(db.slot_block),
+                         dev_u32(db.slot_off), q, tab, dev_u32(lens),
+                         int(lens.max()), plan=plan)
+    want = orc.decode_step(ref, db.slot_block, db.slot_off,
+                           nk16.astype(np.float32), nv16.astype(np.float32),
+                           tables, db.max_blocks, lens, qn)
+    assert np.abs(got.cpu().numpy() - want).max() < ATOL_F32
+    ids = dev_u32(np.arange(db.num_blocks))
+    assert np.array_equal(_bits(st.read_blocks(0, 0, ids).cpu().numpy()),
+                          _bits(ref.k))
+    assert np.array_equal(_bits(st.read_blocks(0, 1, ids).cpu().numpy()),
+                          _bits(ref.v))
 
 
 def test_f32_smollm2_config():
