@@ -808,6 +808,48 @@ def test_decode_step_equals_append_then_decode(planned, src, G, hd, bs,
     assert _decode_vs_oracle(a, 0, db, q, window=window) < ATOL
 
 
+@pytest.mark.parametrize("planned", [False, True])
+@pytest.mark.parametrize("G,hd", [(1, 32), (4, 64), (2, 128), (4, 256),
+                                  (3, 64), (6, 64)])
+def test_decode_step_short_items(planned, G, hd):
+    """Contexts all under 192 tokens: the launch shape for short items (four
+    waves of two loads per chunk for groups of up to four heads, two waves
+    of four otherwise). The fused step leaves the cache bits of
+    append-then-decode and matches it and the oracle."""
+    from rvllm_amd.kv_storage import HipDecodePlan
+    nkv, bs = 2, 16
+    rng = np.random.default_rng(hd * 10 + G)
+    lens = rng.integers(1, 192, 40).astype(np.uint32)
+    lens[:3] = [1, 191, 64]
+    cfg = W.Config("short", 9, 1, nkv * G, nkv, hd, bs, len(lens))
+    db = W.ragged_batch(cfg, lens, seed=G + hd)
+    stores = [HipKvStorage(1, db.num_blocks, bs, nkv, hd) for _ in range(2)]
+    for st in stores:
+        fill_layer(st, 0, seed=5)
+    g = torch.Generator("cuda").manual_seed(11)
+    nk = torch.randn(len(lens), nkv, hd, device="cuda", generator=g)
+    nv = torch.randn(len(lens), nkv, hd, device="cuda", generator=g)
+    q = torch.randn(len(lens), nkv * G, hd, device="cuda", generator=g)
+    sb, so = dev_u32(db.slot_block), dev_u32(db.slot_off)
+    tables, ctx = dev_u32(db.padded_tables()), dev_u32(lens)
+    a, b = stores
+    if planned:
+        plan = HipDecodePlan(a, lens, nkv * G)
+        out_a = a.decode_step(0, nk, nv, sb, so, q, tables, ctx, plan=plan)
+    else:
+        out_a = a.decode_step(0, nk, nv, sb, so, q, tables, ctx,
+                              int(lens.max()))
+    b.write_tokens(0, sb, so, nk, nv)
+    out_b = b.paged_decode(0, q, tables, ctx, int(lens.max()))
+    ids = dev_u32(np.arange(db.num_blocks))
+    for which in (0, 1):
+        assert torch.equal(a.read_blocks(0, which, ids),
+                           b.read_blocks(0, which, ids))
+    assert (out_a - out_b).abs().max().item() < 5e-4
+    db.ctx_lens = lens
+    assert _decode_vs_oracle(a, 0, db, q) < ATOL
+
+
 # ---- continuous-batching churn through the block manager -------------------
 def test_churn_driver_parity():
     """A few churn steps (finish 10%, admit 64-token prompts, decode all)
