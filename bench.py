@@ -45,6 +45,10 @@ def parse():
                    "qwen3, gemma); 0 = the config's own")
     p.add_argument("--no-cpu", action="store_true",
                    help="skip the CPU baseline leg")
+    p.add_argument("--no-secondary", dest="secondary", action="store_false",
+                   help="default run only: skip the secondary records "
+                   "(Llama-3.2-1B 256 x 4096, the Qwen3 prefill append, the "
+                   "200-step churn)")
     p.add_argument("--f32-cache", dest="f32_cache", action="store_true",
                    default=None,
                    help="f32 cache cells, the reference's own (default for "
@@ -803,7 +807,8 @@ def run_prefill(args, torch, W):
             "avg_launch_ms": round(launch_ms, 5),
         },
     }
-    print(json.dumps(res), flush=True)
+    st.close()
+    return res
 
 
 def run_churn(args, torch, W):
@@ -895,7 +900,8 @@ def run_churn(args, torch, W):
     rc = read_ceiling(torch, dec_bytes, max(args.steps // 10, 3))
     rc["frac"] = round(achieved / rc["GB/s"], 4)
     res["roofline"]["stream_read_ceiling"] = rc
-    print(json.dumps(res), flush=True)
+    drv.close()
+    return res
 
 
 def main():
@@ -915,10 +921,10 @@ def main():
         copy_calibration(torch, max(args.steps, 5))
         return
     if args.churn:
-        run_churn(args, torch, W)
+        print(json.dumps(run_churn(args, torch, W)), flush=True)
         return
     if args.prefill:
-        run_prefill(args, torch, W)
+        print(json.dumps(run_prefill(args, torch, W)), flush=True)
         return
     if args.prep:
         run_prep(args, torch, W)
@@ -935,6 +941,61 @@ def main():
     if args.cow:
         run_cow(args, torch, W)
         return
+    res = run_decode(args, torch, W, cpu=not args.no_cpu)
+    if (args.secondary and args.config == "qwen3-0.6b" and not args.batch
+            and not args.ctx):
+        res["secondary"] = secondary_records(args, torch, W)
+    print(json.dumps(res), flush=True)
+
+
+def _sub_args(args, **kw):
+    """A copy of the command-line arguments with some fields replaced."""
+    d = dict(vars(args))
+    d.update(kw)
+    return argparse.Namespace(**d)
+
+
+def _secondary(res, role):
+    """The part of a workload's record a secondary entry keeps."""
+    keep = ("metric", "value", "unit", "steps", "warmup", "ms_per_step",
+            "ms_per_step_median", "dtype", "config", "pct_of_peak",
+            "tok_per_s", "roofline")
+    out = {"role": role}
+    out.update({k: res[k] for k in keep if k in res})
+    return out
+
+
+def secondary_records(args, torch, W):
+    """The rest of the north star's target workloads, run after the
+    headline in the same process (as rvllm's bench sweeps its workloads in
+    one invocation): the Llama-3.2-1B shape at 256 x 4096, configs[2]'s
+    prefill append (f32 source rows, scatter only) and configs[4]'s
+    200-step churn. Each pool is freed before the next is made."""
+    out = []
+    steps = max(args.steps // 2, 5)
+    r = run_decode(_sub_args(args, config="llama-3.2-1b", batch=256,
+                             ctx=4096, plan=None, unfused=False), torch, W,
+                   cpu=False)
+    out.append(_secondary(r, "north-star shape 2: Llama-3.2-1B, 256 seqs "
+                             "x 4096 tokens, fused decode step"))
+    torch.cuda.empty_cache()
+    r = run_prefill(_sub_args(args, config="qwen3-0.6b", batch=0, ctx=0,
+                              prefill="f32", steps=steps,
+                              warmup=min(args.warmup, 2)), torch, W)
+    out.append(_secondary(r, "configs[2] prefill append (scatter only, "
+                             "f32 source rows)"))
+    torch.cuda.empty_cache()
+    r = run_churn(_sub_args(args, config="gemma-3-270m", batch=0, ctx=0,
+                            steps=200, warmup=3), torch, W)
+    out.append(_secondary(r, "configs[4] churn, 200 engine steps"))
+    torch.cuda.empty_cache()
+    return out
+
+
+def run_decode(args, torch, W, cpu):
+    """The decode step of --config (append + paged decode per layer, fused
+    by default) timed over --steps; returns the record."""
+    from rvllm_amd.kv_storage import HipKvStorage
     db = build_workload(W, args.config, args.batch, args.ctx)
     c = db.cfg
     f32 = (args.f32_cache if args.f32_cache is not None
@@ -1118,12 +1179,14 @@ def main():
     rc = read_ceiling(torch, dec_bytes, max(args.steps, 3))
     rc["frac"] = round(achieved / rc["GB/s"], 4)
     res["roofline"]["stream_read_ceiling"] = rc
-    if not args.no_cpu:
+    if cpu:
         from oracle import oracle as orc
         res["cpu_baseline"] = cpu_baseline(orc, W, st, db, args.cpu_seconds,
                                              f32=f32)
-    print(json.dumps(res), flush=True)
+    if plan is not None:
+        plan.close()
     st.close()
+    return res
 
 
 if __name__ == "__main__":

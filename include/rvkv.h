@@ -146,10 +146,14 @@ int rvkv_paged_decode(const rvkv_pool *pool, uint32_t layer, const float *q,
  * array of device memory that each GPU holds for the life of the process;
  * a shape whose rvkv_decode_workspace_bytes exceeds 8 MiB is rejected with
  * RVKV_EUNSUPPORTED (only reachable at head_dim 256 with > 4 query heads per
- * KV head). Every call on one GPU shares that GPU's array, so calls
- * that overlap on one GPU (several streams, several threads) race; calls
- * queued on one stream do not. Same arguments, rules and results as
- * rvkv_paged_decode otherwise. */
+ * KV head). Every call on one GPU shares that GPU's array and finds the
+ * last call's contents in it. Calls on one stream are ordered by the
+ * stream; a call on another stream of the same GPU first waits (on the
+ * device, via an event created once per GPU) for the last call that used
+ * the array, and calls from several host threads take it one at a time.
+ * Not ordered: a stream under graph capture, so a captured graph's replays
+ * race with calls on other streams of that GPU. Same arguments, rules and
+ * results as rvkv_paged_decode otherwise. */
 int rvkv_paged_decode_noalloc(const rvkv_pool *pool, uint32_t layer,
                               const float *q, const uint32_t *block_tables,
                               const uint32_t *ctx_lens, uint32_t batch,

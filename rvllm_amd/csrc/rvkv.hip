@@ -2321,6 +2321,14 @@ namespace {
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void *g_scratch_ptr[kMaxDevices];
+// Cross-stream ordering of the scratch array: the stream of the last call
+// that used it and an event recorded on that stream after its launches.
+// A call on another stream waits on that event first, so calls on
+// different streams of one device serialise on the array instead of
+// overwriting each other's partials.
+hipEvent_t g_scratch_done[kMaxDevices];
+hipStream_t g_scratch_stream[kMaxDevices];
+bool g_scratch_used[kMaxDevices];
 
 // Device `dev`'s copy of `scratch`, looked up once per device (with that
 // device current; the caller's current device is restored).
@@ -2336,12 +2344,45 @@ int scratch_device_ptr(const char *op, int dev, void **out) {
       return hip_fail(op, e);
     void *ptr = nullptr;
     e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    hipEvent_t ev = nullptr;
+    if (e == hipSuccess)
+      e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
     if (cur != dev) (void)hipSetDevice(cur);
     if (e != hipSuccess) return hip_fail(op, e);
     if (!ptr) return fail(RVKV_EHIP, op, "scratch has no device address");
     g_scratch_ptr[dev] = ptr;
+    g_scratch_done[dev] = ev;
   }
   *out = g_scratch_ptr[dev];
+  return RVKV_OK;
+}
+
+// Orders this call's use of device `dev`'s scratch array after the last
+// call's when that one ran on another stream (the caller holds
+// g_scratch_mu from here until scratch_release, so calls from several
+// threads take the array one at a time). A stream under graph capture
+// is not ordered (an event recorded outside the capture cannot be waited
+// on inside it): a captured graph's replays race with calls on other
+// streams, as the header states.
+int scratch_acquire(const char *op, int dev, hipStream_t stream,
+                    bool *capturing) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(stream, &cs);
+  if (e != hipSuccess) return hip_fail(op, e);
+  *capturing = cs != hipStreamCaptureStatusNone;
+  if (*capturing) return RVKV_OK;
+  if (g_scratch_used[dev] && g_scratch_stream[dev] != stream &&
+      (e = hipStreamWaitEvent(stream, g_scratch_done[dev], 0)) != hipSuccess)
+    return hip_fail(op, e);
+  return RVKV_OK;
+}
+
+// Records the end of this call's launches on `stream` for the next caller.
+int scratch_release(const char *op, int dev, hipStream_t stream) {
+  hipError_t e = hipEventRecord(g_scratch_done[dev], stream);
+  if (e != hipSuccess) return hip_fail(op, e);
+  g_scratch_stream[dev] = stream;
+  g_scratch_used[dev] = true;
   return RVKV_OK;
 }
 
@@ -2417,8 +2458,18 @@ int paged_decode_ws(const char *op, const rvkv_pool *pool, uint32_t layer,
   a.avg_tokens = a.part_tokens < max_ctx_len ? a.part_tokens : max_ctx_len;
   a.max_tokens = a.avg_tokens;
   const dim3 grid(w.n_parts, pool->n_kv * a.n_sub, batch);
-  return launch_decode_pair(op, a, decode_hd(pool->head_dim), gt, grid,
-                            dim3(n_heads, batch), w.n_parts > 1, pool->stream);
+  const bool ordered = no_alloc && w.bytes > 0;
+  bool capturing = false;
+  std::unique_lock<std::mutex> lock(g_scratch_mu, std::defer_lock);
+  if (ordered) lock.lock();
+  if (ordered &&
+      (rc = scratch_acquire(op, pool->device, pool->stream, &capturing)))
+    return rc;
+  rc = launch_decode_pair(op, a, decode_hd(pool->head_dim), gt, grid,
+                          dim3(n_heads, batch), w.n_parts > 1, pool->stream);
+  if (rc == RVKV_OK && ordered && !capturing)
+    rc = scratch_release(op, pool->device, pool->stream);
+  return rc;
 }
 
 }  // namespace
@@ -2551,19 +2602,18 @@ int rvkv_decode_step(rvkv_pool *pool, const rvkv_decode_plan *plan,
   if (rc) return rc;
   if (a.generic) {
     // The generic kernel: the append and the decode as two launches on the
-    // stream.
+    // stream. Every check runs before the append, so a refused call leaves
+    // the cache unchanged.
+    if (plan) {
+      if (plan->n_kv != pool->n_kv || plan->head_dim != pool->head_dim)
+        return fail(RVKV_EINVAL, op, "plan was built for another pool shape");
+    } else if (batch > 65535) {
+      return fail(RVKV_EUNSUPPORTED, op, "batch too large");
+    }
     if ((rc = rvkv_append(pool, layer, k, v, src_dtype, slot_block, slot_off,
                           batch)))
       return rc;
-    if (a.generic) {
-      if (plan) {
-        if (plan->n_kv != pool->n_kv || plan->head_dim != pool->head_dim)
-          return fail(RVKV_EINVAL, op, "plan was built for another pool shape");
-      } else if (batch > 65535) {
-        return fail(RVKV_EUNSUPPORTED, op, "batch too large");
-      }
-      return decode_generic(op, pool, layer, a, batch, scale);
-    }
+    return decode_generic(op, pool, layer, a, batch, scale);
   } else {
     a.new_k = k;
     a.new_v = v;

@@ -176,6 +176,14 @@ class ChurnDriver:
                 ctx, self.batch, self.max_blocks, c.n_heads, 0, scale,
                 c.window, self._out_p[layer], ws_p, ws_n))
 
+    def close(self) -> None:
+        """Frees the plan and the pool (the block manager frees with the
+        object)."""
+        if self.plan is not None:
+            self.plan.close()
+            self.plan = None
+        self.st.close()
+
     def decode_bytes(self, lens) -> int:
         """Algorithmic bytes of one decode launch at these lengths."""
         c = self.cfg

@@ -137,8 +137,10 @@ class HipKvStorage:
     """CudaKvStorage (src/cuda/kv_storage.rs:65-164) on MI355X: one zeroed
     pool for all layers' K and V, owned by librvkv. Cells are f16 (the
     default) or, with dtype=torch.float32, f32 like rvllm's own cache (every
-    operation; attention and attn_prep on an f32 pool run the generic
-    kernels)."""
+    operation). On an f32 pool, decode at head_dim 32/64/128/256 with
+    power-of-two blocks runs the tuned decode_f32_kernel (split partials and
+    a reduction, as on f16); prefill, attn_prep and decode at other shapes
+    run the generic kernels."""
 
     def __init__(self, n_layers: int, num_blocks: int, block_size: int,
                  n_kv_heads: int, head_dim: int, stream=None,

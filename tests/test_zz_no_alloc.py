@@ -59,12 +59,16 @@ def test_noalloc_decode_matches_workspace_decode():
         assert torch.equal(got, want), (i, (got - want).abs().max().item())
 
 
-@pytest.mark.parametrize("hd,bs,dtype", [(128, 16, torch.float32),
-                                          (96, 12, torch.float16)])
-def test_noalloc_decode_other_pools(hd, bs, dtype):
+@pytest.mark.parametrize("hd,bs,dtype,split", [(128, 16, torch.float32, True),
+                                                (96, 16, torch.float16, True),
+                                                (96, 12, torch.float16, False)])
+def test_noalloc_decode_other_pools(hd, bs, dtype, split):
     """An f32 pool (the f32 decode kernel, its partials in the scratch
-    array) and a shape on the generic kernel (no partials): bit-identical to
-    rvkv_paged_decode, two calls in a row, the second smaller."""
+    array), head_dim 96 on an f16 pool with power-of-two blocks (the tuned
+    kernel at a rounded-up head_dim, whose partial rows have the rounded
+    width, in the scratch array) and a shape on the generic kernel (no
+    partials): bit-identical to rvkv_paged_decode, two calls in a row, the
+    second smaller."""
     print(f"\n[gpu] noalloc other pools hd={hd} bs={bs} {dtype}", flush=True)
     nkv, H = 2, 6
     st = HipKvStorage(1, 1200, bs, nkv, hd, dtype=dtype)
@@ -81,6 +85,8 @@ def test_noalloc_decode_other_pools(hd, bs, dtype):
         max_ctx = int(lens.max())
         tables, ctx = dev_u32(db.padded_tables()), dev_u32(lens)
         q = torch.randn(len(lens), H, hd, device="cuda", generator=g)
+        if split and i == 0:
+            assert st.decode_workspace_bytes(len(lens), H, max_ctx) > 0
         want = st.paged_decode(0, q, tables, ctx, max_ctx)
         got = _noalloc(st, q, tables, ctx, max_ctx)
         torch.cuda.synchronize()
@@ -104,3 +110,38 @@ def test_noalloc_decode_rejects_oversized_partials():
                        "partials exceed the 8 MiB scratch") as e:
         _noalloc(st, q, tables, ctx, max_ctx)
     assert e.value.code == RVKV_EUNSUPPORTED
+
+
+def test_noalloc_decode_two_streams():
+    """Two calls that both keep partials in the scratch array, queued on two
+    different streams with no host synchronisation between them: the second
+    waits for the first on the device, so both match rvkv_paged_decode."""
+    print("\n[gpu] noalloc decode on two streams", flush=True)
+    bs, nkv, hd, H = 16, 4, 128, 16
+    st = HipKvStorage(1, 2200, bs, nkv, hd)
+    fill_layer(st, 0, seed=5)
+    lens = [np.array([9000, 12000, 4000], np.uint32),
+            np.array([15000, 300, 8000, 7000], np.uint32)]
+    dbs = [W.ragged_batch(W.Config("na3", 9, 1, H, nkv, hd, bs, len(x)), x,
+                          seed=20 + i) for i, x in enumerate(lens)]
+    args = []
+    for i, (x, db) in enumerate(zip(lens, dbs)):
+        assert db.num_blocks <= 2200
+        q = torch.randn(len(x), H, hd, device="cuda",
+                        generator=torch.Generator("cuda").manual_seed(30 + i))
+        args.append((q, dev_u32(db.padded_tables()), dev_u32(x),
+                     int(x.max())))
+        assert st.decode_workspace_bytes(len(x), H, int(x.max())) > 0
+    want = [st.paged_decode(0, q, t, c, m) for q, t, c, m in args]
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    got = []
+    for s, (q, t, c, m) in zip((s1, s2), args):
+        with torch.cuda.stream(s):
+            st.set_stream(s)
+            got.append(_noalloc(st, q, t, c, m))
+    torch.cuda.synchronize()
+    st.set_stream(torch.cuda.current_stream())
+    for i in range(2):
+        assert torch.equal(got[i], want[i]), (
+            i, (got[i] - want[i]).abs().max().item())
