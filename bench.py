@@ -164,6 +164,59 @@ def read_ceiling(torch, nbytes, steps):
             "GB/s": round(nb / (ms * 1e-3) / 1e9, 2)}
 
 
+def copy_ceiling(torch, nbytes, read_frac, steps):
+    """The plain streaming-copy rate at one launch's size and read/write mix:
+    the copy probe (16-byte non-temporal loads and stores, contiguous on both
+    sides) moving `nbytes` in total, split read:write as 2:1, 1:1 or 1:2
+    (whichever is nearest read_frac), over buffers rotated so no launch
+    finds its data in the MALL."""
+    import ctypes
+
+    from rvllm_amd import _lib
+    lib = _lib.load_calib()
+    ra, wa = min(((2, 1), (1, 1), (1, 2)),
+                 key=lambda r: abs(r[0] / (r[0] + r[1]) - read_frac))
+    unit = 32 * ra * wa  # keeps both sides whole 16-byte units
+    rd = int(nbytes) * ra // (ra + wa) // unit * unit
+    wr = rd * wa // ra
+    n_buf = max(2, -(-(3 << 29) // (rd + wr)))
+    srcs = [torch.zeros(rd // 4, dtype=torch.int32, device="cuda")
+            for _ in range(n_buf)]
+    dsts = [torch.empty(wr // 4, dtype=torch.int32, device="cuda")
+            for _ in range(n_buf)]
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def sweep():
+        for a, b in zip(srcs, dsts):
+            _lib.check_calib(lib.rvkv_calib_copy_probe(
+                ctypes.c_void_p(a.data_ptr()), ctypes.c_void_p(b.data_ptr()),
+                rd, wr, 65536, stream))
+    sweep()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        sweep()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / (steps * n_buf)
+    del srcs, dsts
+    return {"read_bytes": rd, "write_bytes": wr, "avg_launch_ms": round(ms, 5),
+            "GB/s": round((rd + wr) / (ms * 1e-3) / 1e9, 2)}
+
+
+def with_copy_ceiling(torch, res, read_frac, steps):
+    """Adds roofline.stream_copy_ceiling (and the launch's fraction of it)
+    to a byte mover's record."""
+    r = res["roofline"]
+    cc = copy_ceiling(torch, r["algorithmic_bytes_per_launch"], read_frac,
+                      steps)
+    cc["frac"] = round(r["achieved"] / cc["GB/s"], 4)
+    r["stream_copy_ceiling"] = cc
+    return res
+
+
 def measured_traffic(config, batch, unfused, ctx=0):
     """HBM bytes per decode launch measured by rocprofv3 --pmc (FETCH_SIZE +
     WRITE_SIZE, each scaled by the same counter's reading for a copy of
@@ -593,8 +646,11 @@ def run_gather(args, torch, W):
          "global_batch": db.batch, "seq_len": plan.ctx_len,
          "parallelism": "single GPU"},
         f"f16 cache -> {args.gather}")
-    print(json.dumps(res), flush=True)
     st.close()
+    del ok, ov
+    torch.cuda.empty_cache()
+    with_copy_ceiling(torch, res, read / per_launch, max(args.steps // 4, 3))
+    print(json.dumps(res), flush=True)
 
 
 def run_cow(args, torch, W):
@@ -636,8 +692,10 @@ def run_cow(args, torch, W):
          "global_batch": len(src), "seq_len": c.block_size,
          "parallelism": "single GPU"},
         "f16 (bit copy)")
-    print(json.dumps(res), flush=True)
     st.close()
+    torch.cuda.empty_cache()
+    with_copy_ceiling(torch, res, 0.5, max(args.steps // 4, 3))
+    print(json.dumps(res), flush=True)
 
 
 def run_prep(args, torch, W):
@@ -726,6 +784,12 @@ def run_prep(args, torch, W):
             "avg_launch_ms": round(launch_ms, 5),
         },
     }
+    st.close()
+    del q, k, v, q_out
+    torch.cuda.empty_cache()
+    rd = 4 * H * hd + 8 * KV * hd  # q, k, v in (per token)
+    wr = 4 * H * hd + 4 * KV * hd  # q out, k/v cells
+    with_copy_ceiling(torch, res, rd / (rd + wr), max(args.steps // 4, 3))
     print(json.dumps(res), flush=True)
 
 
@@ -808,7 +872,10 @@ def run_prefill(args, torch, W):
         },
     }
     st.close()
-    return res
+    del k, v, sb, so
+    torch.cuda.empty_cache()
+    return with_copy_ceiling(torch, res, src_bytes / (src_bytes + 2),
+                             max(args.steps // 2, 3))
 
 
 def run_churn(args, torch, W):

@@ -94,6 +94,20 @@ int rvkv_append(rvkv_pool *pool, uint32_t layer, const void *k, const void *v,
                 rvkv_dtype src_dtype, const uint32_t *slot_block,
                 const uint32_t *slot_off, uint32_t n_tokens);
 
+/* n_layers calls of rvkv_append with the same slots, layers layer0 ..
+ * layer0+n_layers-1, in one launch: the batched form of the per-layer
+ * KvStorage::write_tokens (src/kv_storage.rs:116-150) that a prefill makes
+ * for every layer with one slot list (write_positions, src/engine.rs:365-388).
+ * Layer l's rows are k/v + l*src_layer_stride elements of src_dtype
+ * (src_layer_stride >= n_tokens*n_kv_heads*head_dim when n_layers > 1).
+ * Same rounding, validation and out-of-range slot rule as rvkv_append; the
+ * cache afterwards is bit-identical to the per-layer calls. f32 pools and
+ * head_dim % 8 != 0 run one append per layer. */
+int rvkv_append_layers(rvkv_pool *pool, uint32_t layer0, uint32_t n_layers,
+                       const void *k, const void *v, rvkv_dtype src_dtype,
+                       uint64_t src_layer_stride, const uint32_t *slot_block,
+                       const uint32_t *slot_off, uint32_t n_tokens);
+
 /* ---- block-table gather ---------------------------------------------
  * Replaces CudaKvStorage::gather (src/cuda/kv_storage.rs:132-164) ->
  * kv_gather_wrapper (src/cuda/ops.rs:381-445) -> kv_gather.cu, and

@@ -28,6 +28,8 @@ SIGNATURES = {
     "rvkv_pool_bytes": (_sz, [_P]),
     "rvkv_pool_set_stream": (_int, [_P, _P]),
     "rvkv_append": (_int, [_P, _u32, _P, _P, _int, _P, _P, _u32]),
+    "rvkv_append_layers": (_int, [_P, _u32, _u32, _P, _P, _int, _u64, _P, _P,
+                                  _u32]),
     "rvkv_gather": (_int, [_P, _u32, _P, _u32, _u32, _u32, _P, _P, _int]),
     "rvkv_paged_decode": (_int, [_P, _u32, _P, _P, _P, _u32, _u32, _u32, _u32,
                                  _f32, _i32, _P, _P, _sz]),
@@ -148,6 +150,8 @@ def load_calib() -> ctypes.CDLL:
         L = ctypes.CDLL(path)
         L.rvkv_calib_read_probe.restype = _int
         L.rvkv_calib_read_probe.argtypes = [_P, _sz, _u32, _P, _P]
+        L.rvkv_calib_copy_probe.restype = _int
+        L.rvkv_calib_copy_probe.argtypes = [_P, _P, _sz, _sz, _u32, _P]
         L.rvkv_calib_last_error.restype = ctypes.c_char_p
         L.rvkv_calib_last_error.argtypes = []
         _calib = L

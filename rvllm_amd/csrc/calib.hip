@@ -2,7 +2,8 @@
 // against: how fast this device reads a buffer of a given size once, with
 // nothing else in the launch (no tables, no arithmetic worth the name).
 // It has no counterpart in rvllm; it exists so a paged-KV launch of B bytes
-// can be compared with the best plain read of B bytes on the same device.
+// can be compared with the best plain read of B bytes on the same device
+// (and a byte mover with the best plain copy of its read and write bytes).
 // Built into its own librvkv_calib.so for the benchmark: it is not part of
 // the product ABI (include/rvkv.h).
 //
@@ -53,6 +54,44 @@ __global__ void __launch_bounds__(kReadThreads)
   if (acc == 0x9e3779b9u && sink) sink[0] = acc;  // practically never
 }
 
+// The mixed read/write counterpart: each unit reads RA and writes WA
+// 16-byte words (a doubled side is two contiguous halves, so every load and
+// store instruction covers one contiguous run), non-temporal loads and
+// stores, four units in flight per lane. RA:WA = 2:1, 1:1 and 1:2 match the
+// byte movers (f32 rows appended as f16, f16 copies, f16 gathered to f32).
+template <int RA, int WA>
+__global__ void __launch_bounds__(kReadThreads)
+    copy_probe_kernel(const uint4 *__restrict__ src, uint4 *__restrict__ dst,
+                      uint64_t n_units, uint64_t per_wg) {
+  const uint64_t lo = (uint64_t)blockIdx.x * per_wg;
+  const uint64_t hi = lo + per_wg < n_units ? lo + per_wg : n_units;
+  typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+  const u32x4v *s4 = reinterpret_cast<const u32x4v *>(src);
+  u32x4v *d4 = reinterpret_cast<u32x4v *>(dst);
+  for (uint64_t i = lo + threadIdx.x; i < hi;
+       i += (uint64_t)kReadThreads * kReadUnroll) {
+    u32x4v v[kReadUnroll][RA];
+#pragma unroll
+    for (int u = 0; u < kReadUnroll; ++u) {
+      const uint64_t j = i + (uint64_t)u * kReadThreads;
+#pragma unroll
+      for (int r = 0; r < RA; ++r)
+        v[u][r] = j < hi ? __builtin_nontemporal_load(s4 + r * n_units + j)
+                         : u32x4v{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int u = 0; u < kReadUnroll; ++u) {
+      const uint64_t j = i + (uint64_t)u * kReadThreads;
+      if (j >= hi) continue;
+      u32x4v w = v[u][0];
+      if constexpr (RA == 2) w ^= v[u][1];
+#pragma unroll
+      for (int r = 0; r < WA; ++r)
+        __builtin_nontemporal_store(r ? ~w : w, d4 + r * n_units + j);
+    }
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -72,6 +111,47 @@ int rvkv_calib_read_probe(const void *buf, size_t bytes, uint32_t workgroups,
   hipLaunchKernelGGL(read_probe_kernel, dim3(workgroups), dim3(kReadThreads),
                      0, reinterpret_cast<hipStream_t>(stream),
                      static_cast<const uint4 *>(buf), n16, per_wg, sink);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : calib_fail(hipGetErrorString(e));
+}
+
+// Reads read_bytes from src and writes write_bytes to dst in one launch;
+// read_bytes:write_bytes must be 2:1, 1:1 or 1:2, both multiples of 16 (of
+// 32 for the doubled side). Returns 0, or -1 with the reason.
+int rvkv_calib_copy_probe(const void *src, void *dst, size_t read_bytes,
+                          size_t write_bytes, uint32_t workgroups,
+                          void *stream) {
+  if (read_bytes == 0 || write_bytes == 0) return 0;
+  if (!src || !dst) return calib_fail("src/dst is NULL");
+  if ((uintptr_t)src % 16 || (uintptr_t)dst % 16)
+    return calib_fail("src and dst must be 16-byte aligned");
+  int ra, wa;
+  if (read_bytes == 2 * write_bytes) {
+    ra = 2; wa = 1;
+  } else if (read_bytes == write_bytes) {
+    ra = 1; wa = 1;
+  } else if (2 * read_bytes == write_bytes) {
+    ra = 1; wa = 2;
+  } else {
+    return calib_fail("read:write must be 2:1, 1:1 or 1:2");
+  }
+  if (read_bytes % (16 * ra) || write_bytes % (16 * wa))
+    return calib_fail("sizes must be whole 16-byte units");
+  if (workgroups == 0) workgroups = 16384;
+  const uint64_t n_units = read_bytes / (16 * ra);
+  const uint64_t per_wg = (n_units + workgroups - 1) / workgroups;
+  const uint4 *s = static_cast<const uint4 *>(src);
+  uint4 *d = static_cast<uint4 *>(dst);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (ra == 2)
+    hipLaunchKernelGGL((copy_probe_kernel<2, 1>), dim3(workgroups),
+                       dim3(kReadThreads), 0, st, s, d, n_units, per_wg);
+  else if (wa == 2)
+    hipLaunchKernelGGL((copy_probe_kernel<1, 2>), dim3(workgroups),
+                       dim3(kReadThreads), 0, st, s, d, n_units, per_wg);
+  else
+    hipLaunchKernelGGL((copy_probe_kernel<1, 1>), dim3(workgroups),
+                       dim3(kReadThreads), 0, st, s, d, n_units, per_wg);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? 0 : calib_fail(hipGetErrorString(e));
 }

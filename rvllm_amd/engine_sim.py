@@ -5,7 +5,8 @@ for the gemma-3-270m churn workload:
 - every step a fraction of the running sequences finishes, and their blocks
   return to a seeded-shuffled, fragmented free list;
 - the same number of new sequences is admitted with short prompts, whose
-  K/V rows are appended (prefill append);
+  K/V rows of every layer are appended in one launch (prefill append,
+  rvkv_append_layers);
 - then every running sequence decodes one token: its slot comes from
   logical_to_physical(num_tokens) (rvkv_bm_append_slots), and one fused
   rvkv_decode_step per layer runs under a decode plan rebuilt from the
@@ -62,8 +63,10 @@ class ChurnDriver:
         self.nv = [torch.randn((batch, KV, hd), generator=g, device=dev)
                    for _ in range(L)]
         n_prompt = max(1, self.n_churn * prompt_len)
-        self.pk = torch.randn((n_prompt, KV, hd), generator=g, device=dev)
-        self.pv = torch.randn((n_prompt, KV, hd), generator=g, device=dev)
+        # Each layer's rows of the admitted prompts (f32, as a prefill's
+        # projections leave them).
+        self.pk = torch.randn((L, n_prompt, KV, hd), generator=g, device=dev)
+        self.pv = torch.randn((L, n_prompt, KV, hd), generator=g, device=dev)
         self.out = [torch.empty_like(self.q[0]) for _ in range(L)]
         P = ctypes.c_void_p
         self._q_p = [P(t.data_ptr()) for t in self.q]
@@ -166,10 +169,13 @@ class ChurnDriver:
         tables, ctx = P(db["tables"].data_ptr()), P(db["ctx"].data_ptr())
         pk, pv = P(self.pk.data_ptr()), P(self.pv.data_ptr())
         scale = 1.0 / np.sqrt(c.head_dim)
+        if n_prompt_tok:
+            # The admitted prompts' rows of every layer in one launch.
+            check(L.rvkv_append_layers(
+                st._pool, 0, c.n_layers, pk, pv, RVKV_F32,
+                self.pk.shape[1] * c.n_kv_heads * c.head_dim, pb, po,
+                n_prompt_tok))
         for layer in range(c.n_layers):
-            if n_prompt_tok:
-                check(L.rvkv_append(st._pool, layer, pk, pv, RVKV_F32, pb, po,
-                                    n_prompt_tok))
             check(L.rvkv_decode_step(
                 st._pool, plan._plan, layer, self._nk_p[layer],
                 self._nv_p[layer], RVKV_F32, sb, so, self._q_p[layer], tables,

@@ -213,6 +213,31 @@ class HipKvStorage:
                                   _DT[k.dtype], _ptr(block_ids),
                                   _ptr(offsets), n_tokens))
 
+    def write_tokens_layers(self, layer0: int, block_ids: torch.Tensor,
+                            offsets: torch.Tensor, k: torch.Tensor,
+                            v: torch.Tensor) -> None:
+        """write_tokens for layers layer0 .. layer0 + k.shape[0] - 1 with one
+        slot list, in one launch (rvkv_append_layers). k, v:
+        [n_layers, n_tokens, n_kv, hd] f32 or f16."""
+        _need(k.shape == v.shape and k.dim() == 4,
+              "kv_write: k/v must be [n_layers, n_tokens, n_kv_heads, "
+              "head_dim] of one shape")
+        n_layers, n_tokens = int(k.shape[0]), int(k.shape[1])
+        _need(n_tokens != 0 and n_layers != 0, "kv_write: k/v len is 0")
+        _need(tuple(k.shape[2:]) == (self.n_kv_heads, self.head_dim),
+              "kv_write: k/v rows must be [n_kv_heads, head_dim]")
+        _need(block_ids.numel() == n_tokens and offsets.numel() == n_tokens,
+              "kv_write: block_ids/offsets length must equal n_tokens")
+        _need(k.dtype == v.dtype and k.dtype in _DT,
+              "kv_write: k/v must both be float32 or float16")
+        _need(k.is_contiguous() and v.is_contiguous() and
+              block_ids.is_contiguous() and offsets.is_contiguous(),
+              "kv_write: inputs must be contiguous")
+        check(self._L.rvkv_append_layers(
+            self._pool, layer0, n_layers, _ptr(k), _ptr(v), _DT[k.dtype],
+            n_tokens * self.n_kv_heads * self.head_dim, _ptr(block_ids),
+            _ptr(offsets), n_tokens))
+
     # -- gather ---------------------------------------------------------
     def gather(self, layer: int, plan: HipGatherPlan, out_k: torch.Tensor,
                out_v: torch.Tensor) -> None:

@@ -159,6 +159,58 @@ def test_append_f16_source_copies_bits():
     assert np.array_equal(bits(st.read_blocks(0, 1, ids)), ref.v)
 
 
+@pytest.mark.parametrize("src", ["f32", "f16"])
+@pytest.mark.parametrize("nkv,hd,bs,pool_dt", [(1, 256, 16, torch.float16),
+                                               (8, 128, 16, torch.float16),
+                                               (3, 12, 3, torch.float16),
+                                               (2, 64, 16, torch.float32)])
+def test_append_layers_equals_per_layer_appends(src, nkv, hd, bs, pool_dt):
+    """rvkv_append_layers over layers 1..3 of a 5-layer pool (one launch on
+    f16 pools with head_dim % 8 == 0, per-layer appends otherwise) leaves
+    exactly the cache bits of three rvkv_append calls, and the oracle's;
+    layers 0 and 4 stay untouched. Out-of-range slots are skipped."""
+    rng = np.random.default_rng(hd + nkv + bs)
+    nb, L = 29, 5
+    a = HipKvStorage(L, nb, bs, nkv, hd, dtype=pool_dt)
+    b = HipKvStorage(L, nb, bs, nkv, hd, dtype=pool_dt)
+    slots = rng.permutation(nb * bs)[: nb * bs // 3]
+    n = len(slots)
+    blk, off = (slots // bs).astype(np.int64), slots % bs
+    blk[3] = nb + 5  # skipped
+    rows = (rng.standard_normal((2, 3, n, nkv, hd)) * 3).astype(np.float32)
+    rows.reshape(-1)[: len(SPECIALS)] = SPECIALS
+    if src == "f16":
+        rows = rows.astype(np.float16)
+    k, v = torch.from_numpy(rows[0]).cuda(), torch.from_numpy(rows[1]).cuda()
+    sb, so = dev_u32(blk), dev_u32(off)
+    a.write_tokens_layers(1, sb, so, k, v)
+    for l in range(3):
+        b.write_tokens(1 + l, sb, so, k[l].contiguous(), v[l].contiguous())
+    ids = dev_u32(np.arange(nb))
+    for layer in range(L):
+        for which in (0, 1):
+            ga = bits(a.read_blocks(layer, which, ids))
+            gb = bits(b.read_blocks(layer, which, ids))
+            assert np.array_equal(ga, gb), (layer, which)
+            if layer in (0, 4):
+                assert not ga.any()
+    if pool_dt == torch.float16:
+        for l in range(3):
+            ref = orc.KvCache(nb, bs, nkv, hd, orc.F16)
+            keep = blk < nb
+            if src == "f32":
+                ref.write_tokens(blk[keep], off[keep], rows[0, l][keep],
+                                 rows[1, l][keep])
+            else:
+                ref.write_tokens_f16(blk[keep], off[keep],
+                                     rows[0, l][keep].view(np.uint16),
+                                     rows[1, l][keep].view(np.uint16))
+            assert np.array_equal(bits(a.read_blocks(1 + l, 0, ids)), ref.k)
+            assert np.array_equal(bits(a.read_blocks(1 + l, 1, ids)), ref.v)
+    with pytest.raises(RvkvError, match="kv_write: layer range out of range"):
+        a.write_tokens_layers(3, sb, so, k, v)
+
+
 def test_append_skips_out_of_range_slots():
     st = HipKvStorage(1, 4, 16, 1, 64)
     k = torch.ones(3, 1, 64, device="cuda")
@@ -930,7 +982,8 @@ def test_churn_full_scale_gemma():
             want_dec = orc.f32_to_f16_bits(src_new[layer].cpu().numpy())
             got_dec = rows[[at[int(b)] for b in blocks], offs]
             assert np.array_equal(got_dec, want_dec)
-            want_pr = orc.f32_to_f16_bits(src_prompt.cpu().numpy()[:len(pb)])
+            want_pr = orc.f32_to_f16_bits(
+                src_prompt[layer].cpu().numpy()[:len(pb)])
             got_pr = rows[[at[int(b)] for b in pb], po]
             assert np.array_equal(got_pr, want_pr)
     sample = list(range(0, 1024, 64))
