@@ -212,8 +212,15 @@ int rvkv_decode_plan_update(rvkv_decode_plan *plan,
  * tables ([batch, max_blocks], what GatherPlan::new takes besides the read
  * counts, src/kv_storage.rs:50-75): items of sequences that share prefix
  * blocks are then ordered back to back, so those blocks are read from HBM
- * about once per XCD instead of once per sharer. Results are the same as
- * without tables; tables_host NULL is rvkv_decode_plan_update. */
+ * about once per XCD instead of once per sharer. On the matrix-core decode
+ * (head_dim 64, 5-16 query heads per KV head, no window) the blocks that up
+ * to 32 / group sharers hold alike, below each one's last position, become
+ * group items: one workgroup reads them once for all those sharers, whose
+ * partials the reduction merges with their own ranges' (results then match
+ * the lengths-only plan to within the decode tolerance, not bit for bit).
+ * tables_host must hold the same block ids as the device tables the decode
+ * calls pass (a group reads its first member's table for every member).
+ * tables_host NULL is rvkv_decode_plan_update. */
 int rvkv_decode_plan_update_tables(rvkv_decode_plan *plan,
                                    const uint32_t *ctx_lens_host,
                                    const uint32_t *tables_host,

@@ -37,7 +37,9 @@ int fail(int code, const char *op, const char *reason);
 // Records "<op>: <HIP error string>" and returns RVKV_EHIP.
 int hip_fail(const char *op, hipError_t e);
 // Matrix-core decode over a decode plan's work items (prefill.hip): used
-// for large GQA groups, where the VALU decode is instruction-bound.
+// for large GQA groups, where the VALU decode is instruction-bound. groups:
+// the plan's shared-prefix member lists (items flagged 0x80000000 in their
+// seq field index them).
 bool mfma_decode_wanted(const rvkv_pool *pool, uint32_t n_heads);
 int mfma_decode(const rvkv_pool *pool, uint32_t layer, const float *q,
                 const uint32_t *tables, const uint32_t *ctx_lens,
@@ -46,7 +48,8 @@ int mfma_decode(const rvkv_pool *pool, uint32_t layer, const float *q,
                 float *ws_acc, float *ws_ml, float *out,
                 const void *new_k = nullptr, const void *new_v = nullptr,
                 const uint32_t *new_blk = nullptr,
-                const uint32_t *new_off = nullptr, bool new_f32 = false);
+                const uint32_t *new_off = nullptr, bool new_f32 = false,
+                const uint32_t *groups = nullptr);
 // Paged attention for shapes the tuned kernels do not take (generic.hip):
 // any head_dim <= 1024, any block size, f16 or f32 cells, f32 arithmetic.
 // pos_offset NULL: decode (one row per sequence at read_num - 1). Keys

@@ -117,6 +117,10 @@ struct PrefillArgs {
   // output; otherwise the unnormalised partial (acc, m, l) goes to ws_acc /
   // ws_ml [slot][n_heads] for the decode reduction pass. NULL: prefill.
   const uint4 *items;
+  // Shared-prefix group items (seq field | kGroupItem): word offset of a
+  // list {n, n sequences, n slots}; the group's n * group query rows share
+  // the item's key range, whose blocks all members' tables hold alike.
+  const uint32_t *groups;
   float *ws_acc, *ws_ml;
   // Fused append (decode mode): this step's K/V row of every sequence
   // ([batch, n_kv, hd], f32 or f16) goes to slot (new_blk[b], new_off[b])
@@ -128,6 +132,7 @@ struct PrefillArgs {
 };
 
 constexpr uint32_t kNoSlot = 0xFFFFFFFFu;
+constexpr uint32_t kGroupItem = 0x80000000u;
 
 template <int HD, int WAVES>
 struct Lds {
@@ -248,6 +253,10 @@ __global__ void __launch_bounds__(
   // K/V, which then stays in that XCD's L2. Within a head, long (late)
   // rows go first.
   uint32_t tile, kvh, b, item_lo = 0, item_hi = 0xFFFFFFFFu, slot = kNoSlot;
+  // Group item: member list (n, sequences, slots); its first member's
+  // table serves every member over the item's range.
+  const uint32_t *gl = nullptr;
+  uint32_t n_mem = 0;
   if (a.items) {  // decode items: grid (items, n_kv), plan order kept
     const uint4 it = a.items[blockIdx.x];
     b = it.x;
@@ -256,6 +265,11 @@ __global__ void __launch_bounds__(
     slot = it.w;
     kvh = blockIdx.y;
     tile = 0;
+    if (b & kGroupItem) {
+      gl = a.groups + (b & ~kGroupItem);
+      n_mem = gl[0];
+      b = gl[1];
+    }
   } else {
     const uint32_t n_wg = a.n_tiles * a.n_kv * a.batch;
     const uint32_t w = blockIdx.x, xcd = w % 8, idx = w / 8;
@@ -282,9 +296,14 @@ __global__ void __launch_bounds__(
   const uint32_t ctx = min(a.read_num[b], cap);
   const uint32_t *table = a.tables + (size_t)b * a.max_blocks;
 
-  // Key range any row of the workgroup sees, in whole tiles.
+  // Query rows of this (sequence, KV head): group * q_len, or a group
+  // item's members' rows (each member one decode row per head).
+  const uint32_t rows = gl ? n_mem * a.group : a.rows;
+  // Key range any row of the workgroup sees, in whole tiles. (A group
+  // item's range ends below every member's position, so ctx and off bound
+  // none of it.)
   const uint32_t r_first = tile * kBM;
-  const uint32_t r_last = min(r_first + kBM, a.rows) - 1u;
+  const uint32_t r_last = min(r_first + kBM, rows) - 1u;
   const uint32_t k_end = min(min(ctx, off + r_last / a.group + 1u), item_hi);
   // (item_lo is a multiple of 256, so of BN)
   const uint32_t k_begin = max(
@@ -293,8 +312,8 @@ __global__ void __launch_bounds__(
 
   // The same for this wave's 32 rows (wave-uniform).
   const uint32_t rw0 = r_first + rgrp * kWaveRows;
-  const bool wave_live = rw0 < a.rows;
-  const uint32_t rw1 = min(rw0 + kWaveRows, a.rows) - 1u;
+  const bool wave_live = rw0 < rows;
+  const uint32_t rw1 = min(rw0 + kWaveRows, rows) - 1u;
   const uint32_t w_end =
       wave_live ? min(min(ctx, off + rw1 / a.group + 1u), item_hi) : 0u;
   const uint32_t w_begin = lo_bound(off + rw0 / a.group, a.window);
@@ -305,13 +324,17 @@ __global__ void __launch_bounds__(
 
   // This lane's query row.
   const uint32_t r = rw0 + ln;
-  const bool row_ok = r < a.rows;
-  const uint32_t qi = row_ok ? r / a.group : 0u;
-  const uint32_t head = kvh * a.group + (row_ok ? r - qi * a.group : 0u);
+  const bool row_ok = r < rows;
+  const uint32_t ri = row_ok ? r / a.group : 0u;
+  const uint32_t head = kvh * a.group + (row_ok ? r - ri * a.group : 0u);
+  // A group item's row ri / group is member ri's one decode row.
+  const uint32_t qi = gl ? 0u : ri;
+  const uint32_t bq = gl && row_ok ? gl[1 + ri] : b;
+  const uint32_t my_slot = gl ? (row_ok ? gl[1 + n_mem + ri] : kNoSlot) : slot;
   const uint32_t p = off + qi;
   const uint32_t row_hi = row_ok ? min(min(ctx, p + 1u), item_hi) : 0u;
   const uint32_t row_lo = max(lo_bound(p, a.window), item_lo);
-  const size_t qrow = ((size_t)b * a.q_len + qi) * a.n_heads + head;
+  const size_t qrow = ((size_t)bq * a.q_len + qi) * a.n_heads + head;
   // The appended key (fused decode step) when this item holds it.
   const uint32_t newtok =
       (a.new_k && ctx >= 1u && ctx - 1u >= item_lo && ctx - 1u < item_hi)
@@ -837,9 +860,9 @@ __global__ void __launch_bounds__(
     }
   }
   const float lt = sum_halves(l);
-  if (slot != kNoSlot) {  // a split decode sequence: unnormalised partial
+  if (gl || slot != kNoSlot) {  // split decode sequences: partials
     if (row_ok) {
-      const size_t idx = (size_t)slot * a.n_heads + head;
+      const size_t idx = (size_t)my_slot * a.n_heads + head;
       float *op = a.ws_acc + idx * HD;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
@@ -1014,7 +1037,8 @@ int mfma_decode(const rvkv_pool *pool, uint32_t layer, const float *q,
                 int32_t window, const uint4 *items, uint32_t n_items,
                 float *ws_acc, float *ws_ml, float *out, const void *new_k,
                 const void *new_v, const uint32_t *new_blk,
-                const uint32_t *new_off, bool new_f32) {
+                const uint32_t *new_off, bool new_f32,
+                const uint32_t *groups) {
   const char *op = "paged_decode";
   if (n_items == 0) return RVKV_OK;
   PrefillArgs a{};
@@ -1042,6 +1066,7 @@ int mfma_decode(const rvkv_pool *pool, uint32_t layer, const float *q,
   a.batch = 0;
   a.n_kv = pool->n_kv;
   a.items = items;
+  a.groups = groups;
   a.ws_acc = ws_acc;
   a.ws_ml = ws_ml;
   a.new_k = new_k;

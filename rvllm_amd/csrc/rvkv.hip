@@ -605,6 +605,9 @@ struct DecodeArgs {
 };
 
 constexpr uint32_t kNoSlot = 0xFFFFFFFFu;
+// A plan item whose seq field has this bit is a shared-prefix group item
+// (matrix-core decode only); the other bits locate its member list.
+constexpr uint32_t kGroupItem = 0x80000000u;
 
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {
@@ -2231,7 +2234,9 @@ int planned_mfma(const char *op, const rvkv_pool *pool,
   int rc = rvkv_detail::mfma_decode(
       pool, layer, a.q, a.tables, a.ctx_lens, max_blocks, plan->n_heads,
       scale, plan->window, a.items, plan->n_items, a.ws_acc, a.ws_ml, a.out,
-      a.new_k, a.new_v, a.new_blk, a.new_off, a.new_f32);
+      a.new_k, a.new_v, a.new_blk, a.new_off, a.new_f32,
+      reinterpret_cast<const uint32_t *>(plan->d_buf + plan->n_items +
+                                         plan->n_reds));
   if (rc || plan->n_reds == 0) return rc;
   return launch_reduce(op, a, decode_hd(pool->head_dim),
                        dim3(plan->n_heads, plan->n_reds),
@@ -2275,9 +2280,93 @@ int plan_build(rvkv_decode_plan *pl, const uint32_t *ctx_lens_host,
   uint32_t P = 256;
   while (P < want && P < (1u << 30)) P <<= 1;
 
+  // Items of at most P tokens over [start, n), with 1/8 slack so a range
+  // just past a multiple of P does not get a sliver item; split evenly on
+  // 256-token boundaries. Returns the count and the step.
+  auto split = [&](uint32_t start, uint32_t n, uint32_t *step_out) {
+    const uint32_t span = n - start;
+    uint32_t k = div_up(span, P + P / 8);
+    const uint32_t step = ((div_up(span, k) + 255u) & ~255u);
+    *step_out = step;
+    return div_up(span, step);
+  };
+
+  // Shared-prefix groups (matrix-core decode, host tables, no window): the
+  // sequences whose tables open with the same blocks are taken up to S at a
+  // time (S * group query rows fill one 32-row matrix tile), longest first;
+  // a group reads the blocks all its members share, [0, T), once for all of
+  // them, and each member reads only [T, n) on its own. T is a multiple of
+  // 256 below every member's appended position (n - 1), so a group never
+  // holds a key this step writes. Each member's partial of a group range is
+  // one more partition of that member for the reduction.
+  const uint32_t group = pl->n_heads / pool->n_kv;
+  std::vector<uint32_t> gstart(batch, 0xFFFFFFFFu);  // own-range start
+  std::vector<uint32_t> gidx(batch, 0xFFFFFFFFu);    // group of a member
+  struct Group {
+    uint32_t T;
+    std::vector<uint32_t> mem;
+  };
+  std::vector<Group> groups;
+  static const uint32_t no_groups = env_u32("RVKV_DECODE_NO_GROUPS");
+  if (mfma && tables_host && window <= 0 && group <= 16 && max_blocks &&
+      !no_groups) {
+    const uint32_t S = std::min<uint32_t>(32 / group, 8);
+    const uint32_t lg = ilog2(pool->block_size);
+    std::vector<std::pair<uint32_t, uint32_t>> cand;  // (first block, b)
+    for (uint32_t b = 0; b < batch; ++b)
+      if (ctx_lens_host[b] > 256u)
+        cand.push_back({tables_host[(size_t)b * max_blocks], b});
+    std::sort(cand.begin(), cand.end(), [&](const auto &x, const auto &y) {
+      if (x.first != y.first) return x.first < y.first;
+      if (ctx_lens_host[x.second] != ctx_lens_host[y.second])
+        return ctx_lens_host[x.second] > ctx_lens_host[y.second];
+      return x.second < y.second;
+    });
+    for (size_t i = 0; i < cand.size();) {
+      size_t j = i;
+      while (j < cand.size() && cand[j].first == cand[i].first) ++j;
+      for (size_t c = i; c + 1 < j; c += S) {
+        const size_t e = std::min(j, c + S);
+        if (e - c < 2) break;
+        uint32_t min_n = 0xFFFFFFFFu;
+        for (size_t m = c; m < e; ++m)
+          min_n = std::min(min_n, ctx_lens_host[cand[m].second]);
+        // Blocks every member has at the same place, below min_n - 1.
+        const uint32_t lim =
+            std::min<uint32_t>((min_n - 1) >> lg, max_blocks);
+        const uint32_t *t0 = tables_host + (size_t)cand[c].second * max_blocks;
+        uint32_t common = 0;
+        while (common < lim) {
+          bool same = true;
+          for (size_t m = c + 1; m < e && same; ++m)
+            same = tables_host[(size_t)cand[m].second * max_blocks + common] ==
+                   t0[common];
+          if (!same) break;
+          ++common;
+        }
+        const uint32_t T =
+            std::min<uint32_t>(common << lg, min_n - 1) & ~255u;
+        if (T < 256) continue;
+        Group g{T, {}};
+        for (size_t m = c; m < e; ++m) {
+          g.mem.push_back(cand[m].second);
+          gstart[cand[m].second] = T;
+          gidx[cand[m].second] = (uint32_t)groups.size();
+        }
+        groups.push_back(std::move(g));
+      }
+      i = j;
+    }
+  }
+
   std::vector<uint4> items, reds;
   items.reserve(batch);
   uint32_t slots = 0;
+  // First slot of each grouped member (its group partials come first).
+  std::vector<uint32_t> mslot(batch, 0);
+  std::vector<uint32_t> gpieces(groups.size(), 0), gstep(groups.size(), 0);
+  for (size_t g = 0; g < groups.size(); ++g)
+    gpieces[g] = split(0, groups[g].T, &gstep[g]);
   for (uint32_t b = 0; b < batch; ++b) {
     const uint32_t n = ctx_lens_host[b];
     if (n == 0) {  // zero row
@@ -2285,26 +2374,40 @@ int plan_build(rvkv_decode_plan *pl, const uint32_t *ctx_lens_host,
       continue;
     }
     const uint32_t lo = (window > 0 && n > (uint32_t)window) ? n - window : 0;
-    const uint32_t start = lo & ~255u;
-    // Items of at most P tokens, with 1/8 slack so a sequence just past a
-    // multiple of P does not get a sliver item; split evenly on 256-token
-    // boundaries.
-    const uint32_t span = n - start;
-    uint32_t k = div_up(span, P + P / 8);
-    const uint32_t step = ((div_up(span, k) + 255u) & ~255u);
-    k = div_up(span, step);
-    if (k == 1) {
+    const bool grouped = gidx[b] != 0xFFFFFFFFu;
+    const uint32_t start = grouped ? gstart[b] : lo & ~255u;
+    const uint32_t pre = grouped ? gpieces[gidx[b]] : 0;
+    uint32_t step;
+    const uint32_t k = split(start, n, &step);
+    if (k == 1 && pre == 0) {
       items.push_back(make_uint4(b, start, n, kNoSlot));
       continue;
     }
+    mslot[b] = slots;
     for (uint32_t i = 0; i < k; ++i) {
       const uint32_t t0 = start + i * step;
-      items.push_back(
-          make_uint4(b, t0, t0 + step < n ? t0 + step : n, slots + i));
+      items.push_back(make_uint4(b, t0, t0 + step < n ? t0 + step : n,
+                                 slots + pre + i));
     }
-    reds.push_back(make_uint4(b, slots, k, 0));
-    slots += k;
+    reds.push_back(make_uint4(b, slots, pre + k, 0));
+    slots += pre + k;
   }
+  // Group items: {kGroupItem | word offset of the member list, t0, t1, 0};
+  // list = n, then the members' sequences, then their slots for this piece.
+  std::vector<uint32_t> glist;
+  for (size_t g = 0; g < groups.size(); ++g) {
+    const Group &G = groups[g];
+    for (uint32_t i = 0; i < gpieces[g]; ++i) {
+      const uint32_t t0 = i * gstep[g];
+      const uint32_t t1 = std::min(t0 + gstep[g], G.T);
+      items.push_back(make_uint4(kGroupItem | (uint32_t)glist.size(), t0, t1,
+                                 0));
+      glist.push_back((uint32_t)G.mem.size());
+      for (uint32_t m : G.mem) glist.push_back(m);
+      for (uint32_t m : G.mem) glist.push_back(mslot[m] + i);
+    }
+  }
+  while (glist.size() % 4) glist.push_back(0);
   // Longest items first: the short tail fills in behind them. With the
   // block tables, items of one length are further ordered by the first
   // block they read, so the items of sequences that share prefix blocks
@@ -2319,7 +2422,10 @@ int plan_build(rvkv_decode_plan *pl, const uint32_t *ctx_lens_host,
     std::vector<std::pair<uint32_t, uint32_t>> by_block(items.size());
     for (size_t i = 0; i < items.size(); ++i) {
       const uint32_t bi = items[i].y >> lg;
-      fb[i] = bi < max_blocks ? tables_host[(size_t)items[i].x * max_blocks + bi]
+      const uint32_t sq = items[i].x & kGroupItem
+                              ? glist[(items[i].x & ~kGroupItem) + 1]
+                              : items[i].x;
+      fb[i] = bi < max_blocks ? tables_host[(size_t)sq * max_blocks + bi]
                               : 0xFFFFFFFFu;
       by_block[i] = {fb[i], items[i].z - items[i].y};
     }
@@ -2353,7 +2459,7 @@ int plan_build(rvkv_decode_plan *pl, const uint32_t *ctx_lens_host,
                        return (x.z - x.y) > (y.z - y.y);
                      });
   }
-  const size_t need = items.size() + reds.size();
+  const size_t need = items.size() + reds.size() + glist.size() / 4;
   hipError_t e = hipSuccess;
   if (pl->uploaded) e = hipEventSynchronize(pl->uploaded);
   if (e == hipSuccess && need > pl->cap) {
@@ -2373,6 +2479,8 @@ int plan_build(rvkv_decode_plan *pl, const uint32_t *ctx_lens_host,
   if (e != hipSuccess) return hip_fail(op, e);
   std::copy(items.begin(), items.end(), pl->h_buf);
   std::copy(reds.begin(), reds.end(), pl->h_buf + items.size());
+  std::memcpy(pl->h_buf + items.size() + reds.size(), glist.data(),
+              glist.size() * sizeof(uint32_t));
   e = hipMemcpyAsync(pl->d_buf, pl->h_buf, need * sizeof(uint4),
                      hipMemcpyHostToDevice, pool->stream);
   if (e == hipSuccess) e = hipEventRecord(pl->uploaded, pool->stream);

@@ -570,6 +570,18 @@ def test_config_qwen25_ragged_prefix_cow():
     rng = np.random.default_rng(0)
     sample = sorted(set(sharers[:6]) | set(rng.choice(db.batch, 6).tolist()))
     assert _decode_vs_oracle(st, 1, db, q, sample=sample) < ATOL
+    # The benchmark's path: the plan built with the host tables (shared
+    # prefix blocks read by group items on the matrix cores).
+    from rvllm_amd.kv_storage import HipDecodePlan
+    plan = HipDecodePlan(st, db.ctx_lens, c.n_heads)
+    plan.update(db.ctx_lens, db.padded_tables())
+    out = st.paged_decode_planned(1, plan, q, dev_u32(db.padded_tables()),
+                                  dev_u32(db.ctx_lens)).cpu().numpy()
+    cache, padded, mb = oracle_subset(st, 1, [db.tables[b] for b in sample],
+                                      db.ctx_lens[sample])
+    want = orc.paged_decode_f64(cache, q.cpu().numpy()[sample],
+                                padded.reshape(-1), mb, db.ctx_lens[sample])
+    assert np.abs(out[sample] - want).max() < ATOL
 
 
 # ---- planned decode (ragged batches) --------------------------------------
@@ -730,9 +742,11 @@ def test_decode_masked_slots_hold_inf(G, hd):
 @pytest.mark.parametrize("G", [2, 7])
 def test_planned_decode_shared_prefix_order(G):
     """A plan updated with the host block tables orders the items of
-    prefix sharers back to back; the outputs are bitwise those of the plan
-    built from the lengths alone, and match the oracle. G 7: matrix-core
-    decode."""
+    prefix sharers back to back and match the oracle. G 2 (VALU decode):
+    bitwise the outputs of the plan built from the lengths alone. G 7
+    (matrix-core decode): the sharers' common blocks become group items
+    read once for up to four sharers, so the partition (and the summation
+    order) differs: within 5e-4 of the lengths-only plan."""
     from rvllm_amd.kv_storage import HipDecodePlan
     bs, nkv, hd = 32, 2, 64
     rng = np.random.default_rng(G)
@@ -761,13 +775,115 @@ def test_planned_decode_shared_prefix_order(G):
     ctx = dev_u32(lens)
     plan = HipDecodePlan(st, lens, G * nkv)
     a = st.paged_decode_planned(0, plan, q, tab, ctx).clone()
+    ws_plain = plan.workspace_bytes
     plan.update(lens, db.padded_tables())
     b = st.paged_decode_planned(0, plan, q, tab, ctx)
-    assert torch.equal(a, b)
+    if G < 5:
+        assert torch.equal(a, b)
+    else:
+        # the group partials are extra partitions of their members
+        assert plan.workspace_bytes > ws_plain
+        assert (a - b).abs().max().item() < 5e-4
     cache, padded, mb = oracle_subset(st, 0, tables, lens)
     want = orc.paged_decode_f64(cache, q.cpu().numpy(), padded.reshape(-1),
                                 mb, lens)
     assert np.abs(b.cpu().numpy() - want).max() < ATOL
+
+
+@pytest.mark.parametrize("G", [5, 7, 8, 16])
+def test_planned_decode_prefix_groups(G):
+    """Matrix-core decode with shared-prefix group items (up to 32 // G
+    sharers per item). Sharers of two prefixes, with members whose common
+    part ends mid-prefix (a private block replaces a shared one), members
+    shorter than the prefix, sequences sharing only their first block (no
+    group), long members whose own range is split, and one empty sequence.
+    The planned decode, the fused decode step (uniform plan rebuilt with
+    tables) and a second update all match the oracle; the fused step's
+    cache bits equal rvkv_append's."""
+    from rvllm_amd.kv_storage import HipDecodePlan
+    print(f"\n[gpu] prefix groups G={G}", flush=True)
+    bs, nkv, hd = 32, 2, 64
+    rng = np.random.default_rng(100 + G)
+    n = 48
+    lens = rng.integers(300, 5000, n).astype(np.uint32)
+    lens[5] = 0
+    lens[6:9] = [400, 700, 260]
+    prefixes = [rng.permutation(300)[:48].astype(np.uint32),
+                300 + rng.permutation(300)[:40].astype(np.uint32)]
+    free = list(range(600, 600 + 9000))
+    tables = []
+    for b in range(n):
+        nb = -(-int(lens[b]) // bs)
+        pref = prefixes[0] if b < 20 else prefixes[1] if b < 34 else None
+        cut = None
+        if b in (3, 22):  # the common part ends at block 9 / 17
+            cut = 9 if b == 3 else 17
+        if b in (40, 41):  # only the first block in common
+            pref, cut = prefixes[1], 1
+        t = []
+        for i in range(nb):
+            last = (i + 1) * bs >= lens[b]  # the block the append writes
+            if (pref is not None and i < len(pref) and not last and
+                    (cut is None or i < cut)):
+                t.append(int(pref[i]))
+            else:
+                t.append(free.pop(rng.integers(len(free))))
+        tables.append(np.array(t, np.uint32))
+    num_blocks = 600 + 9000
+    H = G * nkv
+    cfg = W.Config("pfg", 9, 1, H, nkv, hd, bs, n)
+    db = W.DecodeBatch(cfg, num_blocks, lens, tables,
+                       np.zeros(n, np.uint32), np.zeros(n, np.uint32))
+    st = HipKvStorage(1, num_blocks, bs, nkv, hd)
+    fill_layer(st, 0, seed=G)
+    q = torch.randn(n, H, hd, device="cuda")
+    padded_host = db.padded_tables()
+    tab = dev_u32(padded_host)
+    ctx = dev_u32(lens)
+    plan = HipDecodePlan(st, lens, H)
+    plain = st.paged_decode_planned(0, plan, q, tab, ctx).clone()
+    ws_plain = plan.workspace_bytes
+    plan.update(lens, padded_host)
+    assert plan.workspace_bytes > ws_plain  # groups were formed
+    got = st.paged_decode_planned(0, plan, q, tab, ctx)
+    live = [b for b in range(n) if lens[b]]
+    cache, padded, mb = oracle_subset(st, 0, [tables[b] for b in live],
+                                      lens[live])
+    want = orc.paged_decode_f64(cache, q.cpu().numpy()[live],
+                                padded.reshape(-1), mb, lens[live])
+    assert np.abs(got.cpu().numpy()[live] - want).max() < ATOL
+    assert np.abs(plain.cpu().numpy()[live] - want).max() < ATOL
+    assert not got[5].any()
+    assert (got - plain).abs().max().item() < 5e-4
+    # Fused decode step under the grouped plan: append at position n - 1.
+    last_b = np.array([t[(int(x) - 1) // bs] if x else 0
+                       for t, x in zip(tables, lens)], np.uint32)
+    last_o = np.array([(int(x) - 1) % bs if x else bs for x in lens],
+                      np.uint32)
+    nk = torch.randn(n, nkv, hd, device="cuda")
+    nv = torch.randn(n, nkv, hd, device="cuda")
+    ref = HipKvStorage(1, num_blocks, bs, nkv, hd)
+    fill_layer(ref, 0, seed=G)
+    ref.write_tokens(0, dev_u32(last_b), dev_u32(last_o), nk, nv)
+    step = st.decode_step(0, nk, nv, dev_u32(last_b), dev_u32(last_o), q,
+                          tab, ctx, int(lens.max()), plan=plan)
+    ids = dev_u32(np.unique(last_b))
+    for w in (0, 1):
+        assert torch.equal(st.read_blocks(0, w, ids), ref.read_blocks(0, w, ids))
+    after = ref.paged_decode_planned(0, HipDecodePlan(ref, lens, H), q, tab,
+                                     ctx)
+    assert (step - after).abs().max().item() < 5e-4
+    # A later step: every sequence one token longer, plan updated in place.
+    lens2 = np.where(lens > 0, lens + 1, 0).astype(np.uint32)
+    ok2 = all(-(-int(x) // bs) <= len(t) for t, x in zip(tables, lens2))
+    if ok2:
+        plan.update(lens2, padded_host)
+        got2 = st.paged_decode_planned(0, plan, q, tab, dev_u32(lens2))
+        fresh = st.paged_decode_planned(0, HipDecodePlan(st, lens2, H), q,
+                                        tab, dev_u32(lens2))
+        assert (got2 - fresh).abs().max().item() < 5e-4
+    ref.close()
+    st.close()
 
 
 def test_planned_decode_update_reuses_plan():
@@ -865,8 +981,8 @@ def test_decode_step_equals_append_then_decode(planned, src, G, hd, bs,
                                   (3, 64), (6, 64)])
 def test_decode_step_short_items(planned, G, hd):
     """Contexts all under 192 tokens: the launch shape for short items (four
-    waves of two loads per chunk for groups of up to four heads, two waves
-    of four otherwise). The fused step leaves the cache bits of
+    waves of two loads per chunk for groups of up to four
+    heads, two waves of four otherwise). The fused step leaves the cache bits of
     append-then-decode and matches it and the oracle."""
     from rvllm_amd.kv_storage import HipDecodePlan
     nkv, bs = 2, 16
