@@ -889,21 +889,42 @@ def run_churn(args, torch, W):
     batch = args.batch or c.batch
     drv = ChurnDriver(c, batch, 1024, prompt_len=64, churn=0.10,
                       steps=args.warmup + args.steps + 1)
+    # A serving loop's host: the objects made at start-up leave the garbage
+    # collector's view, so a full collection during the run does not stall
+    # the step it lands in (one such pause measured 36 ms).
+    import gc
+    gc.collect()
+    gc.freeze()
     for _ in range(args.warmup):
         drv.step()
     evs = [torch.cuda.Event(enable_timing=True)
            for _ in range(args.steps + 1)]
     torch.cuda.synchronize()
     b0 = drv.bytes_moved
+    step_bytes_each = []
     t0 = time.perf_counter()
     evs[0].record()
     for i in range(args.steps):
+        b_before = drv.bytes_moved
         drv.step()
+        step_bytes_each.append(drv.bytes_moved - b_before)
         evs[i + 1].record()
     torch.cuda.synchronize()
     dt = (time.perf_counter() - t0) / args.steps
-    step_median_ms = float(np.median([evs[i].elapsed_time(evs[i + 1])
-                                      for i in range(args.steps)]))
+    step_ms = [evs[i].elapsed_time(evs[i + 1]) for i in range(args.steps)]
+    step_median_ms = float(np.median(step_ms))
+    # The run in five phases of consecutive steps: GPU time (step events)
+    # and bytes, so the long-context start and the short-context end show.
+    phases = []
+    for idx in np.array_split(np.arange(args.steps), 5):
+        if len(idx) == 0:
+            continue
+        ms = float(np.sum([step_ms[i] for i in idx]))
+        by = float(np.sum([step_bytes_each[i] for i in idx]))
+        phases.append({"steps": f"{int(idx[0])}-{int(idx[-1])}",
+                       "ms_per_step": round(ms / len(idx), 4),
+                       "GB_per_step": round(by / len(idx) / 1e9, 4),
+                       "GB/s": round(by / (ms * 1e-3) / 1e9, 1)})
     step_bytes = (drv.bytes_moved - b0) / args.steps
     # Per-launch decode time at the final state (back-to-back over layers).
     st, plan = drv.st, drv.plan
@@ -932,6 +953,7 @@ def run_churn(args, torch, W):
         "warmup": args.warmup,
         "ms_per_step": round(dt * 1e3, 4),
         "ms_per_step_median": round(step_median_ms, 4),
+        "phases": phases,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -1025,7 +1047,7 @@ def _sub_args(args, **kw):
 def _secondary(res, role):
     """The part of a workload's record a secondary entry keeps."""
     keep = ("metric", "value", "unit", "steps", "warmup", "ms_per_step",
-            "ms_per_step_median", "dtype", "config", "pct_of_peak",
+            "ms_per_step_median", "phases", "dtype", "config", "pct_of_peak",
             "tok_per_s", "roofline")
     out = {"role": role}
     out.update({k: res[k] for k in keep if k in res})

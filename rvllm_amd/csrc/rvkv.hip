@@ -2277,16 +2277,41 @@ int plan_build(rvkv_decode_plan *pl, const uint32_t *ctx_lens_host,
   const double hi_p = (double)total * n_hy / (256.0 * per);
   double want = avg < lo_p ? lo_p : avg;
   if (want > hi_p) want = hi_p;
-  uint32_t P = 256;
+  // Item boundaries: multiples of 256 tokens on the matrix-core decode
+  // (its 32/64-key tiles and block-id prefetch assume them); on the VALU
+  // decode multiples of 64 (any multiple of a wave-wide load's tokens
+  // works), and items down to 128 tokens, so that in a batch of mostly short
+  // sequences a few long ones are cut into items near the typical length
+  // instead of setting the launch's tail (RVKV_DECODE_PLAN_GRAN = 64 or 256
+  // overrides the VALU granule).
+  static const uint32_t forced_gran = env_u32("RVKV_DECODE_PLAN_GRAN");
+  const uint32_t gran =
+      mfma ? 256u : (forced_gran == 64 || forced_gran == 256 ? forced_gran
+                                                             : 64u);
+  uint32_t P = gran == 256 ? 256 : 128;
   while (P < want && P < (1u << 30)) P <<= 1;
 
   // Items of at most P tokens over [start, n), with 1/8 slack so a range
   // just past a multiple of P does not get a sliver item; split evenly on
-  // 256-token boundaries. Returns the count and the step.
+  // gran-token boundaries. Returns the count and the step.
+  // VALU decode: a sequence up to four times the average length (and up to
+  // 2P, within the >= ~256-workgroup bound) stays one item. Splitting it
+  // costs the reduction launch, and a moderately long item that starts
+  // first (longest first) finishes in the launch's tail, when the bandwidth
+  // is its own; the few long survivors of a churning batch are still cut
+  // into items near the typical length.
+  const uint32_t whole_max =
+      mfma ? 0u
+           : (uint32_t)std::min(std::min(4.0 * (double)total / batch, hi_p),
+                                2.0 * P);
   auto split = [&](uint32_t start, uint32_t n, uint32_t *step_out) {
     const uint32_t span = n - start;
+    if (span <= whole_max) {
+      *step_out = span;
+      return 1u;
+    }
     uint32_t k = div_up(span, P + P / 8);
-    const uint32_t step = ((div_up(span, k) + 255u) & ~255u);
+    const uint32_t step = (div_up(span, k) + gran - 1) / gran * gran;
     *step_out = step;
     return div_up(span, step);
   };
@@ -2375,7 +2400,7 @@ int plan_build(rvkv_decode_plan *pl, const uint32_t *ctx_lens_host,
     }
     const uint32_t lo = (window > 0 && n > (uint32_t)window) ? n - window : 0;
     const bool grouped = gidx[b] != 0xFFFFFFFFu;
-    const uint32_t start = grouped ? gstart[b] : lo & ~255u;
+    const uint32_t start = grouped ? gstart[b] : lo / gran * gran;
     const uint32_t pre = grouped ? gpieces[gidx[b]] : 0;
     uint32_t step;
     const uint32_t k = split(start, n, &step);
@@ -2463,14 +2488,16 @@ int plan_build(rvkv_decode_plan *pl, const uint32_t *ctx_lens_host,
   hipError_t e = hipSuccess;
   if (pl->uploaded) e = hipEventSynchronize(pl->uploaded);
   if (e == hipSuccess && need > pl->cap) {
-    // Growing: the old device list may still be read by queued decodes.
+    // Growing (rare: the first build reserves room for two items per
+    // sequence): the old device list may still be read by queued decodes.
     if (pl->d_buf) e = hipStreamSynchronize(pool->stream);
     if (e == hipSuccess && pl->d_buf) e = hipFree(pl->d_buf);
     if (e == hipSuccess && pl->h_buf) e = hipHostFree(pl->h_buf);
     pl->d_buf = nullptr;
     pl->h_buf = nullptr;
     pl->cap = 0;
-    const size_t cap = need + need / 4 + 16;
+    const size_t cap =
+        std::max<size_t>(need + need / 4 + 16, 2 * (size_t)batch + 64);
     if (e == hipSuccess) e = hipMalloc(&pl->d_buf, cap * sizeof(uint4));
     if (e == hipSuccess) e = hipHostMalloc(&pl->h_buf, cap * sizeof(uint4));
     if (e == hipSuccess) pl->cap = cap;
