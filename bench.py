@@ -564,6 +564,9 @@ def run_engine(args, torch, W):
         tail = rng.integers(0, mcfg.vocab, prompt - len(head)).tolist()
         specs.append(RequestSpec(head + tail, new_tok))
     ecfg = EngineConfig(block_size=bs, num_blocks=num_blocks)
+    import gc
+    gc.collect()
+    gc.freeze()  # start-up objects out of the collector's view (as churn)
     for _ in range(max(args.warmup, 1)):
         run(backend, specs[:4], ecfg)
     torch.cuda.synchronize()
@@ -793,18 +796,21 @@ def run_prep(args, torch, W):
     print(json.dumps(res), flush=True)
 
 
-def run_prefill(args, torch, W):
+def run_prefill(args, torch, W, st=None):
     """Scatter-only prefill append: every sequence's ctx tokens (K and V
     rows [tokens, n_kv, hd] of the source dtype) appended into its
     block-table slots, one rvkv_append per layer (the slot lists are built
     once, like the engine's write_positions). The source rows are one
     device buffer reused by every layer (each layer's write goes to its own
-    pool, and the source is far larger than the 256 MB MALL)."""
+    pool, and the source is far larger than the 256 MB MALL). st: an
+    existing pool of this workload's shape to write into (kept open)."""
     from rvllm_amd.kv_storage import HipKvStorage
     db = build_workload(W, args.config, args.batch, args.ctx)
     c = db.cfg
-    st = HipKvStorage(c.n_layers, db.num_blocks, c.block_size, c.n_kv_heads,
-                      c.head_dim)
+    own = st is None
+    if own:
+        st = HipKvStorage(c.n_layers, db.num_blocks, c.block_size,
+                          c.n_kv_heads, c.head_dim)
     bs = c.block_size
     sb, so, _ = prompt_slots(torch, db)
     n_tok = sb.numel()
@@ -871,7 +877,8 @@ def run_prefill(args, torch, W):
             "avg_launch_ms": round(launch_ms, 5),
         },
     }
-    st.close()
+    if own:
+        st.close()
     del k, v, sb, so
     torch.cuda.empty_cache()
     return with_copy_ceiling(torch, res, src_bytes / (src_bytes + 2),
@@ -928,7 +935,8 @@ def run_churn(args, torch, W):
     step_bytes = (drv.bytes_moved - b0) / args.steps
     # Per-launch decode time at the final state (back-to-back over layers).
     st, plan = drv.st, drv.plan
-    db = drv.devb[(drv.step_index - 1) & 1]
+    from rvllm_amd.engine_sim import NSTAGE
+    db = drv.devb[(drv.step_index - 1) % NSTAGE]
     lens = drv.last[1]
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
@@ -1030,18 +1038,26 @@ def main():
     if args.cow:
         run_cow(args, torch, W)
         return
-    res = run_decode(args, torch, W, cpu=not args.no_cpu)
-    if (args.secondary and args.config == "qwen3-0.6b" and not args.batch
-            and not args.ctx):
-        res["secondary"] = secondary_records(args, torch, W)
+    secondary = (args.secondary and args.config == "qwen3-0.6b"
+                 and not args.batch and not args.ctx and not args.f32_cache
+                 and not args.unfused and not args.graph and args.plan is None)
+    res = run_decode(args, torch, W, cpu=not args.no_cpu, keep_pool=secondary)
+    if secondary:
+        # configs[2]'s prefill append into the headline's own pool (the
+        # same Qwen3 shape): a second 112 GiB pool is never made.
+        st = res.pop("_pool")
+        pre = run_prefill(argparse.Namespace(**{
+            **vars(args), "config": "qwen3-0.6b", "batch": 0, "ctx": 0,
+            "prefill": "f32", "steps": max(args.steps // 2, 5),
+            "warmup": min(args.warmup, 2)}), torch, W, st=st)
+        st.close()
+        torch.cuda.empty_cache()
+        pre = _secondary(pre, "configs[2] prefill append (scatter only, f32 "
+                              "source rows), into the headline's pool")
+        pre["command"] = ("python3 bench.py (after the headline, same "
+                          "process); alone: python3 bench.py --prefill f32")
+        res["secondary"] = secondary_records(args, torch, W) + [pre]
     print(json.dumps(res), flush=True)
-
-
-def _sub_args(args, **kw):
-    """A copy of the command-line arguments with some fields replaced."""
-    d = dict(vars(args))
-    d.update(kw)
-    return argparse.Namespace(**d)
 
 
 def _secondary(res, role):
@@ -1054,36 +1070,54 @@ def _secondary(res, role):
     return out
 
 
+PAUSE_AFTER_FREE_S = 15.0
+
+
+def _child_record(args, extra):
+    """Runs bench.py with `extra` arguments in a child process (a fresh
+    process, as a separate bench invocation would be) and returns its JSON
+    record. The parent has freed its own pools before this."""
+    import subprocess
+    cmd = [sys.executable, os.path.abspath(__file__), "--no-cpu"] + extra
+    p = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+    if p.returncode != 0:
+        raise SystemExit(f"secondary run {' '.join(extra)} failed "
+                         f"({p.returncode}): {p.stderr[-2000:]}")
+    return json.loads(p.stdout.strip().splitlines()[-1])
+
+
 def secondary_records(args, torch, W):
-    """The rest of the north star's target workloads, run after the
-    headline in the same process (as rvllm's bench sweeps its workloads in
-    one invocation): the Llama-3.2-1B shape at 256 x 4096, configs[2]'s
-    prefill append (f32 source rows, scatter only) and configs[4]'s
-    200-step churn. Each pool is freed before the next is made."""
+    """The rest of the north star's target workloads, run within the same
+    bench invocation as the headline (as rvllm's bench sweeps its workloads
+    in one run), each in a child process of its own: configs[4]'s 200-step
+    churn and the Llama-3.2-1B shape at 256 x 4096. (configs[2]'s prefill
+    append runs in this process, on the headline's pool.)"""
+    jobs = [
+        (["--churn", "--steps", "200", "--warmup", "3"],
+         "configs[4] churn, 200 engine steps"),
+        (["--config", "llama-3.2-1b", "--batch", "256", "--ctx", "4096",
+          "--steps", str(args.steps), "--warmup", str(args.warmup)],
+         "north-star shape 2: Llama-3.2-1B, 256 seqs x 4096 tokens, fused "
+         "decode step"),
+    ]
     out = []
-    steps = max(args.steps // 2, 5)
-    r = run_decode(_sub_args(args, config="llama-3.2-1b", batch=256,
-                             ctx=4096, plan=None, unfused=False), torch, W,
-                   cpu=False)
-    out.append(_secondary(r, "north-star shape 2: Llama-3.2-1B, 256 seqs "
-                             "x 4096 tokens, fused decode step"))
-    torch.cuda.empty_cache()
-    r = run_prefill(_sub_args(args, config="qwen3-0.6b", batch=0, ctx=0,
-                              prefill="f32", steps=steps,
-                              warmup=min(args.warmup, 2)), torch, W)
-    out.append(_secondary(r, "configs[2] prefill append (scatter only, "
-                             "f32 source rows)"))
-    torch.cuda.empty_cache()
-    r = run_churn(_sub_args(args, config="gemma-3-270m", batch=0, ctx=0,
-                            steps=200, warmup=3), torch, W)
-    out.append(_secondary(r, "configs[4] churn, 200 engine steps"))
-    torch.cuda.empty_cache()
+    for extra, role in jobs:
+        # A workload started within ~10 s of a large pool's release ran
+        # 10-20 % slower (the churn: 0.84 vs 0.72 ms per step right after
+        # the 112 GiB pool was freed, 0.72 after 10, 25 or 45 s); each run
+        # starts after a pause.
+        time.sleep(PAUSE_AFTER_FREE_S)
+        rec = _child_record(args, extra)
+        rec = _secondary(rec, role)
+        rec["command"] = "python3 bench.py --no-cpu " + " ".join(extra)
+        out.append(rec)
     return out
 
 
-def run_decode(args, torch, W, cpu):
+def run_decode(args, torch, W, cpu, keep_pool=False):
     """The decode step of --config (append + paged decode per layer, fused
-    by default) timed over --steps; returns the record."""
+    by default) timed over --steps; returns the record (keep_pool: the pool
+    is left open, in record["_pool"])."""
     from rvllm_amd.kv_storage import HipKvStorage
     db = build_workload(W, args.config, args.batch, args.ctx)
     c = db.cfg
@@ -1274,7 +1308,10 @@ def run_decode(args, torch, W, cpu):
                                              f32=f32)
     if plan is not None:
         plan.close()
-    st.close()
+    if keep_pool:
+        res["_pool"] = st
+    else:
+        st.close()
     return res
 
 

@@ -204,8 +204,10 @@ int rvkv_decode_plan_create(const rvkv_pool *pool,
                             rvkv_decode_plan **out);
 /* Rebuilds the plan in place for this step's context lengths (same n_heads
  * and window; batch may change), reusing its device and pinned buffers
- * unless the work list outgrows them. Waits only for the plan's own previous
- * upload. The plan keeps a pointer to the pool: destroy it first. */
+ * unless the work list outgrows them. Waits only for the plan's own upload
+ * three updates back (its pinned staging is used in turn), so a host loop
+ * can build up to three steps ahead of the device. The plan keeps a pointer
+ * to the pool: destroy it first. */
 int rvkv_decode_plan_update(rvkv_decode_plan *plan,
                             const uint32_t *ctx_lens_host, uint32_t batch);
 /* rvkv_decode_plan_update with the host copy of this step's padded block

@@ -2215,10 +2215,15 @@ struct rvkv_decode_plan {
   int32_t window;
   uint32_t part_tokens, n_items, n_reds, n_slots, avg_tokens = 0,
       max_tokens = 0;
-  uint4 *d_buf = nullptr;   // items, then reduction rows (device)
-  uint4 *h_buf = nullptr;   // pinned staging copy of the same
-  size_t cap = 0;           // entries both buffers hold
-  hipEvent_t uploaded = nullptr;  // last upload done: staging is free
+  uint4 *d_buf = nullptr;   // items, reduction rows, group lists (device)
+  // Pinned staging copies of the same, used in turn: an update waits only
+  // for the upload kNStage updates back, so the host can build a few steps
+  // ahead of the device (stream order protects d_buf).
+  static constexpr int kNStage = 3;
+  uint4 *h_buf[kNStage] = {};
+  hipEvent_t uploaded[kNStage] = {};  // upload from h_buf[i] done
+  int next = 0;             // staging buffer the next update fills
+  size_t cap = 0;           // entries every buffer holds
   size_t acc_off, ml_off, ws_bytes;
 };
 
@@ -2486,32 +2491,40 @@ int plan_build(rvkv_decode_plan *pl, const uint32_t *ctx_lens_host,
   }
   const size_t need = items.size() + reds.size() + glist.size() / 4;
   hipError_t e = hipSuccess;
-  if (pl->uploaded) e = hipEventSynchronize(pl->uploaded);
+  const int si = pl->next;
+  if (pl->uploaded[si]) e = hipEventSynchronize(pl->uploaded[si]);
   if (e == hipSuccess && need > pl->cap) {
     // Growing (rare: the first build reserves room for two items per
     // sequence): the old device list may still be read by queued decodes.
     if (pl->d_buf) e = hipStreamSynchronize(pool->stream);
     if (e == hipSuccess && pl->d_buf) e = hipFree(pl->d_buf);
-    if (e == hipSuccess && pl->h_buf) e = hipHostFree(pl->h_buf);
+    for (int i = 0; i < rvkv_decode_plan::kNStage; ++i) {
+      if (e == hipSuccess && pl->h_buf[i]) e = hipHostFree(pl->h_buf[i]);
+      pl->h_buf[i] = nullptr;
+    }
     pl->d_buf = nullptr;
-    pl->h_buf = nullptr;
     pl->cap = 0;
     const size_t cap =
         std::max<size_t>(need + need / 4 + 16, 2 * (size_t)batch + 64);
     if (e == hipSuccess) e = hipMalloc(&pl->d_buf, cap * sizeof(uint4));
-    if (e == hipSuccess) e = hipHostMalloc(&pl->h_buf, cap * sizeof(uint4));
+    for (int i = 0; i < rvkv_decode_plan::kNStage; ++i)
+      if (e == hipSuccess)
+        e = hipHostMalloc(&pl->h_buf[i], cap * sizeof(uint4));
     if (e == hipSuccess) pl->cap = cap;
   }
-  if (e == hipSuccess && !pl->uploaded) e = hipEventCreate(&pl->uploaded);
+  if (e == hipSuccess && !pl->uploaded[si])
+    e = hipEventCreateWithFlags(&pl->uploaded[si], hipEventDisableTiming);
   if (e != hipSuccess) return hip_fail(op, e);
-  std::copy(items.begin(), items.end(), pl->h_buf);
-  std::copy(reds.begin(), reds.end(), pl->h_buf + items.size());
-  std::memcpy(pl->h_buf + items.size() + reds.size(), glist.data(),
+  uint4 *h = pl->h_buf[si];
+  std::copy(items.begin(), items.end(), h);
+  std::copy(reds.begin(), reds.end(), h + items.size());
+  std::memcpy(h + items.size() + reds.size(), glist.data(),
               glist.size() * sizeof(uint32_t));
-  e = hipMemcpyAsync(pl->d_buf, pl->h_buf, need * sizeof(uint4),
+  e = hipMemcpyAsync(pl->d_buf, h, need * sizeof(uint4),
                      hipMemcpyHostToDevice, pool->stream);
-  if (e == hipSuccess) e = hipEventRecord(pl->uploaded, pool->stream);
+  if (e == hipSuccess) e = hipEventRecord(pl->uploaded[si], pool->stream);
   if (e != hipSuccess) return hip_fail(op, e);
+  pl->next = (si + 1) % rvkv_decode_plan::kNStage;
 
   pl->batch = batch;
   pl->max_ctx = max_ctx;
@@ -2763,9 +2776,11 @@ void rvkv_decode_plan_destroy(rvkv_decode_plan *plan) {
   if (!plan) return;
   // Decodes queued with this plan may still read its device list.
   (void)hipStreamSynchronize(plan->pool->stream);
-  if (plan->uploaded) (void)hipEventDestroy(plan->uploaded);
+  for (int i = 0; i < rvkv_decode_plan::kNStage; ++i) {
+    if (plan->uploaded[i]) (void)hipEventDestroy(plan->uploaded[i]);
+    if (plan->h_buf[i]) (void)hipHostFree(plan->h_buf[i]);
+  }
   if (plan->d_buf) (void)hipFree(plan->d_buf);
-  if (plan->h_buf) (void)hipHostFree(plan->h_buf);
   delete plan;
 }
 

@@ -12,8 +12,9 @@ for the gemma-3-270m churn workload:
   rvkv_decode_step per layer runs under a decode plan rebuilt from the
   host-side token counts (the per-forward GatherPlan).
 
-Host bookkeeping of step s+1 overlaps the GPU work of step s. The host
-arrays go through pinned, double-buffered staging and non-blocking uploads.
+Host bookkeeping of the next steps overlaps the GPU work of step s. The
+host arrays go through pinned staging used in turn (three sets, as the
+decode plan's own staging) and non-blocking uploads.
 K/V/q contents are synthetic (seeded device RNG); only the bookkeeping and
 the data movement are real.
 """
@@ -28,6 +29,8 @@ from ._lib import RVKV_F32, check
 from .block_manager import BlockManager
 from .kv_storage import HipDecodePlan, HipKvStorage
 from .workloads import Config, Rng, append_bytes
+
+NSTAGE = 3  # host staging sets (the decode plan keeps as many)
 
 
 class ChurnDriver:
@@ -73,15 +76,16 @@ class ChurnDriver:
         self._nk_p = [P(t.data_ptr()) for t in self.nk]
         self._nv_p = [P(t.data_ptr()) for t in self.nv]
         self._out_p = [P(t.data_ptr()) for t in self.out]
-        # Double-buffered pinned staging + device copies of the step arrays.
+        # Pinned staging + device copies of the step arrays, NSTAGE sets used
+        # in turn, so the host can prepare a few steps ahead of the device.
         mb = self.max_blocks
         shapes = {"tables": (batch, mb), "ctx": (batch,), "sb": (batch,),
                   "so": (batch,), "pb": (n_prompt,), "po": (n_prompt,)}
         self.host = [{k: torch.empty(s, dtype=torch.int32, pin_memory=True)
-                      for k, s in shapes.items()} for _ in range(2)]
+                      for k, s in shapes.items()} for _ in range(NSTAGE)]
         self.devb = [{k: torch.empty(s, dtype=torch.int32, device=dev)
-                      for k, s in shapes.items()} for _ in range(2)]
-        self.copied = [torch.cuda.Event(), torch.cuda.Event()]
+                      for k, s in shapes.items()} for _ in range(NSTAGE)]
+        self.copied = [torch.cuda.Event() for _ in range(NSTAGE)]
         self.plan = None
         self.step_index = 0
         self.bytes_moved = 0
@@ -107,7 +111,7 @@ class ChurnDriver:
     def step(self) -> None:
         """One engine step: finish + admit (prefill append), then decode."""
         c, bm, st = self.cfg, self.bm, self.st
-        i = self.step_index & 1
+        i = self.step_index % NSTAGE
         hb, db = self.host[i], self.devb[i]
         self.copied[i].synchronize()  # staging i is free again
         bs = c.block_size
