@@ -145,23 +145,78 @@ def read_ceiling(torch, nbytes, steps):
             for _ in range(n_buf)]
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
-    def sweep():
+    def sweep(wg):
         for b in bufs:
             _lib.check_calib(lib.rvkv_calib_read_probe(
-                ctypes.c_void_p(b.data_ptr()), nb, 0, None, stream))
-    sweep()
-    torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(steps):
-        sweep()
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / (steps * n_buf)
+                ctypes.c_void_p(b.data_ptr()), nb, wg, None, stream))
+
+    # The best workgroup count depends on the size: the best of three.
+    best = None
+    for wg in (2048, 16384, 65536):
+        sweep(wg)
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            sweep(wg)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / (steps * n_buf)
+        if best is None or ms < best[0]:
+            best = (ms, wg)
     del bufs
+    ms, wg = best
     return {"bytes_per_launch": nb, "avg_launch_ms": round(ms, 5),
-            "GB/s": round(nb / (ms * 1e-3) / 1e9, 2)}
+            "GB/s": round(nb / (ms * 1e-3) / 1e9, 2), "workgroups": wg}
+
+
+def paged_ceiling(torch, nbytes, tile_bytes, steps):
+    """The plain read of a paged layer: every tile (tile_bytes, one
+    (block, head) tile of the cache) of a buffer of `nbytes` read once in a
+    random order, as a decode reads a randomly permuted pool, one wave per
+    workgroup with eight 1 KB loads in flight, nothing computed (the paged
+    probe). Buffers rotate so no launch finds its data in the MALL; the best
+    of two workgroup counts."""
+    import ctypes
+
+    from rvllm_amd import _lib
+    lib = _lib.load_calib()
+    n_ids = max(1, int(nbytes) // tile_bytes)
+    nb = n_ids * tile_bytes
+    n_buf = max(2, -(-(3 << 29) // nb))
+    bufs = [torch.zeros(nb // 4, dtype=torch.int32, device="cuda")
+            for _ in range(n_buf)]
+    rng = np.random.default_rng(7)
+    ids = [torch.from_numpy(rng.permutation(n_ids).astype(np.int32)).cuda()
+           for _ in range(n_buf)]
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def sweep(wg):
+        for b, t in zip(bufs, ids):
+            _lib.check_calib(lib.rvkv_calib_paged_probe(
+                ctypes.c_void_p(b.data_ptr()), tile_bytes,
+                ctypes.c_void_p(t.data_ptr()), n_ids, wg, stream))
+
+    best = None
+    for wg in (2048, 8192):
+        sweep(wg)
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            sweep(wg)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / (steps * n_buf)
+        if best is None or ms < best[0]:
+            best = (ms, wg)
+    del bufs, ids
+    ms, wg = best
+    return {"bytes_per_launch": nb, "tile_bytes": tile_bytes,
+            "avg_launch_ms": round(ms, 5),
+            "GB/s": round(nb / (ms * 1e-3) / 1e9, 2), "workgroups": wg}
 
 
 def copy_ceiling(torch, nbytes, read_frac, steps):
@@ -186,24 +241,30 @@ def copy_ceiling(torch, nbytes, read_frac, steps):
             for _ in range(n_buf)]
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
-    def sweep():
+    def sweep(wg):
         for a, b in zip(srcs, dsts):
             _lib.check_calib(lib.rvkv_calib_copy_probe(
                 ctypes.c_void_p(a.data_ptr()), ctypes.c_void_p(b.data_ptr()),
-                rd, wr, 65536, stream))
-    sweep()
-    torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(steps):
-        sweep()
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / (steps * n_buf)
+                rd, wr, wg, stream))
+
+    best = None
+    for wg in (16384, 65536):
+        sweep(wg)
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            sweep(wg)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / (steps * n_buf)
+        if best is None or ms < best[0]:
+            best = (ms, wg)
     del srcs, dsts
+    ms, wg = best
     return {"read_bytes": rd, "write_bytes": wr, "avg_launch_ms": round(ms, 5),
-            "GB/s": round((rd + wr) / (ms * 1e-3) / 1e9, 2)}
+            "GB/s": round((rd + wr) / (ms * 1e-3) / 1e9, 2), "workgroups": wg}
 
 
 def with_copy_ceiling(torch, res, read_frac, steps):
@@ -997,6 +1058,10 @@ def run_churn(args, torch, W):
     rc = read_ceiling(torch, dec_bytes, max(args.steps // 10, 3))
     rc["frac"] = round(achieved / rc["GB/s"], 4)
     res["roofline"]["stream_read_ceiling"] = rc
+    pc = paged_ceiling(torch, drv.decode_bytes(lens),
+                       c.block_size * c.head_dim * 2, max(args.steps // 10, 3))
+    pc["frac"] = round(achieved / pc["GB/s"], 4)
+    res["roofline"]["paged_read_ceiling"] = pc
     drv.close()
     return res
 
@@ -1298,10 +1363,17 @@ def run_decode(args, torch, W, cpu, keep_pool=False):
             "avg_launch_ms": round(dec_ms, 5),
         },
     }
-    # Context for frac: the best plain read of the same bytes per launch.
+    # Context for frac: the best plain read of the same bytes per launch,
+    # contiguous and as randomly placed cache tiles.
     rc = read_ceiling(torch, dec_bytes, max(args.steps, 3))
     rc["frac"] = round(achieved / rc["GB/s"], 4)
     res["roofline"]["stream_read_ceiling"] = rc
+    tile = c.block_size * c.head_dim * cell
+    if tile % 1024 == 0:
+        pc = paged_ceiling(torch, W.decode_bytes(db, cell), tile,
+                           max(args.steps // 2, 3))
+        pc["frac"] = round(achieved / pc["GB/s"], 4)
+        res["roofline"]["paged_read_ceiling"] = pc
     if cpu:
         from oracle import oracle as orc
         res["cpu_baseline"] = cpu_baseline(orc, W, st, db, args.cpu_seconds,

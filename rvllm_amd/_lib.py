@@ -150,6 +150,8 @@ def load_calib() -> ctypes.CDLL:
         L = ctypes.CDLL(path)
         L.rvkv_calib_read_probe.restype = _int
         L.rvkv_calib_read_probe.argtypes = [_P, _sz, _u32, _P, _P]
+        L.rvkv_calib_paged_probe.restype = _int
+        L.rvkv_calib_paged_probe.argtypes = [_P, _u32, _P, _u32, _u32, _P]
         L.rvkv_calib_copy_probe.restype = _int
         L.rvkv_calib_copy_probe.argtypes = [_P, _P, _sz, _sz, _u32, _P]
         L.rvkv_calib_last_error.restype = ctypes.c_char_p

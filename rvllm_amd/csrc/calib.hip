@@ -3,17 +3,18 @@
 // nothing else in the launch (no tables, no arithmetic worth the name).
 // It has no counterpart in rvllm; it exists so a paged-KV launch of B bytes
 // can be compared with the best plain read of B bytes on the same device
-// (and a byte mover with the best plain copy of its read and write bytes).
+// (and a byte mover with the best plain copy of its read and write bytes,
+// and a paged decode with a plain read of the same tiles in table order).
 // Built into its own librvkv_calib.so for the benchmark: it is not part of
 // the product ABI (include/rvkv.h).
 //
 // Each workgroup streams one contiguous slice with 16-byte non-temporal
 // loads, four in flight per lane, and folds them into a sum that is stored
 // only if it equals an impossible sentinel (so the loads are not optimised
-// away and nothing is written). The default of 16384 workgroups and the
-// non-temporal hint were the fastest plain read measured on this part
-// (6.6 TB/s over 4.3 GB, against 6.0 TB/s with plain loads and 2048
-// workgroups).
+// away and nothing is written). The non-temporal hint is worth ~10 % over
+// plain loads; the best workgroup count depends on the size (over 4.3 GB:
+// 7.0 TB/s at 2048, 6.5 at 8192, 6.6 at 16384, 7.2 at 65536), so callers
+// take the best of several.
 #include <hip/hip_runtime.h>
 
 #include <cstddef>
@@ -92,6 +93,42 @@ __global__ void __launch_bounds__(kReadThreads)
   }
 }
 
+// Paged read: one wave per workgroup streams its share of `tiles` (ids
+// into a buffer of tile_bytes tiles) with eight wave-wide 1 KB loads in
+// flight, non-temporal, nothing computed: the access pattern of a paged
+// decode (every (block, head) tile of a layer read once, in table order)
+// without its arithmetic.
+constexpr int kPagedUnroll = 8;
+__global__ void __launch_bounds__(64)
+    paged_probe_kernel(const char *__restrict__ base,
+                       const uint32_t *__restrict__ ids, uint32_t n_ids,
+                       uint32_t tiles_per_wg, uint32_t loads_per_tile,
+                       uint32_t tile_bytes, uint32_t *__restrict__ sink) {
+  typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+  typedef const __attribute__((address_space(4))) uint32_t cu32;
+  const uint32_t t0 = blockIdx.x * tiles_per_wg;
+  const uint32_t t1 = t0 + tiles_per_wg < n_ids ? t0 + tiles_per_wg : n_ids;
+  cu32 *t = (cu32 *)(uintptr_t)ids;
+  uint32_t acc = 0;
+  const uint32_t l_end = (t1 > t0 ? t1 - t0 : 0) * loads_per_tile;
+  for (uint32_t l0 = 0; l0 < l_end; l0 += kPagedUnroll) {
+    u32x4v v[kPagedUnroll];
+#pragma unroll
+    for (int u = 0; u < kPagedUnroll; ++u) {
+      const uint32_t l = l0 + u < l_end ? l0 + u : l_end - 1;
+      const uint32_t id = t[t0 + l / loads_per_tile];
+      const u32x4v *p = reinterpret_cast<const u32x4v *>(
+                            base + (size_t)id * tile_bytes +
+                            (size_t)(l % loads_per_tile) * 1024) +
+                        threadIdx.x;
+      v[u] = __builtin_nontemporal_load(p);
+    }
+#pragma unroll
+    for (int u = 0; u < kPagedUnroll; ++u) acc ^= v[u][0] ^ v[u][3];
+  }
+  if (acc == 0x9e3779b9u && sink) sink[0] = acc;
+}
+
 }  // namespace
 
 extern "C" {
@@ -111,6 +148,27 @@ int rvkv_calib_read_probe(const void *buf, size_t bytes, uint32_t workgroups,
   hipLaunchKernelGGL(read_probe_kernel, dim3(workgroups), dim3(kReadThreads),
                      0, reinterpret_cast<hipStream_t>(stream),
                      static_cast<const uint4 *>(buf), n16, per_wg, sink);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : calib_fail(hipGetErrorString(e));
+}
+
+// Reads n_ids tiles of tile_bytes (a multiple of 1024) at base + id *
+// tile_bytes, ids from a device table, in `workgroups` one-wave workgroups
+// (0: n_ids / 256). Returns 0, or -1 with the reason.
+int rvkv_calib_paged_probe(const void *base, uint32_t tile_bytes,
+                           const uint32_t *ids, uint32_t n_ids,
+                           uint32_t workgroups, void *stream) {
+  if (n_ids == 0) return 0;
+  if (!base || !ids) return calib_fail("base/ids is NULL");
+  if (tile_bytes == 0 || tile_bytes % 1024 || (uintptr_t)base % 16)
+    return calib_fail("tiles must be whole KiB, base 16-byte aligned");
+  if (workgroups == 0) workgroups = n_ids / 256 ? n_ids / 256 : 1;
+  const uint32_t per = (n_ids + workgroups - 1) / workgroups;
+  workgroups = (n_ids + per - 1) / per;
+  hipLaunchKernelGGL(paged_probe_kernel, dim3(workgroups), dim3(64), 0,
+                     reinterpret_cast<hipStream_t>(stream),
+                     static_cast<const char *>(base), ids, n_ids, per,
+                     tile_bytes / 1024, tile_bytes, nullptr);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? 0 : calib_fail(hipGetErrorString(e));
 }
