@@ -258,7 +258,9 @@ __global__ void __launch_bounds__(
   const uint32_t *gl = nullptr;
   uint32_t n_mem = 0;
   if (a.items) {  // decode items: grid (items, n_kv), plan order kept
-    const uint4 it = a.items[blockIdx.x];
+    typedef const __attribute__((address_space(4))) uint32_t cu32;
+    cu32 *itp = (cu32 *)(uintptr_t)(a.items + blockIdx.x);  // scalar loads
+    const uint4 it = make_uint4(itp[0], itp[1], itp[2], itp[3]);
     b = it.x;
     item_lo = it.y;
     item_hi = it.z;
@@ -291,9 +293,13 @@ __global__ void __launch_bounds__(
 
   // Decode: the one query row sits at position read_num - 1 (an empty
   // sequence wraps to 2^32 - 1 and sees no key).
-  const uint32_t off = a.items ? a.read_num[b] - 1u : a.pos_offset[b];
+  // (b is uniform: the per-sequence words come by scalar loads)
+  typedef const __attribute__((address_space(4))) uint32_t cu32s;
+  const uint32_t rn = *(cu32s *)(uintptr_t)(a.read_num + b);
+  const uint32_t off =
+      a.items ? rn - 1u : *(cu32s *)(uintptr_t)(a.pos_offset + b);
   const uint32_t cap = a.max_blocks << a.bs_log2;
-  const uint32_t ctx = min(a.read_num[b], cap);
+  const uint32_t ctx = min(rn, cap);
   const uint32_t *table = a.tables + (size_t)b * a.max_blocks;
 
   // Query rows of this (sequence, KV head): group * q_len, or a group

@@ -605,6 +605,20 @@ struct DecodeArgs {
 };
 
 constexpr uint32_t kNoSlot = 0xFFFFFFFFu;
+
+// A wave-uniform word read through the constant address space, so it is a
+// scalar load (the kernels also store to global memory, and through a plain
+// pointer the compiler may use vector loads). Only for inputs no kernel of
+// the launch writes.
+__device__ __forceinline__ uint32_t sload(const uint32_t *p) {
+  typedef const __attribute__((address_space(4))) uint32_t cu32;
+  return *(cu32 *)(uintptr_t)p;
+}
+__device__ __forceinline__ uint4 sload4(const uint4 *p) {
+  typedef const __attribute__((address_space(4))) uint32_t cu32;
+  cu32 *q = (cu32 *)(uintptr_t)p;
+  return make_uint4(q[0], q[1], q[2], q[3]);
+}
 // A plan item whose seq field has this bit is a shared-prefix group item
 // (matrix-core decode only); the other bits locate its member list.
 constexpr uint32_t kGroupItem = 0x80000000u;
@@ -852,7 +866,7 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
   const uint32_t sub = hy - kvh * a.n_sub;
   uint32_t b, t0, tend, slot;
   if (a.items) {  // planned: one work item per grid.x
-    const uint4 it = a.items[blockIdx.x];
+    const uint4 it = sload4(a.items + blockIdx.x);
     b = it.x;
     t0 = it.y;
     tend = it.z;
@@ -906,7 +920,7 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
     }
   }
 
-  uint32_t ctx = a.ctx_lens[b];
+  uint32_t ctx = sload(a.ctx_lens + b);
   ctx = min(ctx, a.ctx_cap);
   const uint32_t lo =
       (a.window > 0 && ctx > (uint32_t)a.window) ? ctx - (uint32_t)a.window : 0;
@@ -1246,7 +1260,7 @@ __global__ void __launch_bounds__(256) decode_f32_kernel(DecodeArgs a) {
   const uint32_t sub = blockIdx.y - kvh * a.n_sub;
   uint32_t b, t0, tend, slot;
   if (a.items) {
-    const uint4 it = a.items[blockIdx.x];
+    const uint4 it = sload4(a.items + blockIdx.x);
     b = it.x;
     t0 = it.y;
     tend = it.z;
@@ -1274,7 +1288,7 @@ __global__ void __launch_bounds__(256) decode_f32_kernel(DecodeArgs a) {
                             x.w * a.qscale);
     }
   }
-  uint32_t ctx = min(a.ctx_lens[b], a.ctx_cap);
+  uint32_t ctx = min(sload(a.ctx_lens + b), a.ctx_cap);
   const uint32_t lo =
       (a.window > 0 && ctx > (uint32_t)a.window) ? ctx - (uint32_t)a.window : 0;
   const uint32_t t1 = min(tend, ctx);
@@ -1519,13 +1533,15 @@ __global__ void __launch_bounds__(64) decode_reduce_kernel(DecodeArgs a) {
   const int lane = threadIdx.x;
   uint32_t b, slot0, np;
   if (a.reds) {
-    const uint4 r = a.reds[blockIdx.y];
-    b = r.x;
-    slot0 = r.y;
-    np = r.z;
+    // The row is wave-uniform: scalar loads (constant address space).
+    typedef const __attribute__((address_space(4))) uint32_t cu32;
+    cu32 *r = (cu32 *)(uintptr_t)(a.reds + blockIdx.y);
+    b = r[0];
+    slot0 = r[1];
+    np = r[2];
   } else {
     b = blockIdx.y;
-    const uint32_t ctx = min(a.ctx_lens[b], a.ctx_cap);
+    const uint32_t ctx = min(sload(a.ctx_lens + b), a.ctx_cap);
     if (ctx <= a.part_tokens) return;  // written directly
     slot0 = b * a.n_parts;
     np = (ctx + a.part_tokens - 1) / a.part_tokens;
