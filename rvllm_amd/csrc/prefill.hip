@@ -418,16 +418,11 @@ __global__ void __launch_bounds__(
   const bool v_lane = VP >= NTH || tid < VP;
 
   // Are all the blocks holding keys below k_end valid? One scan of its
-  // table range; then the masks need no per-key flags (key < row_hi already
+  // table range (after the first tiles' loads are out, below; until then
+  // all_ok is false, so those loads take the path that checks every block
+  // id); then the masks need no per-key flags (key < row_hi already
   // implies key < k_end). Loads still check every block id themselves.
-  bool all_ok = true;
-  if (k_begin < k_end) {
-    int bad = 0;
-    for (uint32_t i = (k_begin >> a.bs_log2) + tid;
-         i <= ((k_end - 1u) >> a.bs_log2); i += NTH)
-      bad |= table[i] >= a.num_blocks;
-    all_ok = !__syncthreads_or(bad);
-  }
+  bool all_ok = false;
 
   // Per-lane constants: tiles start at multiples of the tile width BN, so
   // a chunk's byte offset inside its (block, head) tile and its block index
@@ -821,6 +816,12 @@ __global__ void __launch_bounds__(
       if (k_begin + BN < k_end) load(I1{}, k_begin + BN);
       fetch_ids(k_begin + 2 * BN);
     }
+    // The table scan, with the first tiles' loads in flight.
+    int bad = 0;
+    for (uint32_t i = (k_begin >> a.bs_log2) + tid;
+         i <= ((k_end - 1u) >> a.bs_log2); i += NTH)
+      bad |= table[i] >= a.num_blocks;
+    all_ok = !__syncthreads_or(bad);
   }
   if constexpr (WAVES == 1) {
     if (newtok != 0xFFFFFFFFu) {
