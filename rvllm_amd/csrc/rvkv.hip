@@ -60,6 +60,20 @@ __device__ __forceinline__ uint32_t as_u32(h2 x) {
 // whose lanes write two separate halves, measured slower with it).
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 typedef float f32x4v __attribute__((ext_vector_type(4)));
+// A wave-uniform word read through the constant address space, so it is a
+// scalar load (the kernels also store to global memory, and through a plain
+// pointer the compiler may use vector loads). Only for inputs no kernel of
+// the launch writes.
+__device__ __forceinline__ uint32_t sload(const uint32_t *p) {
+  typedef const __attribute__((address_space(4))) uint32_t cu32;
+  return *(cu32 *)(uintptr_t)p;
+}
+__device__ __forceinline__ uint4 sload4(const uint4 *p) {
+  typedef const __attribute__((address_space(4))) uint32_t cu32;
+  cu32 *q = (cu32 *)(uintptr_t)p;
+  return make_uint4(q[0], q[1], q[2], q[3]);
+}
+
 __device__ __forceinline__ uint4 load_nt16(const void *p) {
   const u32x4v x = __builtin_nontemporal_load(static_cast<const u32x4v *>(p));
   return make_uint4(x[0], x[1], x[2], x[3]);
@@ -475,7 +489,7 @@ __global__ void __launch_bounds__(256)
                        const uint32_t *__restrict__ src,
                        const uint32_t *__restrict__ dst, size_t tensor_elems,
                        size_t block_elems, uint32_t num_blocks) {
-  const uint32_t s = src[blockIdx.y], d = dst[blockIdx.y];
+  const uint32_t s = sload(src + blockIdx.y), d = sload(dst + blockIdx.y);
   if (s >= num_blocks || d >= num_blocks) return;
   uint16_t *t = base + (size_t)blockIdx.z * tensor_elems;
   const W *from = reinterpret_cast<const W *>(t + (size_t)s * block_elems);
@@ -606,19 +620,6 @@ struct DecodeArgs {
 
 constexpr uint32_t kNoSlot = 0xFFFFFFFFu;
 
-// A wave-uniform word read through the constant address space, so it is a
-// scalar load (the kernels also store to global memory, and through a plain
-// pointer the compiler may use vector loads). Only for inputs no kernel of
-// the launch writes.
-__device__ __forceinline__ uint32_t sload(const uint32_t *p) {
-  typedef const __attribute__((address_space(4))) uint32_t cu32;
-  return *(cu32 *)(uintptr_t)p;
-}
-__device__ __forceinline__ uint4 sload4(const uint4 *p) {
-  typedef const __attribute__((address_space(4))) uint32_t cu32;
-  cu32 *q = (cu32 *)(uintptr_t)p;
-  return make_uint4(q[0], q[1], q[2], q[3]);
-}
 // A plan item whose seq field has this bit is a shared-prefix group item
 // (matrix-core decode only); the other bits locate its member list.
 constexpr uint32_t kGroupItem = 0x80000000u;
