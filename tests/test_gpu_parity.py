@@ -886,6 +886,68 @@ def test_planned_decode_prefix_groups(G):
     st.close()
 
 
+@pytest.mark.parametrize("case", range(12))
+def test_planned_decode_prefix_groups_random(case):
+    """Random prefix forests for the group items: a few shared prefixes of
+    random lengths, sharers that keep a random number of their prefix's
+    blocks, random context lengths (some shorter than their prefix), group
+    sizes 5-16, block sizes 16/32/64. The plan built with the host tables
+    must give every row within 5e-4 of the lengths-only plan, and sampled
+    rows within 2e-3 of the oracle."""
+    from rvllm_amd.kv_storage import HipDecodePlan
+    rng = np.random.default_rng(7000 + case)
+    G = int(rng.choice([5, 6, 7, 8, 11, 16]))
+    bs = int(rng.choice([16, 32, 64]))
+    nkv, hd = int(rng.choice([1, 2])), 64
+    H = G * nkv
+    n = int(rng.integers(20, 90))
+    n_pref = int(rng.integers(1, 4))
+    pref_blocks = [int(rng.integers(4, 48)) for _ in range(n_pref)]
+    pool_blocks = 0
+    prefixes = []
+    for pb in pref_blocks:
+        prefixes.append(np.arange(pool_blocks, pool_blocks + pb, dtype=np.uint32))
+        pool_blocks += pb
+    lens = rng.integers(2, 3500, n).astype(np.uint32)
+    tables = []
+    for b in range(n):
+        nb = -(-int(lens[b]) // bs)
+        owner = int(rng.integers(-1, n_pref))  # -1: no prefix
+        keep = int(rng.integers(0, pref_blocks[owner] + 1)) if owner >= 0 else 0
+        t = []
+        for i in range(nb):
+            last = (i + 1) * bs >= lens[b]  # the appended key's block: private
+            if owner >= 0 and i < keep and not last:
+                t.append(int(prefixes[owner][i]))
+            else:
+                t.append(pool_blocks)
+                pool_blocks += 1
+        tables.append(np.array(t, np.uint32))
+    perm = rng.permutation(pool_blocks).astype(np.uint32)
+    tables = [perm[t] for t in tables]
+    cfg = W.Config("pgr", 9, 1, H, nkv, hd, bs, n)
+    db = W.DecodeBatch(cfg, pool_blocks, lens, tables,
+                       np.zeros(n, np.uint32), np.zeros(n, np.uint32))
+    st = HipKvStorage(1, pool_blocks, bs, nkv, hd)
+    fill_layer(st, 0, seed=case)
+    q = torch.randn(n, H, hd, device="cuda",
+                    generator=torch.Generator("cuda").manual_seed(case))
+    tab, ctx = dev_u32(db.padded_tables()), dev_u32(lens)
+    plan = HipDecodePlan(st, lens, H)
+    plain = st.paged_decode_planned(0, plan, q, tab, ctx).clone()
+    plan.update(lens, db.padded_tables())
+    got = st.paged_decode_planned(0, plan, q, tab, ctx)
+    assert torch.isfinite(got).all()
+    assert (got - plain).abs().max().item() < 5e-4, case
+    sample = sorted(rng.choice(n, min(n, 10), replace=False).tolist())
+    cache, padded, mb = oracle_subset(st, 0, [tables[b] for b in sample],
+                                      lens[sample])
+    want = orc.paged_decode_f64(cache, q.cpu().numpy()[sample],
+                                padded.reshape(-1), mb, lens[sample])
+    assert np.abs(got.cpu().numpy()[sample] - want).max() < ATOL, case
+    st.close()
+
+
 def test_planned_decode_update_reuses_plan():
     """update() with new lengths (a decode step later, batch change) gives
     the same results as a freshly built plan."""
