@@ -88,6 +88,23 @@ constexpr int kWaveRows = 32;  // query rows per wave
 // head_dim 64 (prefill and the decode mode); transposed was as fast or up to
 // 2.4 % faster at 128 and 256, where the P.V product issues more V reads.
 constexpr bool v_rowmajor(int hd) { return hd <= 64; }
+// Tiles staged by LDS DMA (global_load_lds_dwordx4: each lane's 16 bytes go
+// from memory straight into LDS, no staging registers and no LDS stores):
+// head_dim 128 in 4-wave workgroups. Without staging registers two such
+// workgroups fit on a CU, each with its own barrier, so the two waves of a
+// SIMD are not held in the same phase (one's softmax can overlap the other's
+// matrix work). Rows are unpadded (a lane writes 16 consecutive bytes of
+// the wave's 1 KiB); chunk c of row r sits in slot c ^ swz(r).
+template <int HD, int WAVES>
+constexpr bool dma_tiles() { return HD == 128 && WAVES == 4; }
+// The slot swizzle of a 256-byte row (16 chunks; LDS serves 64 banks of 4
+// bytes, one 256-byte row, per cycle): the two 2-bit halves of r % 16
+// swapped. A K fragment read (16 lanes, rows 0-15 of one chunk column)
+// then meets 16 different slots, and a transposing V read (32 lanes, rows
+// 4j..4j+3, four consecutive chunks) 16 as well.
+__device__ __forceinline__ uint32_t swz(uint32_t r) {
+  return ((r & 3u) << 2) | ((r >> 2) & 3u);
+}
 // At head_dim 256 the two waves of a pair share 32 query rows: each holds
 // half of the head dimension of Q and O (the S product's two halves are
 // added through LDS), so a wave's O and Q fit two waves per SIMD.
@@ -132,21 +149,27 @@ struct PrefillArgs {
 };
 
 constexpr uint32_t kNoSlot = 0xFFFFFFFFu;
+// 1 KiB of zeros: under LDS DMA the rows of keys that are not read (past
+// the range, unreadable blocks) are loaded from here, so their V is 0 in
+// LDS (masked keys get probability 0, and 0 * stale V must stay 0).
+__device__ __align__(16) uint4 g_pf_zero[64];
 constexpr uint32_t kGroupItem = 0x80000000u;
 
 template <int HD, int WAVES>
 struct Lds {
   static constexpr int BN = tile_keys<HD, WAVES>();
-  static constexpr int KS = HD + 8;  // K row stride in halves (16 B pad)
+  static constexpr bool DMA = dma_tiles<HD, WAVES>();
+  // K row stride in halves (16 B pad; unpadded and swizzled under DMA)
+  static constexpr int KS = DMA ? HD : HD + 8;
   // Row-major V stride: 32 halves of pad. The transposing reads of P.V
   // (four keys x four dims per 16 lanes) met 0.33 bank conflicts per LDS
   // access with 8, 16 or 24 halves of pad (Llama prefill, 17 M conflict
   // cycles a launch) and none with 32.
-  static constexpr int VRS = HD + 32;
+  static constexpr int VRS = DMA ? HD : HD + 32;
   static constexpr size_t k_bytes = (size_t)BN * KS * 2;
   static constexpr int VS = BN + 8;  // Vt row stride in halves (transposed)
   static constexpr size_t v_bytes =
-      v_rowmajor(HD) ? (size_t)BN * VRS * 2 : (size_t)HD * VS * 2;
+      v_rowmajor(HD) || DMA ? (size_t)BN * VRS * 2 : (size_t)HD * VS * 2;
   // Workgroups of several waves double-buffer the tile, so one barrier a
   // tile both publishes it and retires the buffer the next tile overwrites
   // (a one-wave workgroup orders its own LDS accesses).
@@ -236,7 +259,8 @@ __global__ void __launch_bounds__(
   constexpr int kBM = block_rows<HD, WAVES>();
   using LD = Lds<HD, WAVES>;
   constexpr int KS = LD::KS, VS = LD::VS, BN = LD::BN, VRS = LD::VRS;
-  constexpr bool TRV = v_rowmajor(HD);
+  constexpr bool DMA = LD::DMA;
+  constexpr bool TRV = v_rowmajor(HD) || DMA;
   constexpr int NT = BN / 32;                 // 32-key sub-tiles per tile
   // This wave's share of the head dimension: all of it, or one half.
   constexpr int KC = HD / 16 / (SPLIT ? 2 : 1);  // MFMA k-steps of S
@@ -244,6 +268,8 @@ __global__ void __launch_bounds__(
   constexpr int CPR = HD / 8;                 // 16-byte chunks per key row
   constexpr int CHK = BN * CPR / NTH;         // K chunks per thread per tile
   static_assert(CHK >= 1 && BN * CPR % NTH == 0, "tile/thread mismatch");
+  static_assert(!DMA || (CPR == 16 && !SPLIT && WAVES > 1),
+                "DMA tiles: 16 chunks a row, 16-slot swizzle");
   extern __shared__ __align__(16) unsigned char smem[];
 
   // XCD-aware order: workgroups are dispatched round-robin over the 8 XCDs
@@ -434,7 +460,10 @@ __global__ void __launch_bounds__(
   for (int i = 0; i < CHK; ++i) {
     const int c = tid + NTH * i;
     k_key[i] = (uint32_t)(c / CPR);
-    k_off[i] = ((k_key[i] & bs_mask) * HD + (c % CPR) * 8) * 2;
+    // (under DMA the chunk is read from the slot this lane writes)
+    const uint32_t dc =
+        DMA ? (uint32_t)(c % CPR) ^ swz(k_key[i]) : (uint32_t)(c % CPR);
+    k_off[i] = ((k_key[i] & bs_mask) * HD + dc * 8) * 2;
     k_db[i] = k_key[i] >> a.bs_log2;
   }
   // (one block of all heads is far below 4 GiB; checked on the host)
@@ -502,6 +531,47 @@ __global__ void __launch_bounds__(
   auto load = [&](auto S, uint32_t kt) {
     constexpr int si = decltype(S)::value;
     const uint32_t t_off = (kt & bs_mask) * HD * 2;  // 0 unless bs > 64
+    if constexpr (DMA) {
+      // Instruction i of wave w fills chunks 64w + NTH*i .. + 63 of the
+      // tile's buffer (tile j uses buffer j % 2, as in step): 1 KiB, four
+      // whole rows, one block id. Keys not read load zeros.
+      typedef __attribute__((address_space(3))) void lds_t;
+      unsigned char *lb = smem + (((kt - k_begin) / BN) & 1u) * LD::buf;
+      if (all_ok && kt + BN <= k_end) {  // uniform: every key read
+#pragma unroll
+        for (int i = 0; i < CHK; ++i) {
+          const uint32_t dst = (64u * wave + (uint32_t)(NTH * i)) * 16u;
+          const uint64_t off =
+              (uint64_t)kid[i] * blk_bytes + (t_off + k_off[i]);
+          __builtin_amdgcn_global_load_lds((const void *)(kbase + off),
+                                           (lds_t *)(lb + dst), 16, 0, 0);
+          __builtin_amdgcn_global_load_lds(
+              (const void *)(vbase + off), (lds_t *)(lb + LD::k_bytes + dst),
+              16, 0, 0);
+        }
+        return;
+      }
+      const uint64_t zero = reinterpret_cast<uint64_t>(g_pf_zero) + lane * 16;
+#pragma unroll
+      for (int i = 0; i < CHK; ++i) {
+        const uint32_t dst = (64u * wave + (uint32_t)(NTH * i)) * 16u;
+        const bool use = kid[i] < a.num_blocks && kt + k_key[i] < k_end;
+        const uint64_t off =
+            (uint64_t)kid[i] * blk_bytes + (t_off + k_off[i]);
+        // (one address each, selected as integers: no divergent loads)
+        const uint64_t kp = use ? reinterpret_cast<uint64_t>(kbase) + off : zero;
+        const uint64_t vp = use ? reinterpret_cast<uint64_t>(vbase) + off : zero;
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void *>(kp),
+                                         (lds_t *)(lb + dst), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void *>(vp),
+                                         (lds_t *)(lb + LD::k_bytes + dst),
+                                         16, 0, 0);
+        // (the key flags are read only while all_ok is false)
+        if (!all_ok && (lane & 15) == 0)
+          lb[LD::k_bytes + LD::v_bytes + k_key[i]] = (uint8_t)use;
+      }
+      return;
+    }
     if (all_ok && kt + BN <= k_end) {
       // Every key of the tile is below k_end and every block valid: no
       // flags, no id checks (the common case, uniform).
@@ -585,7 +655,7 @@ __global__ void __launch_bounds__(
     if constexpr (LD::NBUF == 1)
       __syncthreads();  // the previous tile is no longer read
 #pragma unroll
-    for (int i = 0; i < CHK; ++i) {
+    for (int i = 0; i < (DMA ? 0 : CHK); ++i) {
       const int c = tid + NTH * i;
       const int key = c / CPR, dc = c % CPR;
       *reinterpret_cast<u32x4 *>(ks + key * KS + dc * 8) = kr[si][i];
@@ -645,6 +715,9 @@ __global__ void __launch_bounds__(
         if (!all_ok && tid == 0) kok[r] = 1;
       }
     }
+    // (DMA: this wave's copies into the tile must have landed before the
+    // barrier publishes it)
+    if constexpr (DMA) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (kt + DEPTH * BN < k_end) {
       load(S, kt + DEPTH * BN);
@@ -668,8 +741,13 @@ __global__ void __launch_bounds__(
         half8 kf[NT];
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-          kf[t] = *reinterpret_cast<const half8 *>(
-              ks + (32 * t + sig) * KS + dh * (KC * 16) + kc * 16 + hl * 8);
+          if constexpr (DMA)
+            kf[t] = *reinterpret_cast<const half8 *>(
+                ks + (32 * t + sig) * KS +
+                (((uint32_t)(2 * kc + hl) ^ swz((uint32_t)sig)) * 8));
+          else
+            kf[t] = *reinterpret_cast<const half8 *>(
+                ks + (32 * t + sig) * KS + dh * (KC * 16) + kc * 16 + hl * 8);
           s[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[t], qf[kc], s[t], 0,
                                                         0, 0);
         }
@@ -795,9 +873,22 @@ __global__ void __launch_bounds__(
           if constexpr (TRV) {
             // Two transposing reads of 4 keys each; the lane's address is
             // the (key, dim) its 16-lane group hands out.
-            const uint16_t *vp = vs + (32 * t + 16 * c + tr_key) * VRS +
-                                 (dh * DT + dt) * 32 + tr_dim;
-            const v4h lo = tr_read(vp), hi = tr_read(vp + 4 * VRS);
+            v4h lo, hi;
+            if constexpr (DMA) {
+              // rows tr_key and tr_key + 4 (< 16) of the sub-tile, each at
+              // its own swizzled slot
+              const uint32_t ch = (uint32_t)(4 * dt) + ((uint32_t)tr_dim >> 3);
+              const uint16_t *vr = vs + (32 * t + 16 * c + tr_key) * VRS +
+                                   (tr_dim & 7);
+              lo = tr_read(vr + ((ch ^ swz((uint32_t)tr_key)) * 8));
+              hi = tr_read(vr + 4 * VRS +
+                           ((ch ^ swz((uint32_t)tr_key + 4u)) * 8));
+            } else {
+              const uint16_t *vp = vs + (32 * t + 16 * c + tr_key) * VRS +
+                                   (dh * DT + dt) * 32 + tr_dim;
+              lo = tr_read(vp);
+              hi = tr_read(vp + 4 * VRS);
+            }
             vf = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
           } else {
             vf = *reinterpret_cast<const half8 *>(
@@ -921,14 +1012,17 @@ void launch_prefill(const PrefillArgs &a, dim3 grid, hipStream_t st) {
                      (Lds<HD, WAVES>::bytes), st, a);
 }
 
-// Waves per workgroup: 8 at head_dim 128 (measured ~5 % faster than 4; 4
-// would not fit the hi/lo q in registers) and at 256 (four pairs); 4 at 64,
-// where 8-wave workgroups would cost the third resident wave per SIMD
-// (measured ~7 % slower), and at 32. RVKV_PREFILL_WAVES=4|8 overrides at 64.
+// Waves per workgroup: 4 at head_dim 128 with the tiles staged by LDS DMA,
+// two workgroups per CU (1.5-2 % faster than one 8-wave workgroup with
+// register staging, which is what fits without DMA); 8 at 256 (four
+// pairs); 4 at 64, where 8-wave workgroups would cost the third resident
+// wave per SIMD (measured ~7 % slower), and at 32. RVKV_PREFILL_WAVES=4|8
+// overrides at 64 and 128.
 uint32_t prefill_waves(uint32_t hd) {
   static const char *env = getenv("RVKV_PREFILL_WAVES");
   static const uint32_t forced = env ? (uint32_t)atoi(env) : 0u;
-  if (split_dims((int)hd) || hd == 128) return 8u;  // (256: four pairs)
+  if (hd == 128) return forced == 8 ? 8u : 4u;
+  if (split_dims((int)hd)) return 8u;  // (four pairs)
   if (hd == 64 && (forced == 4 || forced == 8)) return forced;
   return 4u;
 }
@@ -1012,7 +1106,8 @@ int rvkv_paged_prefill(rvkv_pool *pool, uint32_t layer, const float *q,
       else launch_prefill<64, 4>(a, grid, pool->stream);
       break;
     case 128:
-      launch_prefill<128, 8>(a, grid, pool->stream);
+      if (waves == 4) launch_prefill<128, 4>(a, grid, pool->stream);
+      else launch_prefill<128, 8>(a, grid, pool->stream);
       break;
     default: launch_prefill<256, 8>(a, grid, pool->stream); break;
   }
