@@ -153,6 +153,22 @@ constexpr uint32_t kNoSlot = 0xFFFFFFFFu;
 // the range, unreadable blocks) are loaded from here, so their V is 0 in
 // LDS (masked keys get probability 0, and 0 * stale V must stay 0).
 __device__ __align__(16) uint4 g_pf_zero[64];
+// Buffer resource of one (block, head) tile for the DMA loads: byte range
+// (the lane offsets stay below it) and word 3 (32-bit data format, the
+// value raw buffer accesses use on this architecture).
+constexpr int kRsrcBytes = 0x7fffffff;
+constexpr int kRsrcWord3 = 0x00020000;
+
+// One LDS DMA instruction by buffer load: lane l's 16 bytes at base + off
+// go to lds + 16 l. base and lds are wave-uniform (a descriptor in scalar
+// registers, M0); only the 32-bit offset is per lane.
+__device__ __forceinline__ void dma16(const char *base, uint32_t off,
+                                      unsigned char *lds) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)base, (short)0, kRsrcBytes, kRsrcWord3);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      r, (__attribute__((address_space(3))) void *)lds, 16, off, 0, 0, 0);
+}
 constexpr uint32_t kGroupItem = 0x80000000u;
 
 template <int HD, int WAVES>
@@ -528,7 +544,9 @@ __global__ void __launch_bounds__(
   u32x4 new_kc{}, new_vc{};
   uint16_t new_ve = 0;  // transposed V: element tid of the new row (f16)
   const size_t new_src = ((size_t)b * a.n_kv + kvh) * HD;
-  auto load = [&](auto S, uint32_t kt) {
+  // B: the LDS buffer of tile kt (tile i uses buffer i % NBUF), a
+  // compile-time index so LDS addresses fold into instruction offsets.
+  auto load = [&](auto S, auto B, uint32_t kt) {
     constexpr int si = decltype(S)::value;
     const uint32_t t_off = (kt & bs_mask) * HD * 2;  // 0 unless bs > 64
     if constexpr (DMA) {
@@ -536,18 +554,17 @@ __global__ void __launch_bounds__(
       // tile's buffer (tile j uses buffer j % 2, as in step): 1 KiB, four
       // whole rows, one block id. Keys not read load zeros.
       typedef __attribute__((address_space(3))) void lds_t;
-      unsigned char *lb = smem + (((kt - k_begin) / BN) & 1u) * LD::buf;
+      unsigned char *lb = smem + decltype(B)::value * LD::buf;
       if (all_ok && kt + BN <= k_end) {  // uniform: every key read
 #pragma unroll
         for (int i = 0; i < CHK; ++i) {
           const uint32_t dst = (64u * wave + (uint32_t)(NTH * i)) * 16u;
-          const uint64_t off =
-              (uint64_t)kid[i] * blk_bytes + (t_off + k_off[i]);
-          __builtin_amdgcn_global_load_lds((const void *)(kbase + off),
-                                           (lds_t *)(lb + dst), 16, 0, 0);
-          __builtin_amdgcn_global_load_lds(
-              (const void *)(vbase + off), (lds_t *)(lb + LD::k_bytes + dst),
-              16, 0, 0);
+          // Buffer loads: the block's address (uniform) goes into a
+          // resource descriptor built by scalar instructions, the lane adds
+          // its 32-bit offset; no vector address arithmetic.
+          const uint64_t tb = (uint64_t)kid[i] * blk_bytes + t_off;
+          dma16(kbase + tb, k_off[i], lb + dst);
+          dma16(vbase + tb, k_off[i], lb + LD::k_bytes + dst);
         }
         return;
       }
@@ -640,14 +657,16 @@ __global__ void __launch_bounds__(
 
   // One tile: stage register set S into LDS, refill S with the tile DEPTH
   // ahead, compute.
-  auto step = [&](auto S, uint32_t kt) {
+  auto step = [&](auto S, auto B, uint32_t kt) {
     constexpr int si = decltype(S)::value;
+    constexpr int bi = LD::NBUF == 2 ? decltype(B)::value : 0;
+    // the buffer of the tile DEPTH ahead
+    using BN_ = std::integral_constant<int, LD::NBUF == 2 ? 1 - bi : 0>;
     // Every key of the tile readable: all blocks valid, tile inside k_end.
     const bool tile_ok = all_ok && kt + BN <= k_end;
     // Tile i uses buffer i % NBUF; with two, every wave has passed the
     // previous tile's barrier, so none still reads tile i - 2's buffer.
-    unsigned char *lb =
-        smem + (LD::NBUF == 2 ? ((kt - k_begin) / BN) & 1u : 0u) * LD::buf;
+    unsigned char *lb = smem + bi * LD::buf;
     uint16_t *ks = reinterpret_cast<uint16_t *>(lb);
     // V: row-major (vs, stride KS) or transposed (Vt[d][key], stride VS).
     uint16_t *vs = reinterpret_cast<uint16_t *>(lb + LD::k_bytes);
@@ -720,7 +739,7 @@ __global__ void __launch_bounds__(
     if constexpr (DMA) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (kt + DEPTH * BN < k_end) {
-      load(S, kt + DEPTH * BN);
+      load(S, BN_{}, kt + DEPTH * BN);
       fetch_ids(kt + (DEPTH + 1) * BN);
     }
     // Does any row of the wave see a key of the tile? (Wave-uniform, and
@@ -901,10 +920,10 @@ __global__ void __launch_bounds__(
 
   if (k_begin < k_end) {
     fetch_ids(k_begin);
-    load(I0{}, k_begin);
+    load(I0{}, I0{}, k_begin);
     fetch_ids(k_begin + BN);
     if constexpr (DEPTH == 2) {
-      if (k_begin + BN < k_end) load(I1{}, k_begin + BN);
+      if (k_begin + BN < k_end) load(I1{}, I0{}, k_begin + BN);  // (NBUF 1)
       fetch_ids(k_begin + 2 * BN);
     }
     // The table scan, with the first tiles' loads in flight.
@@ -932,16 +951,18 @@ __global__ void __launch_bounds__(
       }
     }
   }
-  if constexpr (DEPTH == 1) {
-    for (uint32_t kt = k_begin; kt < k_end; kt += BN) step(I0{}, kt);
-  } else {
-    for (uint32_t kt = k_begin; kt < k_end;) {
-      step(I0{}, kt);
-      kt += BN;
-      if (kt >= k_end) break;
-      step(I1{}, kt);
-      kt += BN;
-    }
+  // Two tiles per iteration: register sets (DEPTH 2) or LDS buffers
+  // (NBUF 2) alternate with compile-time indices.
+  using Bx1 = std::integral_constant<int, 1>;
+  for (uint32_t kt = k_begin; kt < k_end;) {
+    step(I0{}, I0{}, kt);
+    kt += BN;
+    if (kt >= k_end) break;
+    if constexpr (DEPTH == 1)
+      step(I0{}, Bx1{}, kt);
+    else
+      step(I1{}, I0{}, kt);
+    kt += BN;
   }
 
   if constexpr (WAVES == 1) {
