@@ -1474,7 +1474,7 @@ def test_prefill_chunked_vs_oracle(G, hd, bs):
     assert np.isfinite(out).all() and err < ATOL, err
 
 
-@pytest.mark.parametrize("hd", [64, 256])
+@pytest.mark.parametrize("hd", [64, 128, 256])
 @pytest.mark.parametrize("window", [1, 37, 300])
 def test_prefill_window(window, hd):
     out, want = _prefill_case(window, 2, 200, 2, 4, hd, 16, window,
