@@ -736,7 +736,9 @@ __global__ void __launch_bounds__(
     }
     // (DMA: this wave's copies into the tile must have landed before the
     // barrier publishes it)
-    if constexpr (DMA) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // (s_waitcnt with vmcnt 0, expcnt and lgkmcnt at their maxima: 0x0f70
+    // in this architecture's encoding)
+    if constexpr (DMA) __builtin_amdgcn_s_waitcnt(0x0f70);
     __syncthreads();
     if (kt + DEPTH * BN < k_end) {
       load(S, BN_{}, kt + DEPTH * BN);
