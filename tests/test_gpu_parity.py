@@ -1474,6 +1474,29 @@ def test_prefill_chunked_vs_oracle(G, hd, bs):
     assert np.isfinite(out).all() and err < ATOL, err
 
 
+@pytest.mark.parametrize("case", range(16))
+def test_prefill_random_shapes(case):
+    """Seeded random prefill shapes on the tuned kernels: head_dim 32-256,
+    block sizes 8-256, groups 1-8, chunk lengths 1-300 (one to several
+    query tiles, partial last tiles), earlier context up to three chunks,
+    ragged read counts, windows, and a sharper q on some cases; each
+    against the float64 oracle."""
+    rng = np.random.default_rng(9100 + case)
+    hd = int(rng.choice([32, 64, 128, 256]))
+    bs = int(rng.choice([8, 16, 32, 64, 128, 256]))
+    G = int(rng.integers(1, 9))
+    nkv = int(rng.integers(1, 3))
+    B = int(rng.integers(1, 4))
+    Q = int(rng.choice([1, 7, 64, 65, 129, 300]))
+    window = int(rng.choice([0, 0, 5, 100]))
+    qscale = float(rng.choice([1.0, 1.0, 6.0]))
+    out, want = _prefill_case(9100 + case, B, Q, nkv, G, hd, bs, window,
+                              qscale=qscale)
+    assert np.isfinite(out).all()
+    err = np.abs(out - want).max()
+    assert err < ATOL, (case, hd, bs, G, nkv, B, Q, window, qscale, err)
+
+
 @pytest.mark.parametrize("hd", [64, 128, 256])
 @pytest.mark.parametrize("window", [1, 37, 300])
 def test_prefill_window(window, hd):
