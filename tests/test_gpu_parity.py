@@ -625,6 +625,60 @@ def test_planned_decode_ragged_splits(window, bs):
     assert np.abs(ref - out).max() < ATOL
 
 
+@pytest.mark.parametrize("case", range(16))
+def test_decode_random_shapes(case):
+    """Seeded random decode batches: head_dim 32-256 (and 80, the ragged
+    path), groups 1-12, block sizes 8-128, 1-40 sequences of log-uniform
+    lengths (some empty), windows. The unplanned and the planned decode
+    are checked against the float64 oracle on a sample; then the fused
+    decode step (append + attend) on the sequences that hold a token, with
+    the oracle reading the cache after the append."""
+    rng = np.random.default_rng(9300 + case)
+    hd = int(rng.choice([32, 64, 80, 128, 256]))
+    G = int(rng.integers(1, 13))
+    nkv = int(rng.integers(1, 3))
+    bs = int(rng.choice([8, 16, 32, 64, 128]))
+    n = int(rng.integers(1, 41))
+    lens = np.exp(rng.uniform(0, np.log(3000), n)).astype(np.uint32)
+    lens[rng.random(n) < 0.1] = 0
+    window = int(rng.choice([0, 0, 0, 50]))
+    H = G * nkv
+    cfg = W.Config("rnd", 9, 1, H, nkv, hd, bs, n)
+    db = W.ragged_batch(cfg, np.maximum(lens, 1), seed=case)
+    db.ctx_lens = lens
+    st = HipKvStorage(1, db.num_blocks, bs, nkv, hd)
+    fill_layer(st, 0, seed=case)
+    q = torch.randn(n, H, hd, device="cuda",
+                    generator=torch.Generator("cuda").manual_seed(case))
+    sample = sorted(rng.choice(n, min(n, 10), replace=False).tolist())
+    shape = (case, hd, G, nkv, bs, n, window)
+    assert _decode_vs_oracle(st, 0, db, q, window, sample) < ATOL, shape
+    err, _, out = _planned_vs_oracle(st, 0, db, q, window, sample)
+    assert err < ATOL, shape
+    assert (out[lens == 0] == 0).all(), shape
+    live = [b for b in sample if lens[b] > 0]
+    if not live:
+        return
+    k = torch.randn(n, nkv, hd, device="cuda")
+    v = torch.randn(n, nkv, hd, device="cuda")
+    keep = lens > 0  # empty sequences append nothing: an out-of-range slot
+    sb = np.where(keep, db.slot_block, 0xFFFFFFFF).astype(np.uint32)
+    got = st.decode_step(0, k, v, dev_u32(sb), dev_u32(db.slot_off), q,
+                         dev_u32(db.padded_tables()), dev_u32(lens),
+                         int(lens.max()), window=window).cpu().numpy()
+    cache, padded, mb = oracle_subset(st, 0, [db.tables[b] for b in live],
+                                      lens[live])
+    want = orc.paged_decode_f64(cache, q.cpu().numpy()[live],
+                                padded.reshape(-1), mb, lens[live],
+                                window=window)
+    assert np.abs(got[live] - want).max() < ATOL, shape
+    # the appended rows are in the cache, rounded to f16
+    for b in live:
+        blk, off = int(db.slot_block[b]), int(db.slot_off[b])
+        row = st.read_blocks(0, 0, dev_u32([blk])).cpu()[0, off]
+        assert torch.equal(row, k[b].cpu().to(torch.float16)), shape
+
+
 @pytest.mark.parametrize("G", [4, 7])
 def test_decode_reduction_over_more_than_64_partitions(G):
     """A 40000-token sequence beside a short one, one KV head: the uniform
