@@ -88,8 +88,9 @@ constexpr int kWaveRows = 32;  // query rows per wave
 // head_dim 64 (prefill and the decode mode); transposed was as fast or up to
 // 2.4 % faster at 128 and 256, where the P.V product issues more V reads.
 constexpr bool v_rowmajor(int hd) { return hd <= 64; }
-// Tiles staged by LDS DMA (global_load_lds_dwordx4: each lane's 16 bytes go
-// from memory straight into LDS, no staging registers and no LDS stores):
+// Tiles staged by LDS DMA (buffer_load_dwordx4 / global_load_lds_dwordx4
+// with the LDS flag: each lane's 16 bytes go from memory straight into LDS,
+// no staging registers and no LDS stores):
 // head_dim 128 in 4-wave workgroups. Without staging registers two such
 // workgroups fit on a CU, each with its own barrier, so the two waves of a
 // SIMD are not held in the same phase (one's softmax can overlap the other's
@@ -735,9 +736,8 @@ __global__ void __launch_bounds__(
       }
     }
     // (DMA: this wave's copies into the tile must have landed before the
-    // barrier publishes it)
-    // (s_waitcnt with vmcnt 0, expcnt and lgkmcnt at their maxima: 0x0f70
-    // in this architecture's encoding)
+    // barrier publishes it: s_waitcnt with vmcnt 0, expcnt and lgkmcnt at
+    // their maxima, 0x0f70 in this architecture's encoding)
     if constexpr (DMA) __builtin_amdgcn_s_waitcnt(0x0f70);
     __syncthreads();
     if (kt + DEPTH * BN < k_end) {
