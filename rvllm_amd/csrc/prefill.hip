@@ -91,20 +91,26 @@ constexpr bool v_rowmajor(int hd) { return hd <= 64; }
 // Tiles staged by LDS DMA (buffer_load_dwordx4 / global_load_lds_dwordx4
 // with the LDS flag: each lane's 16 bytes go from memory straight into LDS,
 // no staging registers and no LDS stores):
-// head_dim 128 in 4-wave workgroups. Without staging registers two such
-// workgroups fit on a CU, each with its own barrier, so the two waves of a
-// SIMD are not held in the same phase (one's softmax can overlap the other's
-// matrix work). Rows are unpadded (a lane writes 16 consecutive bytes of
-// the wave's 1 KiB); chunk c of row r sits in slot c ^ swz(r).
+// head_dim 64 and 128 in 4-wave workgroups. Without staging registers two
+// such workgroups fit on a CU at 128, each with its own barrier, so the two
+// waves of a SIMD are not held in the same phase (one's softmax can overlap
+// the other's matrix work). Rows are unpadded (a lane writes 16 consecutive
+// bytes of the wave's 1 KiB); chunk c of row r sits in slot c ^ swz(r).
 template <int HD, int WAVES>
-constexpr bool dma_tiles() { return HD == 128 && WAVES == 4; }
-// The slot swizzle of a 256-byte row (16 chunks; LDS serves 64 banks of 4
-// bytes, one 256-byte row, per cycle): the two 2-bit halves of r % 16
-// swapped. A K fragment read (16 lanes, rows 0-15 of one chunk column)
-// then meets 16 different slots, and a transposing V read (32 lanes, rows
-// 4j..4j+3, four consecutive chunks) 16 as well.
+constexpr bool dma_tiles() { return (HD == 64 || HD == 128) && WAVES == 4; }
+// The slot swizzle (LDS serves 64 banks of 4 bytes, 256 bytes, per cycle).
+// A K fragment read (16 lanes, rows 0-15 of one chunk column) and a
+// transposing V read (32 lanes, rows 4j..4j+3, four consecutive chunks)
+// must each meet 16 different 16-byte bank groups.
+// 256-byte rows (head_dim 128, 16 chunks): the two 2-bit halves of r % 16
+// swapped. 128-byte rows (64, 8 chunks; two rows a bank cycle, told apart
+// by bit 0 of r): bit 1 of r to bit 2 of the slot, bits 2-3 to bits 0-1.
+template <int HD>
 __device__ __forceinline__ uint32_t swz(uint32_t r) {
-  return ((r & 3u) << 2) | ((r >> 2) & 3u);
+  if constexpr (HD == 128)
+    return ((r & 3u) << 2) | ((r >> 2) & 3u);
+  else
+    return (((r >> 1) & 1u) << 2) | ((r >> 2) & 3u);
 }
 // At head_dim 256 the two waves of a pair share 32 query rows: each holds
 // half of the head dimension of Q and O (the S product's two halves are
@@ -285,8 +291,8 @@ __global__ void __launch_bounds__(
   constexpr int CPR = HD / 8;                 // 16-byte chunks per key row
   constexpr int CHK = BN * CPR / NTH;         // K chunks per thread per tile
   static_assert(CHK >= 1 && BN * CPR % NTH == 0, "tile/thread mismatch");
-  static_assert(!DMA || (CPR == 16 && !SPLIT && WAVES > 1),
-                "DMA tiles: 16 chunks a row, 16-slot swizzle");
+  static_assert(!DMA || ((CPR == 8 || CPR == 16) && !SPLIT && WAVES > 1),
+                "DMA tiles: 8 or 16 chunks a row");
   extern __shared__ __align__(16) unsigned char smem[];
 
   // XCD-aware order: workgroups are dispatched round-robin over the 8 XCDs
@@ -479,7 +485,7 @@ __global__ void __launch_bounds__(
     k_key[i] = (uint32_t)(c / CPR);
     // (under DMA the chunk is read from the slot this lane writes)
     const uint32_t dc =
-        DMA ? (uint32_t)(c % CPR) ^ swz(k_key[i]) : (uint32_t)(c % CPR);
+        DMA ? (uint32_t)(c % CPR) ^ swz<HD>(k_key[i]) : (uint32_t)(c % CPR);
     k_off[i] = ((k_key[i] & bs_mask) * HD + dc * 8) * 2;
     k_db[i] = k_key[i] >> a.bs_log2;
   }
@@ -552,8 +558,9 @@ __global__ void __launch_bounds__(
     const uint32_t t_off = (kt & bs_mask) * HD * 2;  // 0 unless bs > 64
     if constexpr (DMA) {
       // Instruction i of wave w fills chunks 64w + NTH*i .. + 63 of the
-      // tile's buffer (tile j uses buffer j % 2, as in step): 1 KiB, four
-      // whole rows, one block id. Keys not read load zeros.
+      // tile's buffer (tile j uses buffer j % 2, as in step): 1 KiB, whole
+      // rows (four at head_dim 128, eight at 64), one block id. Keys not
+      // read load zeros.
       typedef __attribute__((address_space(3))) void lds_t;
       unsigned char *lb = smem + decltype(B)::value * LD::buf;
       if (all_ok && kt + BN <= k_end) {  // uniform: every key read
@@ -585,7 +592,7 @@ __global__ void __launch_bounds__(
                                          (lds_t *)(lb + LD::k_bytes + dst),
                                          16, 0, 0);
         // (the key flags are read only while all_ok is false)
-        if (!all_ok && (lane & 15) == 0)
+        if (!all_ok && (lane & (CPR - 1)) == 0)  // (a row's first lane)
           lb[LD::k_bytes + LD::v_bytes + k_key[i]] = (uint8_t)use;
       }
       return;
@@ -765,7 +772,7 @@ __global__ void __launch_bounds__(
           if constexpr (DMA)
             kf[t] = *reinterpret_cast<const half8 *>(
                 ks + (32 * t + sig) * KS +
-                (((uint32_t)(2 * kc + hl) ^ swz((uint32_t)sig)) * 8));
+                (((uint32_t)(2 * kc + hl) ^ swz<HD>((uint32_t)sig)) * 8));
           else
             kf[t] = *reinterpret_cast<const half8 *>(
                 ks + (32 * t + sig) * KS + dh * (KC * 16) + kc * 16 + hl * 8);
@@ -897,13 +904,13 @@ __global__ void __launch_bounds__(
             v4h lo, hi;
             if constexpr (DMA) {
               // rows tr_key and tr_key + 4 (< 16) of the sub-tile, each at
-              // its own swizzled slot
+              // its own swizzled slot (chunks 4dt .. 4dt + 3)
               const uint32_t ch = (uint32_t)(4 * dt) + ((uint32_t)tr_dim >> 3);
               const uint16_t *vr = vs + (32 * t + 16 * c + tr_key) * VRS +
                                    (tr_dim & 7);
-              lo = tr_read(vr + ((ch ^ swz((uint32_t)tr_key)) * 8));
+              lo = tr_read(vr + ((ch ^ swz<HD>((uint32_t)tr_key)) * 8));
               hi = tr_read(vr + 4 * VRS +
-                           ((ch ^ swz((uint32_t)tr_key + 4u)) * 8));
+                           ((ch ^ swz<HD>((uint32_t)tr_key + 4u)) * 8));
             } else {
               const uint16_t *vp = vs + (32 * t + 16 * c + tr_key) * VRS +
                                    (dh * DT + dt) * 32 + tr_dim;
