@@ -862,10 +862,9 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
   const int W = blockDim.x >> 6;
   const int rg = lane / R;
   const int c = lane % R;
-  const uint32_t hy = blockIdx.y;  // (KV head, query sub-group)
-  const uint32_t kvh = hy / a.n_sub;
-  const uint32_t sub = hy - kvh * a.n_sub;
   uint32_t b, t0, tend, slot;
+  // (KV head, query sub-group)
+  uint32_t hy = blockIdx.y;
   if (a.items) {  // planned: one work item per grid.x
     const uint4 it = sload4(a.items + blockIdx.x);
     b = it.x;
@@ -877,7 +876,13 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
     t0 = blockIdx.x * a.part_tokens;
     tend = t0 + a.part_tokens;
     slot = a.n_parts > 1 ? b * a.n_parts + blockIdx.x : kNoSlot;
+    // Workgroups go to the XCDs round robin by linear id, and with one
+    // partition the id is hy + gridDim.y * b: rotate hy by the sequence so
+    // each XCD serves every head, not one fixed head's tiles of each block.
+    hy = (hy + b) % gridDim.y;
   }
+  const uint32_t kvh = hy / a.n_sub;
+  const uint32_t sub = hy - kvh * a.n_sub;
   const uint32_t h0 = kvh * a.group + sub * GT;
   const uint32_t ng = min((uint32_t)GT, a.group - sub * GT);
   // Block ids are wave-uniform: read through the constant address space so
@@ -1257,9 +1262,8 @@ __global__ void __launch_bounds__(256) decode_f32_kernel(DecodeArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int W = blockDim.x >> 6;
   const int rg = lane / R, c = lane % R;
-  const uint32_t kvh = blockIdx.y / a.n_sub;
-  const uint32_t sub = blockIdx.y - kvh * a.n_sub;
   uint32_t b, t0, tend, slot;
+  uint32_t hy = blockIdx.y;
   if (a.items) {
     const uint4 it = sload4(a.items + blockIdx.x);
     b = it.x;
@@ -1271,7 +1275,10 @@ __global__ void __launch_bounds__(256) decode_f32_kernel(DecodeArgs a) {
     t0 = blockIdx.x * a.part_tokens;
     tend = t0 + a.part_tokens;
     slot = a.n_parts > 1 ? b * a.n_parts + blockIdx.x : kNoSlot;
+    hy = (hy + b) % gridDim.y;  // (as in the f16 kernel: heads over XCDs)
   }
+  const uint32_t kvh = hy / a.n_sub;
+  const uint32_t sub = hy - kvh * a.n_sub;
   const uint32_t h0 = kvh * a.group + sub * GT;
   const uint32_t ng = min((uint32_t)GT, a.group - sub * GT);
   typedef const __attribute__((address_space(4))) uint32_t cu32;
