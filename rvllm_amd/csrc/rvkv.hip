@@ -2507,6 +2507,36 @@ int plan_build(rvkv_decode_plan *pl, const uint32_t *ctx_lens_host,
     std::vector<uint4> sorted(items.size());
     for (size_t i = 0; i < order.size(); ++i) sorted[i] = items[order[i]];
     items.swap(sorted);
+    // Shared-prefix group items read the same blocks: put them 8 grid
+    // positions apart, so (workgroups going to the XCDs round robin by
+    // linear id) every one of them runs on the same XCD, close together in
+    // time, and each prefix block is fetched into that XCD's L2 once
+    // instead of once per XCD. (RVKV_DECODE_GROUP_XCD=0: plain order.)
+    static const char *gx = getenv("RVKV_DECODE_GROUP_XCD");
+    std::vector<uint4> gi, rest;
+    size_t first_g = items.size();
+    for (size_t i = 0; i < items.size(); ++i) {
+      if (items[i].x & kGroupItem) {
+        if (gi.empty()) first_g = i;
+        gi.push_back(items[i]);
+      } else {
+        rest.push_back(items[i]);
+      }
+    }
+    const size_t n = items.size();
+    if (!(gx && gx[0] == '0') && gi.size() > 1 &&
+        8 * (gi.size() - 1) < n) {
+      size_t p0 = first_g & ~(size_t)7;
+      while (p0 + 8 * (gi.size() - 1) >= n) p0 -= 8;
+      std::vector<char> taken(n, 0);
+      for (size_t i = 0; i < gi.size(); ++i) {
+        items[p0 + 8 * i] = gi[i];
+        taken[p0 + 8 * i] = 1;
+      }
+      size_t r = 0;
+      for (size_t i = 0; i < n; ++i)
+        if (!taken[i]) items[i] = rest[r++];
+    }
   } else {
     std::stable_sort(items.begin(), items.end(),
                      [](const uint4 &x, const uint4 &y) {
