@@ -97,6 +97,13 @@ def parse():
     p.add_argument("--graph", action="store_true",
                    help="time the step as one HIP graph replay (all layers' "
                         "append + decode launches captured once)")
+    p.add_argument("--traffic-pass", action="store_true",
+                   help="internal: a short headline decode after a 2 GiB "
+                        "device copy, run under rocprofv3 --pmc by the "
+                        "default run to measure HBM traffic per launch")
+    p.add_argument("--no-traffic", dest="traffic", action="store_false",
+                   help="default run only: skip the live counter passes "
+                        "(traffic then comes from profiles/)")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only time a plain 2 GiB device-to-device copy (the "
                         "achievable-bandwidth and PMC-counter reference)")
@@ -1084,6 +1091,9 @@ def main():
     if args.copy_calibration:
         copy_calibration(torch, max(args.steps, 5))
         return
+    if args.traffic_pass:
+        traffic_pass(args, torch, W)
+        return
     if args.churn:
         print(json.dumps(run_churn(args, torch, W)), flush=True)
         return
@@ -1124,6 +1134,11 @@ def main():
         pre["command"] = ("python3 bench.py (after the headline, same "
                           "process); alone: python3 bench.py --prefill f32")
         res["secondary"] = secondary_records(args, torch, W) + [pre]
+        if args.traffic:
+            live = live_traffic(args)
+            if live is not None:
+                res["roofline"]["traffic"] = live.pop("traffic")
+                res["roofline"]["traffic_source"] = live
     print(json.dumps(res), flush=True)
 
 
@@ -1179,6 +1194,100 @@ def secondary_records(args, torch, W):
         rec["command"] = "python3 bench.py --no-cpu " + " ".join(extra)
         out.append(rec)
     return out
+
+
+def traffic_pass(args, torch, W):
+    """What the counter passes of live_traffic profile: two launches of the
+    calibration library's copy probe, each reading 2 GiB and writing 2 GiB
+    (the counters' scale), then the headline decode for a few steps (no
+    ceilings, no CPU leg)."""
+    import ctypes
+
+    from rvllm_amd import _lib
+    lib = _lib.load_calib()
+    n = 2 << 30
+    a = torch.zeros(n // 4, dtype=torch.int32, device="cuda")
+    b = torch.empty_like(a)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for _ in range(2):
+        _lib.check_calib(lib.rvkv_calib_copy_probe(
+            ctypes.c_void_p(a.data_ptr()), ctypes.c_void_p(b.data_ptr()),
+            n, n, 16384, stream))
+    torch.cuda.synchronize()
+    del a, b
+    torch.cuda.empty_cache()
+    run_decode(argparse.Namespace(**{**vars(args), "steps": 2, "warmup": 1}),
+               torch, W, cpu=False)
+
+
+def live_traffic(args):
+    """HBM bytes per headline decode launch, measured in this run: two child
+    processes run the traffic pass under rocprofv3 --pmc, one with
+    FETCH_SIZE and one with WRITE_SIZE (KiB per dispatch); each is scaled by
+    what the same counter reads for a copy probe launch that reads 2 GiB
+    and writes 2 GiB, in the same pass. Returns
+    {traffic, ...details} or None (the profiler missing or failing; the
+    record then keeps the committed profile's figure)."""
+    import csv
+    import shutil
+    import subprocess
+    import tempfile
+    prof = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    if not os.path.exists(prof):
+        return None
+    per = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        time.sleep(PAUSE_AFTER_FREE_S)
+        d = tempfile.mkdtemp(prefix="rvkv_pmc_", dir="/tmp")
+        cmd = [prof, "--pmc", counter, "--kernel-include-regex",
+               "decode_part_kernel|decode_reduce_kernel|copy_probe_kernel",
+               "-f", "csv", "-d", d, "-o", "run", "--", sys.executable,
+               os.path.abspath(__file__), "--traffic-pass", "--no-cpu",
+               "--config", args.config]
+        try:
+            p = subprocess.run(cmd, capture_output=True, text=True,
+                               timeout=300, cwd="/tmp",
+                               env={**os.environ, "TMPDIR": "/tmp"})
+        except subprocess.TimeoutExpired:
+            return None
+        rows = []
+        for root, _, files in os.walk(d):
+            for fn in files:
+                if fn.endswith("counter_collection.csv"):
+                    with open(os.path.join(root, fn)) as f:
+                        rows += list(csv.DictReader(f))
+        shutil.rmtree(d, ignore_errors=True)
+        if p.returncode != 0 or not rows:
+            return None
+        vals = {"copy": [], "part": [], "reduce": []}
+        for r in rows:
+            if r.get("Counter_Name") != counter:
+                continue
+            k = r.get("Kernel_Name", "")
+            key = ("copy" if "copy_probe_kernel" in k else
+                   "reduce" if "decode_reduce" in k else
+                   "part" if "decode_part" in k else None)
+            if key:
+                vals[key].append(float(r["Counter_Value"]))
+        if not vals["copy"] or not vals["part"]:
+            return None
+        copy_kib = sum(vals["copy"]) / len(vals["copy"])
+        launch_kib = (sum(vals["part"]) + sum(vals["reduce"])) / len(
+            vals["part"])
+        scale = (2 << 30) / (copy_kib * 1024)
+        per[counter] = {"kib_per_launch": round(launch_kib, 1),
+                        "copy_kib": round(copy_kib, 1),
+                        "scale": round(scale, 6),
+                        "dispatches": len(vals["part"])}
+    traffic = sum(v["kib_per_launch"] * 1024 * v["scale"]
+                  for v in per.values())
+    return {"traffic": int(round(traffic)),
+            "how": "rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, on "
+                   "python3 bench.py --traffic-pass (child processes of "
+                   "this run, after the timed runs); KiB per decode launch "
+                   "x (2 GiB / the same counter's KiB for one copy-probe "
+                   "launch reading and writing 2 GiB)",
+           **{c.lower(): v for c, v in per.items()}}
 
 
 def run_decode(args, torch, W, cpu, keep_pool=False):
@@ -1367,6 +1476,8 @@ def run_decode(args, torch, W, cpu, keep_pool=False):
     }
     # Context for frac: the best plain read of the same bytes per launch,
     # contiguous and as randomly placed cache tiles.
+    if getattr(args, "traffic_pass", False):
+        return res
     rc = read_ceiling(torch, dec_bytes, max(args.steps, 3))
     rc["frac"] = round(achieved / rc["GB/s"], 4)
     res["roofline"]["stream_read_ceiling"] = rc
