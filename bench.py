@@ -1192,6 +1192,11 @@ def secondary_records(args, torch, W):
         rec = _child_record(args, extra)
         rec = _secondary(rec, role)
         rec["command"] = "python3 bench.py --no-cpu " + " ".join(extra)
+        if args.traffic and "--batch" in extra:
+            live = live_traffic(args, extra[:6])
+            if live is not None:
+                rec["roofline"]["traffic"] = live.pop("traffic")
+                rec["roofline"]["traffic_source"] = live
         out.append(rec)
     return out
 
@@ -1220,7 +1225,7 @@ def traffic_pass(args, torch, W):
                torch, W, cpu=False)
 
 
-def live_traffic(args):
+def live_traffic(args, extra=None):
     """HBM bytes per headline decode launch, measured in this run: two child
     processes run the traffic pass under rocprofv3 --pmc, one with
     FETCH_SIZE and one with WRITE_SIZE (KiB per dispatch); each is scaled by
@@ -1242,8 +1247,8 @@ def live_traffic(args):
         cmd = [prof, "--pmc", counter, "--kernel-include-regex",
                "decode_part_kernel|decode_reduce_kernel|copy_probe_kernel",
                "-f", "csv", "-d", d, "-o", "run", "--", sys.executable,
-               os.path.abspath(__file__), "--traffic-pass", "--no-cpu",
-               "--config", args.config]
+               os.path.abspath(__file__), "--traffic-pass", "--no-cpu"] + (
+                   extra if extra is not None else ["--config", args.config])
         try:
             p = subprocess.run(cmd, capture_output=True, text=True,
                                timeout=300, cwd="/tmp",
