@@ -26,9 +26,14 @@ SOURCES = [
 ]
 
 # Packed-FP32 instructions are kept out of generated code on purpose.
+# Kernel-argument preload: a kernel's first six scalar or pointer arguments
+# arrive in SGPRs (the decode kernels take the inputs of their start-up
+# chain that way), so their first table read needs no argument load; on
+# firmware without preload the code object's own prologue loads them.
 HIP_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-kernarg-preload-count=6",
     "-Wall", "-Wno-unused-result",
 ]
 

@@ -847,7 +847,12 @@ __device__ __forceinline__ void decode_chunk(SoftmaxState<GT, NL> &st,
 // normalised output; otherwise it writes its partial (m, l, acc) and the
 // reduction kernel merges the partitions.
 template <int HD, int GT, int U, int NL, bool RAGGED>
-__global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
+__global__ void __launch_bounds__(256) decode_part_kernel(
+    const uint4 *p_items, const uint32_t *p_tables, const uint32_t *p_ctx,
+    uint32_t p_mb, uint32_t p_bs, uint32_t p_pt, DecodeArgs a) {
+  // (The start-up chain's inputs come as leading arguments, which the
+  // build preloads into SGPRs: no argument load before the first table
+  // read. a holds the same values.)
   constexpr int R = HD / (8 * NL);  // lanes per K/V row
   constexpr int RPL = 64 / R;       // rows (tokens) per wave-wide load
   constexpr int TC = U * RPL;       // tokens per chunk
@@ -865,16 +870,16 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
   uint32_t b, t0, tend, slot;
   // (KV head, query sub-group)
   uint32_t hy = blockIdx.y;
-  if (a.items) {  // planned: one work item per grid.x
-    const uint4 it = sload4(a.items + blockIdx.x);
+  if (p_items) {  // planned: one work item per grid.x
+    const uint4 it = sload4(p_items + blockIdx.x);
     b = it.x;
     t0 = it.y;
     tend = it.z;
     slot = it.w;
   } else {  // uniform: fixed-size partitions of every sequence
     b = blockIdx.z;
-    t0 = blockIdx.x * a.part_tokens;
-    tend = t0 + a.part_tokens;
+    t0 = blockIdx.x * p_pt;
+    tend = t0 + p_pt;
     slot = a.n_parts > 1 ? b * a.n_parts + blockIdx.x : kNoSlot;
     // Workgroups go to the XCDs round robin by linear id, and with one
     // partition the id is hy + gridDim.y * b: rotate hy by the sequence so
@@ -889,16 +894,16 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
   // they are scalar loads into SGPRs (a plain pointer may be reloaded with
   // vector loads, since the kernel also stores to global memory).
   typedef const __attribute__((address_space(4))) uint32_t cu32;
-  cu32 *table = (cu32 *)(uintptr_t)(a.tables + (size_t)b * a.max_blocks);
+  cu32 *table = (cu32 *)(uintptr_t)(p_tables + (size_t)b * p_mb);
   const uint32_t first = t0 + (uint32_t)wave * TC;  // this wave's 1st chunk
 
   // The first block ids depend only on the partition: their scalar loads go
   // out together with the ctx_len load (clamped to the table for now).
-  const uint32_t mb1 = a.max_blocks - 1;
+  const uint32_t mb1 = p_mb - 1;
   uint32_t ids[U];
 #pragma unroll
   for (int u = 0; u < U; ++u)
-    ids[u] = table[min((first + u * RPL) >> a.bs_log2, mb1)];
+    ids[u] = table[min((first + u * RPL) >> p_bs, mb1)];
 
   // Row length in elements: HD, or (RAGGED) the cache's head_dim, whose
   // lanes past its end hold zeros.
@@ -926,13 +931,13 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
     }
   }
 
-  uint32_t ctx = sload(a.ctx_lens + b);
+  uint32_t ctx = sload(p_ctx + b);
   ctx = min(ctx, a.ctx_cap);
   const uint32_t lo =
       (a.window > 0 && ctx > (uint32_t)a.window) ? ctx - (uint32_t)a.window : 0;
   const uint32_t t1 = min(tend, ctx);
   // A sequence that one partition covers writes its output directly.
-  if (!a.items && ctx <= a.part_tokens) slot = kNoSlot;
+  if (!p_items && ctx <= p_pt) slot = kNoSlot;
 
   if (t0 >= t1) {
     // Past the end of this sequence (the reduction never reads it). An
@@ -994,8 +999,8 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
       }
     }
 
-    const uint32_t bs_mask = (1u << a.bs_log2) - 1u;
-    const uint32_t last_blk = (ctx - 1) >> a.bs_log2;
+    const uint32_t bs_mask = (1u << p_bs) - 1u;
+    const uint32_t last_blk = (ctx - 1) >> p_bs;
     // Byte offsets: the uniform part (block, head, first row of the load)
     // is scalar; the per-lane part is a constant 32-bit offset.
     const char *kbase = reinterpret_cast<const char *>(a.kc) +
@@ -1004,10 +1009,10 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
                         (size_t)kvh * a.head_stride * 2;
     const uint32_t lane_off = (uint32_t)(rg * hdr * 2 + c * 16);
     const uint64_t blk_bytes = a.block_stride * 2;
-    if (start != first || last_blk < ((first + TC - 1) >> a.bs_log2)) {
+    if (start != first || last_blk < ((first + TC - 1) >> p_bs)) {
 #pragma unroll
       for (int u = 0; u < U; ++u)
-        ids[u] = table[min((start + u * RPL) >> a.bs_log2, last_blk)];
+        ids[u] = table[min((start + u * RPL) >> p_bs, last_blk)];
     }
 
     const char *zero_v = reinterpret_cast<const char *>(g_zero_rows) + lane_off;
@@ -1057,7 +1062,7 @@ __global__ void __launch_bounds__(256) decode_part_kernel(DecodeArgs a) {
     auto fetch_ids = [&](uint32_t (&cid)[U], uint32_t ch) {
 #pragma unroll
       for (int u = 0; u < U; ++u)
-        cid[u] = table[min((ch + u * RPL) >> a.bs_log2, last_blk)];
+        cid[u] = table[min((ch + u * RPL) >> p_bs, last_blk)];
     };
     auto consume = [&](uint4 (&kr)[U][NL], uint4 (&vr)[U][NL], uint32_t ch,
                        uint32_t okmask, bool full) {
@@ -1535,15 +1540,19 @@ __global__ void __launch_bounds__(256) decode_f32_kernel(DecodeArgs a) {
 // out = sum_i 2^(m_i - M) acc_i / sum_i 2^(m_i - M) l_i. Partitions that saw
 // no visible key carry l = 0 and are skipped.
 template <int HD>
-__global__ void __launch_bounds__(64) decode_reduce_kernel(DecodeArgs a) {
+__global__ void __launch_bounds__(64) decode_reduce_kernel(
+    const uint4 *p_reds, const float *p_ml, const float *p_acc,
+    uint32_t p_nh, DecodeArgs a) {
+  // (Leading arguments preloaded into SGPRs by the build; a holds the same
+  // values.)
   constexpr int EPL = HD / 64 > 0 ? HD / 64 : 1;  // elements per lane
   const uint32_t h = blockIdx.x;
   const int lane = threadIdx.x;
   uint32_t b, slot0, np;
-  if (a.reds) {
+  if (p_reds) {
     // The row is wave-uniform: scalar loads (constant address space).
     typedef const __attribute__((address_space(4))) uint32_t cu32;
-    cu32 *r = (cu32 *)(uintptr_t)(a.reds + blockIdx.y);
+    cu32 *r = (cu32 *)(uintptr_t)(p_reds + blockIdx.y);
     b = r[0];
     slot0 = r[1];
     np = r[2];
@@ -1554,11 +1563,11 @@ __global__ void __launch_bounds__(64) decode_reduce_kernel(DecodeArgs a) {
     slot0 = b * a.n_parts;
     np = (ctx + a.part_tokens - 1) / a.part_tokens;
   }
-  const float *ml = a.ws_ml + ((size_t)slot0 * a.n_heads + h) * 2;
-  const size_t ml_step = (size_t)a.n_heads * 2;
-  const float *accp = a.ws_acc + ((size_t)slot0 * a.n_heads + h) * HD;
-  const size_t acc_step = (size_t)a.n_heads * HD;
-  const size_t hrow = (size_t)b * a.n_heads + h;
+  const float *ml = p_ml + ((size_t)slot0 * p_nh + h) * 2;
+  const size_t ml_step = (size_t)p_nh * 2;
+  const float *accp = p_acc + ((size_t)slot0 * p_nh + h) * HD;
+  const size_t acc_step = (size_t)p_nh * HD;
+  const size_t hrow = (size_t)b * p_nh + h;
   if (np <= 8) {
     // Few partitions (the common case): every (m, l) pair (uniform loads)
     // and every partial row are fetched at once, one round trip in all.
@@ -1806,16 +1815,20 @@ void launch_decode(const DecodeArgs &a, dim3 grid, hipStream_t st) {
                        a);
   else if (a.hd != HD)  // a head_dim below HD: rows read element by element
     hipLaunchKernelGGL((decode_part_kernel<HD, GT, 4, 1, true>), grid,
-                       dim3(64 * W), lds, st, a);
+                       dim3(64 * W), lds, st, a.items, a.tables,
+                       a.ctx_lens, a.max_blocks, a.bs_log2, a.part_tokens, a);
   else if (u8)
     hipLaunchKernelGGL((decode_part_kernel<HD, GT, 8, 1, false>), grid,
-                       dim3(64 * W), lds, st, a);
+                       dim3(64 * W), lds, st, a.items, a.tables,
+                       a.ctx_lens, a.max_blocks, a.bs_log2, a.part_tokens, a);
   else if (u2)
     hipLaunchKernelGGL((decode_part_kernel<HD, GT, 2, 1, false>), grid,
-                       dim3(64 * W), lds, st, a);
+                       dim3(64 * W), lds, st, a.items, a.tables,
+                       a.ctx_lens, a.max_blocks, a.bs_log2, a.part_tokens, a);
   else
     hipLaunchKernelGGL((decode_part_kernel<HD, GT, 4, 1, false>), grid,
-                       dim3(64 * W), lds, st, a);
+                       dim3(64 * W), lds, st, a.items, a.tables,
+                       a.ctx_lens, a.max_blocks, a.bs_log2, a.part_tokens, a);
 }
 
 template <int HD>
@@ -2201,10 +2214,10 @@ int launch_decode_pair(const char *op, const DecodeArgs &a, uint32_t hd,
   }
   if (reduce) {
     switch (hd) {
-      case 32: hipLaunchKernelGGL(decode_reduce_kernel<32>, rgrid, dim3(64), 0, st, a); break;
-      case 64: hipLaunchKernelGGL(decode_reduce_kernel<64>, rgrid, dim3(64), 0, st, a); break;
-      case 128: hipLaunchKernelGGL(decode_reduce_kernel<128>, rgrid, dim3(64), 0, st, a); break;
-      default: hipLaunchKernelGGL(decode_reduce_kernel<256>, rgrid, dim3(64), 0, st, a); break;
+      case 32: hipLaunchKernelGGL(decode_reduce_kernel<32>, rgrid, dim3(64), 0, st, a.reds, a.ws_ml, a.ws_acc, a.n_heads, a); break;
+      case 64: hipLaunchKernelGGL(decode_reduce_kernel<64>, rgrid, dim3(64), 0, st, a.reds, a.ws_ml, a.ws_acc, a.n_heads, a); break;
+      case 128: hipLaunchKernelGGL(decode_reduce_kernel<128>, rgrid, dim3(64), 0, st, a.reds, a.ws_ml, a.ws_acc, a.n_heads, a); break;
+      default: hipLaunchKernelGGL(decode_reduce_kernel<256>, rgrid, dim3(64), 0, st, a.reds, a.ws_ml, a.ws_acc, a.n_heads, a); break;
     }
   }
   hipError_t e = hipGetLastError();
@@ -2214,10 +2227,10 @@ int launch_decode_pair(const char *op, const DecodeArgs &a, uint32_t hd,
 int launch_reduce(const char *op, const DecodeArgs &a, uint32_t hd,
                   dim3 rgrid, hipStream_t st) {
   switch (hd) {
-    case 32: hipLaunchKernelGGL(decode_reduce_kernel<32>, rgrid, dim3(64), 0, st, a); break;
-    case 64: hipLaunchKernelGGL(decode_reduce_kernel<64>, rgrid, dim3(64), 0, st, a); break;
-    case 128: hipLaunchKernelGGL(decode_reduce_kernel<128>, rgrid, dim3(64), 0, st, a); break;
-    default: hipLaunchKernelGGL(decode_reduce_kernel<256>, rgrid, dim3(64), 0, st, a); break;
+    case 32: hipLaunchKernelGGL(decode_reduce_kernel<32>, rgrid, dim3(64), 0, st, a.reds, a.ws_ml, a.ws_acc, a.n_heads, a); break;
+    case 64: hipLaunchKernelGGL(decode_reduce_kernel<64>, rgrid, dim3(64), 0, st, a.reds, a.ws_ml, a.ws_acc, a.n_heads, a); break;
+    case 128: hipLaunchKernelGGL(decode_reduce_kernel<128>, rgrid, dim3(64), 0, st, a.reds, a.ws_ml, a.ws_acc, a.n_heads, a); break;
+    default: hipLaunchKernelGGL(decode_reduce_kernel<256>, rgrid, dim3(64), 0, st, a.reds, a.ws_ml, a.ws_acc, a.n_heads, a); break;
   }
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? RVKV_OK : hip_fail(op, e);
