@@ -1249,11 +1249,18 @@ def live_traffic(args, extra=None):
                "-f", "csv", "-d", d, "-o", "run", "--", sys.executable,
                os.path.abspath(__file__), "--traffic-pass", "--no-cpu"] + (
                    extra if extra is not None else ["--config", args.config])
+        # (its own process group, so a pass that overruns is ended with
+        # the bench child it started)
+        p = subprocess.Popen(cmd, stdout=subprocess.DEVNULL,
+                             stderr=subprocess.DEVNULL, cwd="/tmp",
+                             env={**os.environ, "TMPDIR": "/tmp"},
+                             start_new_session=True)
         try:
-            p = subprocess.run(cmd, capture_output=True, text=True,
-                               timeout=300, cwd="/tmp",
-                               env={**os.environ, "TMPDIR": "/tmp"})
+            p.wait(timeout=150)
         except subprocess.TimeoutExpired:
+            os.killpg(p.pid, 9)
+            p.wait()
+            shutil.rmtree(d, ignore_errors=True)
             return None
         rows = []
         for root, _, files in os.walk(d):
