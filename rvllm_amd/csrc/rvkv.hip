@@ -2520,32 +2520,44 @@ int plan_build(rvkv_decode_plan *pl, const uint32_t *ctx_lens_host,
     std::vector<uint4> sorted(items.size());
     for (size_t i = 0; i < order.size(); ++i) sorted[i] = items[order[i]];
     items.swap(sorted);
-    // Shared-prefix group items read the same blocks: put them 8 grid
-    // positions apart, so (workgroups going to the XCDs round robin by
-    // linear id) every one of them runs on the same XCD, close together in
+    // Shared-prefix group items read the same blocks: the items of one
+    // prefix go 8 grid positions apart, so (workgroups going to the XCDs
+    // round robin by linear id) they run on one XCD, close together in
     // time, and each prefix block is fetched into that XCD's L2 once
-    // instead of once per XCD. (RVKV_DECODE_GROUP_XCD=0: plain order.)
+    // instead of once per XCD; different prefixes take different XCDs.
+    // (RVKV_DECODE_GROUP_XCD=0: plain order.)
     static const char *gx = getenv("RVKV_DECODE_GROUP_XCD");
-    std::vector<uint4> gi, rest;
-    size_t first_g = items.size();
+    std::vector<std::vector<uint4>> lane(8);
+    std::vector<uint4> rest;
+    std::vector<std::pair<uint32_t, uint32_t>> prefix;  // (first block, lane)
+    size_t first_g = items.size(), n_g = 0;
     for (size_t i = 0; i < items.size(); ++i) {
-      if (items[i].x & kGroupItem) {
-        if (gi.empty()) first_g = i;
-        gi.push_back(items[i]);
-      } else {
+      if (!(items[i].x & kGroupItem)) {
         rest.push_back(items[i]);
+        continue;
       }
+      if (n_g++ == 0) first_g = i;
+      // A prefix is named by the first block its first member's table holds.
+      const uint32_t sq = glist[(items[i].x & ~kGroupItem) + 1];
+      const uint32_t key = tables_host[(size_t)sq * max_blocks];
+      size_t k = 0;
+      while (k < prefix.size() && prefix[k].first != key) ++k;
+      if (k == prefix.size()) prefix.push_back({key, (uint32_t)(k % 8)});
+      lane[prefix[k].second].push_back(items[i]);
     }
     const size_t n = items.size();
-    if (!(gx && gx[0] == '0') && gi.size() > 1 &&
-        8 * (gi.size() - 1) < n) {
+    size_t span = 0;  // positions the longest lane needs
+    for (int l = 0; l < 8; ++l)
+      if (!lane[l].empty()) span = std::max(span, l + 8 * (lane[l].size() - 1) + 1);
+    if (!(gx && gx[0] == '0') && n_g > 1 && span <= n) {
       size_t p0 = first_g & ~(size_t)7;
-      while (p0 + 8 * (gi.size() - 1) >= n) p0 -= 8;
+      while (p0 + span > n) p0 -= 8;
       std::vector<char> taken(n, 0);
-      for (size_t i = 0; i < gi.size(); ++i) {
-        items[p0 + 8 * i] = gi[i];
-        taken[p0 + 8 * i] = 1;
-      }
+      for (int l = 0; l < 8; ++l)
+        for (size_t j = 0; j < lane[l].size(); ++j) {
+          items[p0 + l + 8 * j] = lane[l][j];
+          taken[p0 + l + 8 * j] = 1;
+        }
       size_t r = 0;
       for (size_t i = 0; i < n; ++i)
         if (!taken[i]) items[i] = rest[r++];
