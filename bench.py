@@ -1350,16 +1350,17 @@ def run_decode(args, torch, W, cpu, keep_pool=False):
             raise SystemExit("--graph cannot capture the per-step plan "
                              "rebuild; use --no-plan with --graph")
 
-    # The library's choice for planned decodes of large groups (hd 64,
-    # group >= 5): the matrix-core decode, preceded by its own append.
-    mfma = (plan is not None and c.head_dim == 64 and
-            c.n_heads // c.n_kv_heads >= 5 and
+    # The library's choice for groups of four and more at head_dim 64 on an
+    # f16 pool, with or without a plan: the matrix-core decode.
+    mfma = (not f32 and c.head_dim == 64 and
+            c.n_heads // c.n_kv_heads >= 4 and
             os.environ.get("RVKV_DECODE_MFMA", "") != "0")
     if mfma:
         decode_kernels = ("prefill_kernel<64, 1> in decode mode (matrix "
                           "cores" + ("" if args.unfused else
                                      ", fused append (rvkv_decode_step)")
-                          + ") + decode_reduce_kernel for split sequences")
+                          + ") + decode_reduce_kernel for split sequences"
+                          " or partitions")
     else:
         decode_kernels = ("decode_part_kernel (+ decode_reduce_kernel for "
                           "split sequences)" + ("" if args.unfused else

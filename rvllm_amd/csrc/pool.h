@@ -39,7 +39,10 @@ int hip_fail(const char *op, hipError_t e);
 // Matrix-core decode over a decode plan's work items (prefill.hip): used
 // for large GQA groups, where the VALU decode is instruction-bound. groups:
 // the plan's shared-prefix member lists (items flagged 0x80000000 in their
-// seq field index them).
+// seq field index them). items NULL: decode without a plan, n_items =
+// batch * dec_parts uniform partitions of dec_part_tokens keys, read counts
+// capped at dec_ctx_cap (partials to ws_acc / ws_ml slot sequence *
+// dec_parts + partition, merged by the uniform reduction pass).
 bool mfma_decode_wanted(const rvkv_pool *pool, uint32_t n_heads);
 int mfma_decode(const rvkv_pool *pool, uint32_t layer, const float *q,
                 const uint32_t *tables, const uint32_t *ctx_lens,
@@ -49,7 +52,9 @@ int mfma_decode(const rvkv_pool *pool, uint32_t layer, const float *q,
                 const void *new_k = nullptr, const void *new_v = nullptr,
                 const uint32_t *new_blk = nullptr,
                 const uint32_t *new_off = nullptr, bool new_f32 = false,
-                const uint32_t *groups = nullptr);
+                const uint32_t *groups = nullptr, uint32_t dec_parts = 0,
+                uint32_t dec_part_tokens = 0,
+                uint32_t dec_ctx_cap = 0xFFFFFFFFu);
 // Paged attention for shapes the tuned kernels do not take (generic.hip):
 // any head_dim <= 1024, any block size, f16 or f32 cells, f32 arithmetic.
 // pos_offset NULL: decode (one row per sequence at read_num - 1). Keys

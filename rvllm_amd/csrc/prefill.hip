@@ -145,6 +145,12 @@ struct PrefillArgs {
   // list {n, n sequences, n slots}; the group's n * group query rows share
   // the item's key range, whose blocks all members' tables hold alike.
   const uint32_t *groups;
+  // Decode mode without a plan (items NULL, dec_parts > 0): grid.x =
+  // sequence * dec_parts + partition, each partition dec_part_tokens keys
+  // (slot = sequence * dec_parts + partition when the sequence spans more
+  // than one, else the output is written), read counts capped at
+  // dec_ctx_cap, as the VALU decode's uniform mode does.
+  uint32_t dec_parts, dec_part_tokens, dec_ctx_cap;
   float *ws_acc, *ws_ml;
   // Fused append (decode mode): this step's K/V row of every sequence
   // ([batch, n_kv, hd], f32 or f16) goes to slot (new_blk[b], new_off[b])
@@ -321,6 +327,14 @@ __global__ void __launch_bounds__(
       n_mem = gl[0];
       b = gl[1];
     }
+  } else if (a.dec_parts) {  // uniform decode partitions
+    b = blockIdx.x / a.dec_parts;
+    const uint32_t part = blockIdx.x - b * a.dec_parts;
+    item_lo = part * a.dec_part_tokens;
+    item_hi = item_lo + a.dec_part_tokens;
+    slot = a.dec_parts > 1 ? blockIdx.x : kNoSlot;
+    kvh = blockIdx.y;
+    tile = 0;
   } else {
     const uint32_t n_wg = a.n_tiles * a.n_kv * a.batch;
     const uint32_t w = blockIdx.x, xcd = w % 8, idx = w / 8;
@@ -344,11 +358,23 @@ __global__ void __launch_bounds__(
   // sequence wraps to 2^32 - 1 and sees no key).
   // (b is uniform: the per-sequence words come by scalar loads)
   typedef const __attribute__((address_space(4))) uint32_t cu32s;
-  const uint32_t rn = *(cu32s *)(uintptr_t)(a.read_num + b);
+  const bool decode = a.items || a.dec_parts;
+  const uint32_t rn = a.dec_parts
+                          ? min(*(cu32s *)(uintptr_t)(a.read_num + b),
+                                a.dec_ctx_cap)
+                          : *(cu32s *)(uintptr_t)(a.read_num + b);
   const uint32_t off =
-      a.items ? rn - 1u : *(cu32s *)(uintptr_t)(a.pos_offset + b);
+      decode ? rn - 1u : *(cu32s *)(uintptr_t)(a.pos_offset + b);
   const uint32_t cap = a.max_blocks << a.bs_log2;
   const uint32_t ctx = min(rn, cap);
+  if (a.dec_parts) {
+    // One partition covers the sequence: its output is written directly
+    // (the reduction skips it). A partition past the sequence's end has
+    // nothing to do (the reduction never reads it); an empty sequence gets
+    // its zero row from partition 0.
+    if (ctx <= a.dec_part_tokens) slot = kNoSlot;
+    if (item_lo >= ctx && item_lo > 0) return;
+  }
   const uint32_t *table = a.tables + (size_t)b * a.max_blocks;
 
   // Query rows of this (sequence, KV head): group * q_len, or a group
@@ -1160,7 +1186,11 @@ bool mfma_decode_wanted(const rvkv_pool *pool, uint32_t n_heads) {
                         pool->block_size <= 256;
   if (env && env[0] == '0') return false;
   if (env && env[0] == '1') return shape_ok;
-  return shape_ok && group >= 5;
+  // From four query heads per KV head the matrix cores beat the VALU
+  // decode: Llama-3.2-1B's shape (G = 4) at 64 x 2048 49.9 vs 52.7 us a
+  // layer, at 256 x 4096 326 vs 343 us (with items of about half a
+  // sequence); below four the VALU decode's work per key is small enough.
+  return shape_ok && group >= 4;
 }
 
 int mfma_decode(const rvkv_pool *pool, uint32_t layer, const float *q,
@@ -1170,7 +1200,8 @@ int mfma_decode(const rvkv_pool *pool, uint32_t layer, const float *q,
                 float *ws_acc, float *ws_ml, float *out, const void *new_k,
                 const void *new_v, const uint32_t *new_blk,
                 const uint32_t *new_off, bool new_f32,
-                const uint32_t *groups) {
+                const uint32_t *groups, uint32_t dec_parts,
+                uint32_t dec_part_tokens, uint32_t dec_ctx_cap) {
   const char *op = "paged_decode";
   if (n_items == 0) return RVKV_OK;
   PrefillArgs a{};
@@ -1199,6 +1230,9 @@ int mfma_decode(const rvkv_pool *pool, uint32_t layer, const float *q,
   a.n_kv = pool->n_kv;
   a.items = items;
   a.groups = groups;
+  a.dec_parts = items ? 0u : dec_parts;
+  a.dec_part_tokens = dec_part_tokens;
+  a.dec_ctx_cap = dec_ctx_cap;
   a.ws_acc = ws_acc;
   a.ws_ml = ws_ml;
   a.new_k = new_k;

@@ -1720,6 +1720,19 @@ uint32_t partition_tokens(const rvkv_pool *p, uint32_t batch, uint32_t n_heads,
                           uint32_t max_ctx) {
   static const uint32_t forced = env_u32("RVKV_DECODE_PART_TOKENS");
   if (forced >= 256 && (forced & (forced - 1)) == 0) return forced;
+  if (rvkv_detail::mfma_decode_wanted(p, n_heads)) {
+    // The matrix-core decode (one wave a partition): enough partitions for
+    // ~1024 waves, and at most 4096 keys a wave, so one long sequence does
+    // not set the launch's tail alone (Llama-3.2-1B's shape: 64 x 2048 at
+    // 1024 keys 49.9 us a layer against 62.6 at 2048; 256 x 4096 at 4096,
+    // no reduction, 326 us against 339 at 2048).
+    const uint64_t pairs = (uint64_t)batch * p->n_kv;
+    const uint64_t parts = pairs >= 1024 ? 1 : (1024 + pairs - 1) / pairs;
+    const uint64_t per = (max_ctx + parts - 1) / parts;
+    uint32_t P = 256;
+    while (P < per && P < 4096) P <<= 1;
+    return P;
+  }
   uint32_t group = n_heads / (p->n_kv ? p->n_kv : 1);
   uint32_t n_sub, gt;
   subgroups(group ? group : 1, &n_sub, &gt);
@@ -2310,10 +2323,15 @@ int plan_build(rvkv_decode_plan *pl, const uint32_t *ctx_lens_host,
   // Tokens per work item: about one sequence, but at least enough that the
   // grid has <= ~1024 workgroups and at most what keeps >= ~256 of them.
   // The matrix-core decode runs one wave per item (the VALU decode four),
-  // so it gets items a quarter as long and four times as many.
+  // so it gets items a quarter as long and four times as many at GQA
+  // groups of five and more, half as long at four (Llama-3.2-1B's shape:
+  // 49.9 us a layer at 64 x 2048 against 62.6 with whole sequences; the
+  // quarter measured best for Qwen2.5's group of seven).
   const bool mfma = rvkv_detail::mfma_decode_wanted(pool, pl->n_heads);
   static const uint32_t forced_div = env_u32("RVKV_DECODE_PLAN_DIV");
-  const double per = forced_div ? (double)forced_div : (mfma ? 4.0 : 1.0);
+  const double per =
+      forced_div ? (double)forced_div
+                 : (mfma ? (pl->n_heads / pool->n_kv >= 5 ? 4.0 : 2.0) : 1.0);
   const double avg = (double)total / batch / per;
   const double lo_p = (double)total * n_hy / (1024.0 * per);
   const double hi_p = (double)total * n_hy / (256.0 * per);
@@ -2725,6 +2743,21 @@ int paged_decode_ws(const char *op, const rvkv_pool *pool, uint32_t layer,
                     uint32_t max_ctx_len, float scale, int32_t window,
                     float *out, void *ws, size_t ws_bytes, bool no_alloc);
 
+// A decode without a plan on the matrix cores: a.n_parts uniform
+// partitions of a.part_tokens keys a sequence (one wave each), then the
+// uniform reduction pass when some sequence spans several.
+int uniform_mfma(const char *op, const rvkv_pool *pool, uint32_t layer,
+                 const DecodeArgs &a, uint32_t batch, float scale) {
+  int rc = rvkv_detail::mfma_decode(
+      pool, layer, a.q, a.tables, a.ctx_lens, a.max_blocks, a.n_heads, scale,
+      a.window, nullptr, batch * a.n_parts, a.ws_acc, a.ws_ml, a.out,
+      a.new_k, a.new_v, a.new_blk, a.new_off, a.new_f32 != 0, nullptr,
+      a.n_parts, a.part_tokens, a.ctx_cap);
+  if (rc || a.n_parts <= 1) return rc;
+  return launch_reduce(op, a, decode_hd(pool->head_dim),
+                       dim3(a.n_heads, batch), pool->stream);
+}
+
 }  // namespace
 
 extern "C" {
@@ -2797,8 +2830,11 @@ int paged_decode_ws(const char *op, const rvkv_pool *pool, uint32_t layer,
   if (ordered &&
       (rc = scratch_acquire(op, pool->device, pool->stream, &capturing)))
     return rc;
-  rc = launch_decode_pair(op, a, decode_hd(pool->head_dim), gt, grid,
-                          dim3(n_heads, batch), w.n_parts > 1, pool->stream);
+  rc = rvkv_detail::mfma_decode_wanted(pool, n_heads)
+           ? uniform_mfma(op, pool, layer, a, batch, scale)
+           : launch_decode_pair(op, a, decode_hd(pool->head_dim), gt, grid,
+                                dim3(n_heads, batch), w.n_parts > 1,
+                                pool->stream);
   if (rc == RVKV_OK && ordered && !capturing)
     rc = scratch_release(op, pool->device, pool->stream);
   return rc;
@@ -2985,6 +3021,8 @@ int rvkv_decode_step(rvkv_pool *pool, const rvkv_decode_plan *plan,
   a.n_parts = w.n_parts;
   a.avg_tokens = a.part_tokens < max_ctx_len ? a.part_tokens : max_ctx_len;
   a.max_tokens = a.avg_tokens;
+  if (rvkv_detail::mfma_decode_wanted(pool, n_heads))
+    return uniform_mfma(op, pool, layer, a, batch, scale);
   const dim3 grid(w.n_parts, pool->n_kv * a.n_sub, batch);
   return launch_decode_pair(op, a, decode_hd(pool->head_dim), gt, grid,
                             dim3(n_heads, batch), w.n_parts > 1, pool->stream);
