@@ -1245,7 +1245,8 @@ def live_traffic(args, extra=None):
         time.sleep(PAUSE_AFTER_FREE_S)
         d = tempfile.mkdtemp(prefix="rvkv_pmc_", dir="/tmp")
         cmd = [prof, "--pmc", counter, "--kernel-include-regex",
-               "decode_part_kernel|decode_reduce_kernel|copy_probe_kernel",
+               "decode_part_kernel|prefill_kernel|decode_reduce_kernel|"
+               "copy_probe_kernel",
                "-f", "csv", "-d", d, "-o", "run", "--", sys.executable,
                os.path.abspath(__file__), "--traffic-pass", "--no-cpu"] + (
                    extra if extra is not None else ["--config", args.config])
@@ -1278,7 +1279,8 @@ def live_traffic(args, extra=None):
             k = r.get("Kernel_Name", "")
             key = ("copy" if "copy_probe_kernel" in k else
                    "reduce" if "decode_reduce" in k else
-                   "part" if "decode_part" in k else None)
+                   "part" if ("decode_part" in k or "prefill_kernel" in k)
+                   else None)
             if key:
                 vals[key].append(float(r["Counter_Value"]))
         if not vals["copy"] or not vals["part"]:
