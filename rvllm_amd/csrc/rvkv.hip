@@ -1805,8 +1805,9 @@ WsLayout ws_layout(const rvkv_pool *p, uint32_t batch, uint32_t n_heads,
 template <int HD, int GT>
 void launch_decode(const DecodeArgs &a, dim3 grid, hipStream_t st) {
   static const uint32_t forced_u = env_u32("RVKV_DECODE_UNROLL");
+  static const uint32_t forced_w = env_u32("RVKV_DECODE_WAVES");
   const uint64_t wgs = (uint64_t)grid.x * grid.y * grid.z;
-  const uint32_t W = decode_waves(wgs, a.max_tokens, GT);
+  uint32_t W = decode_waves(wgs, a.max_tokens, GT);
   // Eight loads per chunk pay off for 512-byte rows, for large groups in
   // single-wave workgroups, and for long items when every wave of the
   // launch fits at two per SIMD (<= 2048 waves; Llama 64 x 2048: 63.0 ->
@@ -1819,6 +1820,12 @@ void launch_decode(const DecodeArgs &a, dim3 grid, hipStream_t st) {
                   (GT <= 4 && a.avg_tokens >= 512 && wgs * W <= 2048));
   const bool u2 = forced_u ? forced_u == 2
                            : GT <= 4 && short_items(wgs, a.max_tokens);
+  // Eight-load kernels hold two waves a SIMD (2048 on the chip): with
+  // 513-1024 uniform workgroups, two waves each keep the launch one
+  // generation long (gemma-3 1024 x 1024: 183.3 -> 180.5 us a layer). (A
+  // plan's ragged items keep four: churn's long-item phase was no faster.)
+  if (!forced_w && !a.items && u8 && W == 4 && wgs > 512 && wgs <= 1024)
+    W = 2;
   // (m, l) pairs rounded up to 16 bytes, then the accumulator rows; at
   // least the f32 kernel's W * GT * (HD + 2) floats.
   const size_t lds =
