@@ -1719,7 +1719,7 @@ uint32_t env_u32(const char *name) {
 uint32_t partition_tokens(const rvkv_pool *p, uint32_t batch, uint32_t n_heads,
                           uint32_t max_ctx) {
   static const uint32_t forced = env_u32("RVKV_DECODE_PART_TOKENS");
-  if (forced >= 256 && (forced & (forced - 1)) == 0) return forced;
+  if (forced >= 256 && forced % 256 == 0) return forced;
   if (rvkv_detail::mfma_decode_wanted(p, n_heads)) {
     // The matrix-core decode (one wave a partition): enough partitions for
     // ~1024 waves, and at most 4096 keys a wave, so one long sequence does
