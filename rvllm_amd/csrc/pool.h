@@ -42,7 +42,9 @@ int hip_fail(const char *op, hipError_t e);
 // seq field index them). items NULL: decode without a plan, n_items =
 // batch * dec_parts uniform partitions of dec_part_tokens keys, read counts
 // capped at dec_ctx_cap (partials to ws_acc / ws_ml slot sequence *
-// dec_parts + partition, merged by the uniform reduction pass).
+// dec_parts + partition, merged by the uniform reduction pass). ksplit 2:
+// each item's keys split over the two waves of its workgroup, merged in
+// the workgroup.
 bool mfma_decode_wanted(const rvkv_pool *pool, uint32_t n_heads);
 int mfma_decode(const rvkv_pool *pool, uint32_t layer, const float *q,
                 const uint32_t *tables, const uint32_t *ctx_lens,
@@ -54,7 +56,7 @@ int mfma_decode(const rvkv_pool *pool, uint32_t layer, const float *q,
                 const uint32_t *new_off = nullptr, bool new_f32 = false,
                 const uint32_t *groups = nullptr, uint32_t dec_parts = 0,
                 uint32_t dec_part_tokens = 0,
-                uint32_t dec_ctx_cap = 0xFFFFFFFFu);
+                uint32_t dec_ctx_cap = 0xFFFFFFFFu, uint32_t ksplit = 1);
 // Paged attention for shapes the tuned kernels do not take (generic.hip):
 // any head_dim <= 1024, any block size, f16 or f32 cells, f32 arithmetic.
 // pos_offset NULL: decode (one row per sequence at read_num - 1). Keys

@@ -275,9 +275,9 @@ __device__ __forceinline__ uint32_t lo_bound(uint32_t p, int32_t window) {
 // matrix work. (With all of O and Q in one wave, head_dim 256 ran one wave
 // per SIMD, its S product serialised on LDS reads: 18 % slower. 128-key
 // tiles at head_dim 64 were measured 7-9 % slower than 64.)
-template <int HD, int WAVES>
+template <int HD, int WAVES, int KSPLIT = 1>
 __global__ void __launch_bounds__(
-    64 * WAVES,
+    64 * WAVES * KSPLIT,
     // (a one-wave workgroup may share a SIMD with others: 2 bounds the
     // registers to two waves per SIMD)
     WAVES == 1 ? 2 : (HD <= 64 ? 12 : 8) / WAVES)
@@ -299,7 +299,32 @@ __global__ void __launch_bounds__(
   static_assert(CHK >= 1 && BN * CPR % NTH == 0, "tile/thread mismatch");
   static_assert(!DMA || ((CPR == 8 || CPR == 16) && !SPLIT && WAVES > 1),
                 "DMA tiles: 8 or 16 chunks a row");
-  extern __shared__ __align__(16) unsigned char smem[];
+  extern __shared__ __align__(16) unsigned char smem_all[];
+  // Decode items split over KSPLIT waves by keys (one-wave workgroups
+  // only): each wave runs the one-wave loop over its share of the item's
+  // keys in its own LDS region, and the waves' softmax states merge at the
+  // end through LDS. tid is the thread's index within its wave then.
+  static_assert(KSPLIT == 1 || WAVES == 1, "key split: one-wave items");
+  const uint32_t kwave =
+      KSPLIT > 1 ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : 0u;
+  unsigned char *const smem = smem_all + kwave * LD::bytes;
+  // Barriers among the threads that share one LDS region: the workgroup,
+  // or with KSPLIT the wave (whose LDS accesses execute in order).
+  auto region_sync = [&]() {
+    if constexpr (KSPLIT > 1) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    } else {
+      __syncthreads();
+    }
+  };
+  auto region_or = [&](int x) {
+    if constexpr (KSPLIT > 1)
+      return __builtin_amdgcn_ballot_w64(x != 0) != 0;
+    else
+      return __syncthreads_or(x) != 0;
+  };
 
   // XCD-aware order: workgroups are dispatched round-robin over the 8 XCDs
   // (each with its own L2), so workgroup w runs on XCD w % 8. Renumber so
@@ -346,7 +371,7 @@ __global__ void __launch_bounds__(
     kvh = (logical / a.n_tiles) % a.n_kv;
     b = logical / a.n_tiles / a.n_kv;
   }
-  const int tid = threadIdx.x;
+  const int tid = KSPLIT > 1 ? (int)(threadIdx.x & 63) : (int)threadIdx.x;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   // Row group of the wave, and the half of the head dimension it holds.
   const uint32_t rgrp = SPLIT ? wave >> 1 : wave;
@@ -374,6 +399,16 @@ __global__ void __launch_bounds__(
     // its zero row from partition 0.
     if (ctx <= a.dec_part_tokens) slot = kNoSlot;
     if (item_lo >= ctx && item_lo > 0) return;
+  }
+  if constexpr (KSPLIT > 1) {
+    // This wave's share of the item's keys, in whole tiles (item_lo is a
+    // multiple of 256); a wave with none keeps an empty range.
+    const uint32_t hi0 = min(item_hi, ctx);
+    const uint32_t len = hi0 > item_lo ? hi0 - item_lo : 0u;
+    const uint32_t sub = (len + KSPLIT * BN - 1) / (KSPLIT * BN) * BN;
+    const uint32_t lo_w = min(item_lo + kwave * sub, max(hi0, item_lo));
+    item_hi = min(lo_w + sub, max(hi0, item_lo));
+    item_lo = lo_w;
   }
   const uint32_t *table = a.tables + (size_t)b * a.max_blocks;
 
@@ -706,7 +741,7 @@ __global__ void __launch_bounds__(
     uint16_t *vs = reinterpret_cast<uint16_t *>(lb + LD::k_bytes);
     uint8_t *kok = lb + LD::k_bytes + LD::v_bytes;
     if constexpr (LD::NBUF == 1)
-      __syncthreads();  // the previous tile is no longer read
+      region_sync();  // the previous tile is no longer read
 #pragma unroll
     for (int i = 0; i < (DMA ? 0 : CHK); ++i) {
       const int c = tid + NTH * i;
@@ -772,7 +807,7 @@ __global__ void __launch_bounds__(
     // barrier publishes it: s_waitcnt with vmcnt 0, expcnt and lgkmcnt at
     // their maxima, 0x0f70 in this architecture's encoding)
     if constexpr (DMA) __builtin_amdgcn_s_waitcnt(0x0f70);
-    __syncthreads();
+    region_sync();
     if (kt + DEPTH * BN < k_end) {
       load(S, BN_{}, kt + DEPTH * BN);
       fetch_ids(kt + (DEPTH + 1) * BN);
@@ -966,7 +1001,7 @@ __global__ void __launch_bounds__(
     for (uint32_t i = (k_begin >> a.bs_log2) + tid;
          i <= ((k_end - 1u) >> a.bs_log2); i += NTH)
       bad |= table[i] >= a.num_blocks;
-    all_ok = !__syncthreads_or(bad);
+    all_ok = !region_or(bad);
   }
   if constexpr (WAVES == 1) {
     if (newtok != 0xFFFFFFFFu) {
@@ -1011,6 +1046,41 @@ __global__ void __launch_bounds__(
         *reinterpret_cast<u32x4 *>(const_cast<uint16_t *>(a.vc) + dst +
                                    tid * 8) = new_vc;
       }
+    }
+  }
+  if constexpr (KSPLIT > 1) {
+    // Merge the waves' states into wave 0: lane-wise (every wave holds the
+    // same rows in the same layout), weights 2^(m_w - M).
+    constexpr int NV = 2 + DT * 16;  // floats a lane stores
+    static_assert((KSPLIT - 1) * NV * 64 * 4 <= KSPLIT * LD::bytes,
+                  "merge area within the workgroup's LDS");
+    float *xs = reinterpret_cast<float *>(smem_all);
+    __syncthreads();  // every wave is done with its tiles
+    if (kwave > 0) {
+      float *dst = xs + (size_t)(kwave - 1) * NV * 64 + lane;
+      dst[0] = m;
+      dst[64] = l;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) dst[(2 + dt * 16 + j) * 64] = o[dt][j];
+    }
+    __syncthreads();
+    if (kwave > 0) return;
+#pragma unroll
+    for (int w = 1; w < KSPLIT; ++w) {
+      const float *src = xs + (size_t)(w - 1) * NV * 64 + lane;
+      const float mw = src[0], lw = src[64];
+      const float M = fmaxf(m, mw);
+      const float aw = __builtin_amdgcn_exp2f(m - M);
+      const float bw = __builtin_amdgcn_exp2f(mw - M);
+      l = l * aw + lw * bw;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          o[dt][j] = o[dt][j] * aw + src[(2 + dt * 16 + j) * 64] * bw;
+      m = M;
     }
   }
   const float lt = sum_halves(l);
@@ -1201,7 +1271,8 @@ int mfma_decode(const rvkv_pool *pool, uint32_t layer, const float *q,
                 const void *new_v, const uint32_t *new_blk,
                 const uint32_t *new_off, bool new_f32,
                 const uint32_t *groups, uint32_t dec_parts,
-                uint32_t dec_part_tokens, uint32_t dec_ctx_cap) {
+                uint32_t dec_part_tokens, uint32_t dec_ctx_cap,
+                uint32_t ksplit) {
   const char *op = "paged_decode";
   if (n_items == 0) return RVKV_OK;
   PrefillArgs a{};
@@ -1240,8 +1311,15 @@ int mfma_decode(const rvkv_pool *pool, uint32_t layer, const float *q,
   a.new_blk = new_blk;
   a.new_off = new_off;
   a.new_f32 = new_f32;
-  hipLaunchKernelGGL((prefill_kernel<64, 1>), dim3(n_items, pool->n_kv),
-                     dim3(64), (Lds<64, 1>::bytes), pool->stream, a);
+  if (ksplit == 4)
+    hipLaunchKernelGGL((prefill_kernel<64, 1, 4>), dim3(n_items, pool->n_kv),
+                       dim3(256), (4 * Lds<64, 1>::bytes), pool->stream, a);
+  else if (ksplit == 2)
+    hipLaunchKernelGGL((prefill_kernel<64, 1, 2>), dim3(n_items, pool->n_kv),
+                       dim3(128), (2 * Lds<64, 1>::bytes), pool->stream, a);
+  else
+    hipLaunchKernelGGL((prefill_kernel<64, 1>), dim3(n_items, pool->n_kv),
+                       dim3(64), (Lds<64, 1>::bytes), pool->stream, a);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? RVKV_OK : hip_fail(op, e);
 }

@@ -1716,22 +1716,36 @@ uint32_t env_u32(const char *name) {
   return v ? (uint32_t)strtoul(v, nullptr, 10) : 0u;
 }
 
+// The matrix-core decode without a plan: waves a partition (its keys split
+// over them, merged in the workgroup) and partition size. About 2048 waves
+// in all, the chip's two a SIMD: four a partition below 1024 (sequence, KV
+// head) pairs, two below 2048, then as many partitions as that still
+// needs; at most 4096 keys a partition, so one long sequence does not set
+// the launch's tail alone. (Llama-3.2-1B's shape: 64 x 2048 as one
+// partition of four waves 47.4-47.8 us a layer, of two 49.2-49.8, two
+// one-wave partitions and the reduction 50.5-50.8, one wave 62.6; 256 x
+// 4096 one wave a sequence, 326 us.)
+uint32_t mfma_uniform_parts(uint64_t pairs, uint32_t max_ctx,
+                            uint32_t *ksplit) {
+  static const uint32_t forced_k = env_u32("RVKV_DECODE_KSPLIT");
+  *ksplit = forced_k == 1 || forced_k == 2 || forced_k == 4
+                ? forced_k
+                : (pairs >= 2048 ? 1u : pairs >= 1024 ? 2u : 4u);
+  const uint64_t items = pairs * *ksplit;
+  const uint64_t parts = items >= 2048 ? 1 : (2048 + items - 1) / items;
+  const uint64_t per = (max_ctx + parts - 1) / parts;
+  uint32_t P = 256;
+  while (P < per && P < 4096) P <<= 1;
+  return P;
+}
+
 uint32_t partition_tokens(const rvkv_pool *p, uint32_t batch, uint32_t n_heads,
                           uint32_t max_ctx) {
   static const uint32_t forced = env_u32("RVKV_DECODE_PART_TOKENS");
   if (forced >= 256 && forced % 256 == 0) return forced;
   if (rvkv_detail::mfma_decode_wanted(p, n_heads)) {
-    // The matrix-core decode (one wave a partition): enough partitions for
-    // ~1024 waves, and at most 4096 keys a wave, so one long sequence does
-    // not set the launch's tail alone (Llama-3.2-1B's shape: 64 x 2048 at
-    // 1024 keys 49.9 us a layer against 62.6 at 2048; 256 x 4096 at 4096,
-    // no reduction, 326 us against 339 at 2048).
-    const uint64_t pairs = (uint64_t)batch * p->n_kv;
-    const uint64_t parts = pairs >= 1024 ? 1 : (1024 + pairs - 1) / pairs;
-    const uint64_t per = (max_ctx + parts - 1) / parts;
-    uint32_t P = 256;
-    while (P < per && P < 4096) P <<= 1;
-    return P;
+    uint32_t ksplit;
+    return mfma_uniform_parts((uint64_t)batch * p->n_kv, max_ctx, &ksplit);
   }
   uint32_t group = n_heads / (p->n_kv ? p->n_kv : 1);
   uint32_t n_sub, gt;
@@ -2755,11 +2769,15 @@ int paged_decode_ws(const char *op, const rvkv_pool *pool, uint32_t layer,
 // uniform reduction pass when some sequence spans several.
 int uniform_mfma(const char *op, const rvkv_pool *pool, uint32_t layer,
                  const DecodeArgs &a, uint32_t batch, float scale) {
+  uint32_t ksplit = 1;
+  static const uint32_t forced = env_u32("RVKV_DECODE_PART_TOKENS");
+  if (!forced)
+    mfma_uniform_parts((uint64_t)batch * pool->n_kv, a.ctx_cap, &ksplit);
   int rc = rvkv_detail::mfma_decode(
       pool, layer, a.q, a.tables, a.ctx_lens, a.max_blocks, a.n_heads, scale,
       a.window, nullptr, batch * a.n_parts, a.ws_acc, a.ws_ml, a.out,
       a.new_k, a.new_v, a.new_blk, a.new_off, a.new_f32 != 0, nullptr,
-      a.n_parts, a.part_tokens, a.ctx_cap);
+      a.n_parts, a.part_tokens, a.ctx_cap, ksplit);
   if (rc || a.n_parts <= 1) return rc;
   return launch_reduce(op, a, decode_hd(pool->head_dim),
                        dim3(a.n_heads, batch), pool->stream);
