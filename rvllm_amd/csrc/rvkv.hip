@@ -1717,20 +1717,20 @@ uint32_t env_u32(const char *name) {
 }
 
 // The matrix-core decode without a plan: waves a partition (its keys split
-// over them, merged in the workgroup) and partition size. About 2048 waves
-// in all, the chip's two a SIMD: four a partition below 1024 (sequence, KV
-// head) pairs, two below 2048, then as many partitions as that still
-// needs; at most 4096 keys a partition, so one long sequence does not set
-// the launch's tail alone. (Llama-3.2-1B's shape: 64 x 2048 as one
-// partition of four waves 47.4-47.8 us a layer, of two 49.2-49.8, two
-// one-wave partitions and the reduction 50.5-50.8, one wave 62.6; 256 x
-// 4096 one wave a sequence, 326 us.)
+// over them, merged in the workgroup) and partition size. Four waves a
+// partition below 2048 (sequence, KV head) pairs (as for plan items), then
+// as many partitions as it takes for ~2048 waves, the chip's two a SIMD;
+// at most 4096 keys a partition, so one long sequence does not set the
+// launch's tail alone. (Llama-3.2-1B's shape: 64 x 2048 as one partition
+// of four waves 47.4-47.8 us a layer, of two 49.2-49.8, two one-wave
+// partitions and the reduction 50.5-50.8, one wave 62.6; 256 x 4096 one
+// wave a sequence, 326 us.)
 uint32_t mfma_uniform_parts(uint64_t pairs, uint32_t max_ctx,
                             uint32_t *ksplit) {
   static const uint32_t forced_k = env_u32("RVKV_DECODE_KSPLIT");
   *ksplit = forced_k == 1 || forced_k == 2 || forced_k == 4
                 ? forced_k
-                : (pairs >= 2048 ? 1u : pairs >= 1024 ? 2u : 4u);
+                : (pairs >= 2048 ? 1u : 4u);
   const uint64_t items = pairs * *ksplit;
   const uint64_t parts = items >= 2048 ? 1 : (2048 + items - 1) / items;
   const uint64_t per = (max_ctx + parts - 1) / parts;
@@ -2300,6 +2300,17 @@ struct rvkv_decode_plan {
 
 namespace {
 
+// Waves a plan item on the matrix cores (its keys split over them, merged
+// in the workgroup): four while the launch has under 2048 workgroups, one
+// from 2048 on (Qwen2.5 ragged, ~1500 workgroups: 74.7 -> 70.8 us a layer;
+// Llama-3.2-1B 64 x 2048, 512: 50.9 -> 48.1 us; 256 x 4096, 2048: one wave
+// 327 us, four 335). RVKV_DECODE_PLAN_KSPLIT=1|2|4 overrides.
+uint32_t planned_ksplit(const rvkv_decode_plan *plan) {
+  static const uint32_t k = env_u32("RVKV_DECODE_PLAN_KSPLIT");
+  if (k == 1 || k == 2 || k == 4) return k;
+  return (uint64_t)plan->n_items * plan->n_kv >= 2048 ? 1u : 4u;
+}
+
 // A planned decode on the matrix cores (large GQA groups): the plan's work
 // items through the prefill kernel in decode mode, which writes the output
 // of whole-context items and the partials of split ones; then the same
@@ -2312,7 +2323,8 @@ int planned_mfma(const char *op, const rvkv_pool *pool,
       scale, plan->window, a.items, plan->n_items, a.ws_acc, a.ws_ml, a.out,
       a.new_k, a.new_v, a.new_blk, a.new_off, a.new_f32,
       reinterpret_cast<const uint32_t *>(plan->d_buf + plan->n_items +
-                                         plan->n_reds));
+                                         plan->n_reds),
+      0, 0, 0xFFFFFFFFu, planned_ksplit(plan));
   if (rc || plan->n_reds == 0) return rc;
   return launch_reduce(op, a, decode_hd(pool->head_dim),
                        dim3(plan->n_heads, plan->n_reds),
@@ -2343,16 +2355,12 @@ int plan_build(rvkv_decode_plan *pl, const uint32_t *ctx_lens_host,
   }
   // Tokens per work item: about one sequence, but at least enough that the
   // grid has <= ~1024 workgroups and at most what keeps >= ~256 of them.
-  // The matrix-core decode runs one wave per item (the VALU decode four),
-  // so it gets items a quarter as long and four times as many at GQA
-  // groups of five and more, half as long at four (Llama-3.2-1B's shape:
-  // 49.9 us a layer at 64 x 2048 against 62.6 with whole sequences; the
-  // quarter measured best for Qwen2.5's group of seven).
+  // (The matrix-core decode splits an item's keys over four waves when
+  // the launch has under 2048 workgroups, see planned_ksplit; with one
+  // wave an item, items a quarter as long measured best for Qwen2.5.)
   const bool mfma = rvkv_detail::mfma_decode_wanted(pool, pl->n_heads);
   static const uint32_t forced_div = env_u32("RVKV_DECODE_PLAN_DIV");
-  const double per =
-      forced_div ? (double)forced_div
-                 : (mfma ? (pl->n_heads / pool->n_kv >= 5 ? 4.0 : 2.0) : 1.0);
+  const double per = forced_div ? (double)forced_div : 1.0;
   const double avg = (double)total / batch / per;
   const double lo_p = (double)total * n_hy / (1024.0 * per);
   const double hi_p = (double)total * n_hy / (256.0 * per);
