@@ -1724,10 +1724,12 @@ uint32_t env_u32(const char *name) {
 // launch's tail alone. (Llama-3.2-1B's shape: 64 x 2048 as one partition
 // of four waves 47.4-47.8 us a layer, of two 49.2-49.8, two one-wave
 // partitions and the reduction 50.5-50.8, one wave 62.6; 256 x 4096 one
-// wave a sequence, 326 us.)
+// wave a sequence, 326 us.) RVKV_DECODE_KSPLIT=1|2|4 overrides; it is read
+// at every call, so a test can take each width (each call sizes and checks
+// its workspace against the same reading).
 uint32_t mfma_uniform_parts(uint64_t pairs, uint32_t max_ctx,
                             uint32_t *ksplit) {
-  static const uint32_t forced_k = env_u32("RVKV_DECODE_KSPLIT");
+  const uint32_t forced_k = env_u32("RVKV_DECODE_KSPLIT");
   *ksplit = forced_k == 1 || forced_k == 2 || forced_k == 4
                 ? forced_k
                 : (pairs >= 2048 ? 1u : 4u);
@@ -2304,9 +2306,10 @@ namespace {
 // in the workgroup): four while the launch has under 2048 workgroups, one
 // from 2048 on (Qwen2.5 ragged, ~1500 workgroups: 74.7 -> 70.8 us a layer;
 // Llama-3.2-1B 64 x 2048, 512: 50.9 -> 48.1 us; 256 x 4096, 2048: one wave
-// 327 us, four 335). RVKV_DECODE_PLAN_KSPLIT=1|2|4 overrides.
+// 327 us, four 335). RVKV_DECODE_PLAN_KSPLIT=1|2|4 overrides; it is read at
+// every launch (the split needs no workspace), so a test can take each width.
 uint32_t planned_ksplit(const rvkv_decode_plan *plan) {
-  static const uint32_t k = env_u32("RVKV_DECODE_PLAN_KSPLIT");
+  const uint32_t k = env_u32("RVKV_DECODE_PLAN_KSPLIT");
   if (k == 1 || k == 2 || k == 4) return k;
   return (uint64_t)plan->n_items * plan->n_kv >= 2048 ? 1u : 4u;
 }

@@ -1134,6 +1134,60 @@ def test_decode_step_short_items(planned, G, hd):
     assert _decode_vs_oracle(a, 0, db, q) < ATOL
 
 
+@pytest.mark.parametrize("ksplit", [1, 2, 4])
+@pytest.mark.parametrize("planned", [False, True])
+@pytest.mark.parametrize("G,bs,window", [(4, 16, 0), (7, 128, 0),
+                                         (8, 16, 300), (7, 32, 5000)])
+def test_decode_step_key_split_widths(monkeypatch, ksplit, planned, G, bs,
+                                      window):
+    """The matrix-core decode (head_dim 64, G >= 4) splits an item's keys
+    over 1, 2 or 4 waves of its workgroup and merges them in LDS; the
+    launch picks 4 or 1 by grid size, so each width is forced here
+    (RVKV_DECODE_KSPLIT / RVKV_DECODE_PLAN_KSPLIT, read at every launch).
+    Contexts from 1 key (three waves with nothing to read) to 9000 (several
+    partitions and the reduction without a plan, split items with one): the
+    fused step leaves append-then-decode's cache bits, its output agrees with
+    every other width to summation order and with the oracle."""
+    from rvllm_amd.kv_storage import HipDecodePlan
+    nkv, hd = 2, 64
+    lens = np.array([9000, 1, 2, 33, 64, 65, 700, 2049, 4097, 129],
+                    np.uint32)
+    cfg = W.Config("ks", 9, 1, nkv * G, nkv, hd, bs, len(lens))
+    db = W.ragged_batch(cfg, lens, seed=G * bs)
+    g = torch.Generator("cuda").manual_seed(3)
+    nk = torch.randn(len(lens), nkv, hd, device="cuda", generator=g)
+    nv = torch.randn(len(lens), nkv, hd, device="cuda", generator=g)
+    q = torch.randn(len(lens), nkv * G, hd, device="cuda", generator=g)
+    sb, so = dev_u32(db.slot_block), dev_u32(db.slot_off)
+    tables, ctx = dev_u32(db.padded_tables()), dev_u32(lens)
+    max_ctx = int(lens.max())
+
+    def run(width):
+        monkeypatch.setenv("RVKV_DECODE_KSPLIT", str(width))
+        monkeypatch.setenv("RVKV_DECODE_PLAN_KSPLIT", str(width))
+        st = HipKvStorage(1, db.num_blocks, bs, nkv, hd)
+        fill_layer(st, 0, seed=17)
+        if planned:
+            plan = HipDecodePlan(st, lens, nkv * G, window=window)
+            out = st.decode_step(0, nk, nv, sb, so, q, tables, ctx, plan=plan)
+        else:
+            out = st.decode_step(0, nk, nv, sb, so, q, tables, ctx, max_ctx,
+                                 window=window)
+        torch.cuda.synchronize()
+        return st, out
+
+    st, out = run(ksplit)
+    ref_st, ref = run(1 if ksplit != 1 else 4)
+    ids = dev_u32(np.arange(db.num_blocks))
+    for which in (0, 1):
+        assert torch.equal(st.read_blocks(0, which, ids),
+                           ref_st.read_blocks(0, which, ids))
+    assert torch.isfinite(out).all()
+    assert (out - ref).abs().max().item() < 5e-4
+    db.ctx_lens = lens
+    assert _decode_vs_oracle(st, 0, db, q, window=window) < ATOL
+
+
 # ---- continuous-batching churn through the block manager -------------------
 def test_churn_driver_parity():
     """A few churn steps (finish 10%, admit 64-token prompts, decode all)
