@@ -2383,9 +2383,11 @@ int plan_build(rvkv_decode_plan *pl, const uint32_t *ctx_lens_host,
   uint32_t P = gran == 256 ? 256 : 128;
   while (P < want && P < (1u << 30)) P <<= 1;
 
-  // Items of at most P tokens over [start, n), with 1/8 slack so a range
-  // just past a multiple of P does not get a sliver item; split evenly on
-  // gran-token boundaries. Returns the count and the step.
+  // Items of at most P tokens over [start, n), with 1/8 slack (1/2 on the
+  // matrix-core decode) so a range just past a multiple of P does not get a
+  // sliver item; split evenly on gran-token boundaries. Returns the count and
+  // the step. (Qwen2.5 ragged, P = 2048: slack 1/2 69.2-69.6 us a layer
+  // against 69.5-71.4 at 1/8, 73.0-73.4 at 3/4 and 73.5-73.6 at 1.)
   // VALU decode: a sequence up to four times the average length (and up to
   // 2P, within the >= ~256-workgroup bound) stays one item. Splitting it
   // costs the reduction launch, and a moderately long item that starts
@@ -2402,7 +2404,7 @@ int plan_build(rvkv_decode_plan *pl, const uint32_t *ctx_lens_host,
       *step_out = span;
       return 1u;
     }
-    uint32_t k = div_up(span, P + P / 8);
+    uint32_t k = div_up(span, P + (mfma ? P / 2 : P / 8));
     const uint32_t step = (div_up(span, k) + gran - 1) / gran * gran;
     *step_out = step;
     return div_up(span, step);
