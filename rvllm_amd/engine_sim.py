@@ -78,13 +78,26 @@ class ChurnDriver:
         self._out_p = [P(t.data_ptr()) for t in self.out]
         # Pinned staging + device copies of the step arrays, NSTAGE sets used
         # in turn, so the host can prepare a few steps ahead of the device.
+        # Each set is one buffer (arrays at 256-byte offsets), moved by one
+        # copy a step: six copies a step left ~5 us of dispatch gap each.
         mb = self.max_blocks
         shapes = {"tables": (batch, mb), "ctx": (batch,), "sb": (batch,),
                   "so": (batch,), "pb": (n_prompt,), "po": (n_prompt,)}
-        self.host = [{k: torch.empty(s, dtype=torch.int32, pin_memory=True)
-                      for k, s in shapes.items()} for _ in range(NSTAGE)]
-        self.devb = [{k: torch.empty(s, dtype=torch.int32, device=dev)
-                      for k, s in shapes.items()} for _ in range(NSTAGE)]
+        offs, n = {}, 0
+        for k, s in shapes.items():
+            offs[k] = n
+            n += -(-int(np.prod(s)) // 64) * 64
+        self.host_flat = [torch.empty(n, dtype=torch.int32, pin_memory=True)
+                          for _ in range(NSTAGE)]
+        self.dev_flat = [torch.empty(n, dtype=torch.int32, device=dev)
+                         for _ in range(NSTAGE)]
+
+        def views(flat):
+            return {k: flat[offs[k]:offs[k] + int(np.prod(s))].view(s)
+                    for k, s in shapes.items()}
+
+        self.host = [views(f) for f in self.host_flat]
+        self.devb = [views(f) for f in self.dev_flat]
         self.copied = [torch.cuda.Event() for _ in range(NSTAGE)]
         self.plan = None
         self.step_index = 0
@@ -137,8 +150,7 @@ class ChurnDriver:
                        lens_out=lens)
         hb["sb"].numpy().view(np.uint32)[:] = blocks
         hb["so"].numpy().view(np.uint32)[:] = offs
-        for k in hb:
-            db[k].copy_(hb[k], non_blocking=True)
+        self.dev_flat[i].copy_(self.host_flat[i], non_blocking=True)
         self.copied[i].record()
         if len(cs):
             st.copy_blocks(torch.from_numpy(cs.view(np.int32)).cuda(),
