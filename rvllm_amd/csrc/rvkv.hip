@@ -882,9 +882,20 @@ __global__ void __launch_bounds__(256) decode_part_kernel(
     tend = t0 + p_pt;
     slot = a.n_parts > 1 ? b * a.n_parts + blockIdx.x : kNoSlot;
     // Workgroups go to the XCDs round robin by linear id, and with one
-    // partition the id is hy + gridDim.y * b: rotate hy by the sequence so
-    // each XCD serves every head, not one fixed head's tiles of each block.
-    hy = (hy + b) % gridDim.y;
+    // partition the id is hy + gridDim.y * b. With a batch of whole eights,
+    // renumber so a sequence's heads are consecutive workgroups of one XCD:
+    // its L2 then asks for all the heads' tiles of each block back to back
+    // (Qwen3-0.6B 256 x 4096: 647.2 -> 642.6 us a layer, three alternating
+    // runs each). Otherwise rotate hy by the sequence, so each XCD serves
+    // every head, not one fixed head's tiles of each block.
+    if (gridDim.x == 1 && gridDim.z % 8 == 0) {
+      const uint32_t L = blockIdx.y + gridDim.y * blockIdx.z;
+      const uint32_t xcd = L % 8, idx = L / 8;
+      b = (idx / gridDim.y) * 8 + xcd;
+      hy = idx % gridDim.y;
+    } else {
+      hy = (hy + b) % gridDim.y;
+    }
   }
   const uint32_t kvh = hy / a.n_sub;
   const uint32_t sub = hy - kvh * a.n_sub;

@@ -1188,6 +1188,44 @@ def test_decode_step_key_split_widths(monkeypatch, ksplit, planned, G, bs,
     assert _decode_vs_oracle(st, 0, db, q, window=window) < ATOL
 
 
+@pytest.mark.parametrize("batch", [16, 24, 12])
+@pytest.mark.parametrize("G,hd", [(2, 128), (4, 64)])
+def test_decode_xcd_sequence_order(batch, G, hd):
+    """One partition per sequence (contexts <= 256) and a batch of whole
+    eights: the uniform decode (VALU at G 2, matrix cores at G 4, hd 64)
+    renumbers its workgroups so a sequence's KV heads run back to back on
+    one XCD; batch 12 keeps the head rotation. Every (sequence, head) is
+    computed once and lands in its own output row: all rows against the
+    oracle, fused step and append-then-decode alike."""
+    nkv, bs = 4, 16
+    rng = np.random.default_rng(batch * 10 + G)
+    lens = rng.integers(1, 257, batch).astype(np.uint32)
+    lens[0] = 256
+    cfg = W.Config("xcd", 9, 1, nkv * G, nkv, hd, bs, batch)
+    db = W.ragged_batch(cfg, lens, seed=batch + G)
+    stores = [HipKvStorage(1, db.num_blocks, bs, nkv, hd) for _ in range(2)]
+    for st in stores:
+        fill_layer(st, 0, seed=9)
+    assert stores[0].decode_workspace_bytes(batch, nkv * G, 256) == 0
+    g = torch.Generator("cuda").manual_seed(batch)
+    nk = torch.randn(batch, nkv, hd, device="cuda", generator=g)
+    nv = torch.randn(batch, nkv, hd, device="cuda", generator=g)
+    q = torch.randn(batch, nkv * G, hd, device="cuda", generator=g)
+    sb, so = dev_u32(db.slot_block), dev_u32(db.slot_off)
+    tables, ctx = dev_u32(db.padded_tables()), dev_u32(lens)
+    a, b = stores
+    out_a = a.decode_step(0, nk, nv, sb, so, q, tables, ctx, int(lens.max()))
+    b.write_tokens(0, sb, so, nk, nv)
+    out_b = b.paged_decode(0, q, tables, ctx, int(lens.max()))
+    ids = dev_u32(np.arange(db.num_blocks))
+    for which in (0, 1):
+        assert torch.equal(a.read_blocks(0, which, ids),
+                           b.read_blocks(0, which, ids))
+    assert (out_a - out_b).abs().max().item() < 5e-4
+    db.ctx_lens = lens
+    assert _decode_vs_oracle(b, 0, db, q) < ATOL
+
+
 # ---- continuous-batching churn through the block manager -------------------
 def test_churn_driver_parity():
     """A few churn steps (finish 10%, admit 64-token prompts, decode all)
