@@ -1837,14 +1837,17 @@ void launch_decode(const DecodeArgs &a, dim3 grid, hipStream_t st) {
   uint32_t W = decode_waves(wgs, a.max_tokens, GT);
   // Eight loads per chunk pay off for 512-byte rows, for large groups in
   // single-wave workgroups, and for long items when every wave of the
-  // launch fits at two per SIMD (<= 2048 waves; Llama 64 x 2048: 63.0 ->
-  // 64.8 % of 8 TB/s); two for short items with groups of up to four
-  // (with four waves a workgroup, above); otherwise four keep more waves
-  // resident.
+  // launch fits at two per SIMD in workgroups of several waves (<= 2048
+  // waves; Llama 64 x 2048 on this kernel: 63.0 -> 64.8 % of 8 TB/s); two
+  // for short items with groups of up to four (with four waves a
+  // workgroup, above); otherwise four keep more waves resident (Qwen3-0.6B
+  // 256 x 4096, 2048 one-wave workgroups: 640.1 us a layer at four, 642.0
+  // at eight).
   const bool u8 =
       forced_u ? forced_u == 8
                : ((HD >= 256 && a.avg_tokens >= 512) || (GT >= 5 && W == 1) ||
-                  (GT <= 4 && a.avg_tokens >= 512 && wgs * W <= 2048));
+                  (GT <= 4 && a.avg_tokens >= 512 && W > 1 &&
+                   wgs * W <= 2048));
   const bool u2 = forced_u ? forced_u == 2
                            : GT <= 4 && short_items(wgs, a.max_tokens);
   // Eight-load kernels hold two waves a SIMD (2048 on the chip): with
