@@ -1188,15 +1188,17 @@ def test_decode_step_key_split_widths(monkeypatch, ksplit, planned, G, bs,
     assert _decode_vs_oracle(st, 0, db, q, window=window) < ATOL
 
 
+@pytest.mark.parametrize("window", [0, 100])
 @pytest.mark.parametrize("batch", [16, 24, 12])
 @pytest.mark.parametrize("G,hd", [(2, 128), (4, 64)])
-def test_decode_xcd_sequence_order(batch, G, hd):
+def test_decode_xcd_sequence_order(batch, G, hd, window):
     """One partition per sequence (contexts <= 256) and a batch of whole
     eights: the uniform decode (VALU at G 2, matrix cores at G 4, hd 64)
     renumbers its workgroups so a sequence's KV heads run back to back on
     one XCD; batch 12 keeps the head rotation. Every (sequence, head) is
     computed once and lands in its own output row: all rows against the
-    oracle, fused step and append-then-decode alike."""
+    oracle, fused step and append-then-decode alike, with and without a
+    sliding window."""
     nkv, bs = 4, 16
     rng = np.random.default_rng(batch * 10 + G)
     lens = rng.integers(1, 257, batch).astype(np.uint32)
@@ -1214,16 +1216,17 @@ def test_decode_xcd_sequence_order(batch, G, hd):
     sb, so = dev_u32(db.slot_block), dev_u32(db.slot_off)
     tables, ctx = dev_u32(db.padded_tables()), dev_u32(lens)
     a, b = stores
-    out_a = a.decode_step(0, nk, nv, sb, so, q, tables, ctx, int(lens.max()))
+    out_a = a.decode_step(0, nk, nv, sb, so, q, tables, ctx, int(lens.max()),
+                          window=window)
     b.write_tokens(0, sb, so, nk, nv)
-    out_b = b.paged_decode(0, q, tables, ctx, int(lens.max()))
+    out_b = b.paged_decode(0, q, tables, ctx, int(lens.max()), window=window)
     ids = dev_u32(np.arange(db.num_blocks))
     for which in (0, 1):
         assert torch.equal(a.read_blocks(0, which, ids),
                            b.read_blocks(0, which, ids))
     assert (out_a - out_b).abs().max().item() < 5e-4
     db.ctx_lens = lens
-    assert _decode_vs_oracle(b, 0, db, q) < ATOL
+    assert _decode_vs_oracle(b, 0, db, q, window=window) < ATOL
 
 
 # ---- continuous-batching churn through the block manager -------------------
